@@ -1,0 +1,101 @@
+"""Pins the decode half of the oracle bit for bit against the reference decode host library
+compiled from the reference's own sources (oracle/_ref, built by `make -C oracle ref`).
+
+Every decode entry point is compared on dense random layers (several KV lengths, non-unit norm
+weights), on the reference KAT layers, and on the error paths.  Skipped only when the reference
+library is absent (it is built wherever the reference tree is mounted and travels with the tree).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from _cases import (SRAM, bits_equal, decode_attention, decode_layer, decode_mlp, empty_layer, first_mismatch,
+                    quantized_kv_history, random_hidden, random_layer)
+from _oracle import oracle, ref_decode
+from work_llm_accelerator_amd.layout import HIDDEN, KV_WIDTH, LAYOUT
+
+REF = ref_decode()
+pytestmark = pytest.mark.skipif(REF is None, reason="oracle/_ref/libqwen_decode_ref.so not built")
+
+
+@pytest.fixture(scope="module")
+def layer():
+    return random_layer(seed=11)
+
+
+@pytest.mark.parametrize("past", [0, 1, 5, 64, 300])
+def test_decode_layer_bitexact(layer, past):
+    o = oracle()
+    x = random_hidden(100 + past, 1)
+    k_hist, v_hist = quantized_kv_history(200 + past, past + 1)
+    kc_o, vc_o, kc_r, vc_r = k_hist.copy(), v_hist.copy(), k_hist.copy(), v_hist.copy()
+    st_o, out_o = decode_layer(o.oracle_decode_layer_smoke_forward, layer, x, past, kc_o, vc_o)
+    st_r, out_r = decode_layer(REF.qwen_decode_layer_smoke_forward, layer, x, past, kc_r, vc_r)
+    assert st_o == st_r == 0
+    assert bits_equal(out_o, out_r), first_mismatch(out_o, out_r)
+    assert bits_equal(kc_o, kc_r) and bits_equal(vc_o, vc_r)
+
+
+def test_decode_attention_and_mlp_bitexact(layer):
+    o = oracle()
+    x = random_hidden(7, 1, scale=3.0)
+    kc, vc = quantized_kv_history(8, 10)
+    args = (layer, x, 9)
+    st_o, a_o = decode_attention(o.oracle_decode_attention_smoke_forward, *args, kc.copy(), vc.copy())
+    st_r, a_r = decode_attention(REF.qwen_decode_attention_smoke_forward, *args, kc.copy(), vc.copy())
+    assert st_o == st_r == 0 and bits_equal(a_o, a_r), first_mismatch(a_o, a_r)
+    st_o, m_o = decode_mlp(o.oracle_decode_mlp_smoke_forward, layer, a_o)
+    st_r, m_r = decode_mlp(REF.qwen_decode_mlp_smoke_forward, layer, a_r)
+    assert st_o == st_r == 0 and bits_equal(m_o, m_r), first_mismatch(m_o, m_r)
+
+
+def test_decode_top_bitexact_offsets(layer):
+    """Top wrapper with non-zero activation / weight / scale / KV base addresses."""
+    o = oracle()
+    past = 3
+    w_base, s_base = 4096, 8192  # bytes; weight and scale images shifted inside larger buffers
+    wd = np.zeros(LAYOUT.total_parameter_bytes + w_base, np.uint8)
+    wd[w_base:] = layer.weight_ddr
+    sd = np.zeros(layer.scale_ddr.size + s_base // 4, np.float32)
+    sd[s_base // 4:] = layer.scale_ddr
+    act = np.zeros(HIDDEN * 4, np.float32)
+    act[HIDDEN:2 * HIDDEN] = random_hidden(3, 1)
+    k_hist, v_hist = quantized_kv_history(4, past + 1)
+    kv = np.zeros(KV_WIDTH * 16, np.float32)
+    k_base, v_base = KV_WIDTH * 4 * 2, KV_WIDTH * 4 * 9
+    kv[k_base // 4:k_base // 4 + k_hist.size] = k_hist
+    kv[v_base // 4:v_base // 4 + v_hist.size] = v_hist
+    res = []
+    for fn in (o.oracle_decode_top_smoke_forward, REF.qwen_decode_top_smoke_forward):
+        a, k = act.copy(), kv.copy()
+        st = fn(5, past, HIDDEN * 4, HIDDEN * 4 * 3, w_base, s_base, k_base, v_base, wd, sd, k, a, *SRAM())
+        res.append((st, a, k))
+    assert res[0][0] == res[1][0] == 0
+    assert bits_equal(res[0][1], res[1][1]), first_mismatch(res[0][1], res[1][1])
+    assert bits_equal(res[0][2], res[1][2])
+
+
+@pytest.mark.parametrize("layer_id,past,code", [(-1, 0, 10), (28, 0, 10), (0, -1, 10)])
+def test_decode_top_descriptor_errors(layer_id, past, code):
+    o = oracle()
+    case = empty_layer()
+    for fn in (o.oracle_decode_top_smoke_forward, REF.qwen_decode_top_smoke_forward):
+        act = np.zeros(2 * HIDDEN, np.float32)
+        kv = np.zeros(2 * KV_WIDTH, np.float32)
+        st = fn(layer_id, past, 0, HIDDEN * 4, 0, 0, 0, KV_WIDTH * 4, case.weight_ddr, case.scale_ddr, kv, act,
+                *SRAM())
+        assert st == code
+
+
+def test_decode_stub_bitexact():
+    o = oracle()
+    x = random_hidden(5, 1)
+    out_o = np.ones(HIDDEN, np.float32)
+    out_r = np.ones(HIDDEN, np.float32)
+    assert o.oracle_decode_stub_forward(x, 4, out_o) == 0
+    assert REF.qwen_decode_stub_forward(x, 4, out_r) == 0
+    assert bits_equal(out_o, out_r)
+    assert not np.any(out_o)
+    assert o.oracle_decode_stub_forward(x, -1, out_o) == REF.qwen_decode_stub_forward(x, -1, out_r) == 1

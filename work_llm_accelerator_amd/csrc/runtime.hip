@@ -1,0 +1,227 @@
+// Host runtime: arena, RoPE tables, layer staging and the per-layer executors.
+#include "runtime.hpp"
+
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <stdexcept>
+#include <string>
+
+#include "kernels.hpp"
+
+namespace qwen {
+
+Mode mode_from_env() {
+  const char* m = std::getenv("QWEN_HIP_MODE");
+  if (m && (std::strcmp(m, "fast") == 0 || std::strcmp(m, "FAST") == 0)) return Mode::Fast;
+  return Mode::Ordered;
+}
+
+void hip_check(hipError_t e, const char* what) {
+  if (e != hipSuccess) throw HipError{e, what};
+}
+
+HostLayer resolve_host_layer(const uint8_t* wd, const float* sd, uint64_t wb, uint64_t sb) {
+  HostLayer p;
+  p.ln = sd + (sb + QWEN_OFF_INPUT_LN) / 4;
+  p.post_ln = sd + (sb + QWEN_OFF_POST_LN) / 4;
+  p.qw = wd + wb + QWEN_OFF_Q_W;
+  p.kw = wd + wb + QWEN_OFF_K_W;
+  p.vw = wd + wb + QWEN_OFF_V_W;
+  p.ow = wd + wb + QWEN_OFF_O_W;
+  p.qb = sd + (sb + QWEN_OFF_Q_B) / 4;
+  p.kb = sd + (sb + QWEN_OFF_K_B) / 4;
+  p.vb = sd + (sb + QWEN_OFF_V_B) / 4;
+  p.qs = sd + (sb + QWEN_OFF_Q_S) / 4;
+  p.ks = sd + (sb + QWEN_OFF_K_S) / 4;
+  p.vs = sd + (sb + QWEN_OFF_V_S) / 4;
+  p.os = sd + (sb + QWEN_OFF_O_S) / 4;
+  p.gs = sd + (sb + QWEN_OFF_GATE_S) / 4;
+  p.us = sd + (sb + QWEN_OFF_UP_S) / 4;
+  p.ds = sd + (sb + QWEN_OFF_DOWN_S) / 4;
+  p.gw = wd + wb + QWEN_OFF_GATE_W;
+  p.uw = wd + wb + QWEN_OFF_UP_W;
+  p.dw = wd + wb + QWEN_OFF_DOWN_W;
+  return p;
+}
+
+// ---------------------------------------------------------------------------------------------
+Arena::~Arena() {
+  // Process teardown: the HIP runtime may already be gone; leave the block to the driver.
+}
+
+void Arena::reserve(size_t bytes) {
+  if (bytes <= cap_) return;
+  if (used_ != 0) throw std::runtime_error("arena grown while in use");
+  if (base_) {
+    QWEN_HIP(hipDeviceSynchronize());
+    QWEN_HIP(hipFree(base_));
+    base_ = nullptr;
+    cap_ = 0;
+  }
+  const size_t want = bytes + (bytes >> 3) + (1u << 20);
+  QWEN_HIP(hipMalloc(reinterpret_cast<void**>(&base_), want));
+  cap_ = want;
+}
+
+void* Arena::alloc(size_t bytes) {
+  const size_t off = (used_ + 255u) & ~size_t(255u);
+  if (off + bytes > cap_) throw std::runtime_error("arena capacity exceeded");
+  used_ = off + bytes;
+  return base_ + off;
+}
+
+// ---------------------------------------------------------------------------------------------
+Runtime& Runtime::get() {
+  static Runtime* rt = new Runtime();  // never destroyed: HIP objects outlive static teardown
+  return *rt;
+}
+
+Runtime::Runtime() {
+  // Default-priority stream (no priority other than the default is ever used).
+  QWEN_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
+}
+
+void decode_rope_row_host(int position, float* out) {
+  // qwen_decode_attention_kernel.cpp:29-42: angle in double with libm pow, cos, sin.
+  for (int p = 0; p < QWEN_HEAD_DIM / 2; ++p) {
+    const double angle = static_cast<double>(position) *
+                         std::pow(static_cast<double>(QWEN_ROPE_THETA),
+                                  -2.0 * static_cast<double>(p) / static_cast<double>(QWEN_HEAD_DIM));
+    out[p] = static_cast<float>(std::cos(angle));
+    out[64 + p] = static_cast<float>(std::sin(angle));
+  }
+}
+
+const float* Runtime::prefill_rope(int positions) {
+  if (positions <= prefill_rope_rows_) return prefill_rope_;
+  int rows = 256;
+  while (rows < positions) rows *= 2;
+  if (rows > QWEN_MAX_SEQ) rows = QWEN_MAX_SEQ;
+  float* fresh = nullptr;
+  QWEN_HIP(hipMalloc(reinterpret_cast<void**>(&fresh), sizeof(float) * 128u * (size_t)rows));
+  launch_rope_table_prefill(fresh, 0, rows, stream);
+  QWEN_HIP(hipGetLastError());
+  QWEN_HIP(hipStreamSynchronize(stream));
+  if (prefill_rope_) QWEN_HIP(hipFree(prefill_rope_));
+  prefill_rope_ = fresh;
+  prefill_rope_rows_ = rows;
+  return prefill_rope_;
+}
+
+const float* Runtime::decode_rope(int positions) {
+  if (positions <= decode_rope_rows_) return decode_rope_;
+  int rows = 256;
+  while (rows < positions) rows *= 2;
+  if (rows > QWEN_MAX_SEQ) rows = QWEN_MAX_SEQ;
+  std::vector<float> host((size_t)rows * 128u);
+  for (int r = 0; r < rows; ++r) decode_rope_row_host(r, &host[(size_t)r * 128u]);
+  float* fresh = nullptr;
+  QWEN_HIP(hipMalloc(reinterpret_cast<void**>(&fresh), sizeof(float) * host.size()));
+  QWEN_HIP(hipMemcpy(fresh, host.data(), sizeof(float) * host.size(), hipMemcpyHostToDevice));
+  if (decode_rope_) QWEN_HIP(hipFree(decode_rope_));
+  decode_rope_ = fresh;
+  decode_rope_rows_ = rows;
+  return decode_rope_;
+}
+
+// ---------------------------------------------------------------------------------------------
+size_t staged_layer_bytes() { return QWEN_LAYER_BYTES + 64u * 256u; }
+
+DevLayer stage_layer(Arena& a, const HostLayer& h, hipStream_t st) {
+  DevLayer d;
+  d.qw = stage_in(a, h.qw, QWEN_Q_WEIGHT_BYTES, st);
+  d.kw = stage_in(a, h.kw, QWEN_K_WEIGHT_BYTES, st);
+  d.vw = stage_in(a, h.vw, QWEN_V_WEIGHT_BYTES, st);
+  d.ow = stage_in(a, h.ow, QWEN_O_WEIGHT_BYTES, st);
+  d.gw = stage_in(a, h.gw, QWEN_GATE_WEIGHT_BYTES, st);
+  d.uw = stage_in(a, h.uw, QWEN_UP_WEIGHT_BYTES, st);
+  d.dw = stage_in(a, h.dw, QWEN_DOWN_WEIGHT_BYTES, st);
+  d.ln = stage_in(a, h.ln, QWEN_HIDDEN, st);
+  d.post_ln = stage_in(a, h.post_ln, QWEN_HIDDEN, st);
+  d.qb = stage_in(a, h.qb, QWEN_HIDDEN, st);
+  d.kb = stage_in(a, h.kb, QWEN_KV_WIDTH, st);
+  d.vb = stage_in(a, h.vb, QWEN_KV_WIDTH, st);
+  d.qs = stage_in(a, h.qs, QWEN_HIDDEN, st);
+  d.ks = stage_in(a, h.ks, QWEN_KV_WIDTH, st);
+  d.vs = stage_in(a, h.vs, QWEN_KV_WIDTH, st);
+  d.os = stage_in(a, h.os, QWEN_HIDDEN, st);
+  d.gs = stage_in(a, h.gs, QWEN_INTERMEDIATE, st);
+  d.us = stage_in(a, h.us, QWEN_INTERMEDIATE, st);
+  d.ds = stage_in(a, h.ds, QWEN_HIDDEN, st);
+  return d;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Executors.  Intermediates come from the arena; sizes in floats per token:
+//   xn 1536, q 1536, k 256, v 256, ctx 1536 (attention);  pn 1536, g/u/s 3*8960 (MLP).
+size_t decode_workspace_bytes(int tokens) {
+  return (size_t)tokens * sizeof(float) * (5u * QWEN_HIDDEN + 2u * QWEN_KV_WIDTH + 3u * QWEN_INTERMEDIATE) +
+         16u * 256u;
+}
+size_t prefill_workspace_bytes(int tokens) { return decode_workspace_bytes(tokens); }
+
+void run_decode_attention(const DevLayer& L, const float* x, const DecodeBatch& b, float* att, Arena& a, Mode m,
+                          hipStream_t st) {
+  (void)m;
+  const int T = b.tokens;
+  float* xn = a.alloc_n<float>((size_t)T * QWEN_HIDDEN);
+  float* q = a.alloc_n<float>((size_t)T * QWEN_HIDDEN);
+  float* k = a.alloc_n<float>((size_t)T * QWEN_KV_WIDTH);
+  float* v = a.alloc_n<float>((size_t)T * QWEN_KV_WIDTH);
+  float* ctx = a.alloc_n<float>((size_t)T * QWEN_HIDDEN);
+  launch_rmsnorm_ordered(x, L.ln, xn, T, false, st);
+  launch_project_ordered(xn, T, QWEN_HIDDEN, L.qw, L.qs, L.qb, QWEN_HIDDEN, q, nullptr, st);
+  launch_project_ordered(xn, T, QWEN_HIDDEN, L.kw, L.ks, L.kb, QWEN_KV_WIDTH, k, nullptr, st);
+  launch_project_ordered(xn, T, QWEN_HIDDEN, L.vw, L.vs, L.vb, QWEN_KV_WIDTH, v, nullptr, st);
+  launch_rope_append_decode(q, k, v, b.pos, b.rope, b.rope_per_token, b.k_cache, b.v_cache, b.cache_stride, T, st);
+  launch_attention_ordered(q, b.k_cache, b.v_cache, b.cache_stride, b.pos, T, false, ctx, st);
+  launch_project_ordered(ctx, T, QWEN_HIDDEN, L.ow, L.os, nullptr, QWEN_HIDDEN, att, nullptr, st);
+  QWEN_HIP(hipGetLastError());
+}
+
+void run_decode_mlp(const DevLayer& L, const float* att, int T, float* out, Arena& a, Mode m, hipStream_t st) {
+  (void)m;
+  float* pn = a.alloc_n<float>((size_t)T * QWEN_HIDDEN);
+  float* g = a.alloc_n<float>((size_t)T * QWEN_INTERMEDIATE);
+  float* u = a.alloc_n<float>((size_t)T * QWEN_INTERMEDIATE);
+  float* s = a.alloc_n<float>((size_t)T * QWEN_INTERMEDIATE);
+  launch_rmsnorm_ordered(att, L.post_ln, pn, T, false, st);
+  launch_project_ordered(pn, T, QWEN_HIDDEN, L.gw, L.gs, nullptr, QWEN_INTERMEDIATE, g, nullptr, st);
+  launch_project_ordered(pn, T, QWEN_HIDDEN, L.uw, L.us, nullptr, QWEN_INTERMEDIATE, u, nullptr, st);
+  launch_silu_mul(g, u, s, (size_t)T * QWEN_INTERMEDIATE, false, st);
+  launch_project_ordered(s, T, QWEN_INTERMEDIATE, L.dw, L.ds, nullptr, QWEN_HIDDEN, out, att, st);
+  QWEN_HIP(hipGetLastError());
+}
+
+void run_prefill_attention(const DevLayer& L, const float* x, int T, const float* rope, float* k_rows, float* v_rows,
+                           float* att, Arena& a, Mode m, hipStream_t st) {
+  (void)m;
+  float* xn = a.alloc_n<float>((size_t)T * QWEN_HIDDEN);
+  float* q = a.alloc_n<float>((size_t)T * QWEN_HIDDEN);
+  float* ctx = a.alloc_n<float>((size_t)T * QWEN_HIDDEN);
+  launch_rmsnorm_ordered(x, L.ln, xn, T, true, st);
+  launch_project_ordered(xn, T, QWEN_HIDDEN, L.kw, L.ks, L.kb, QWEN_KV_WIDTH, k_rows, nullptr, st);
+  launch_project_ordered(xn, T, QWEN_HIDDEN, L.vw, L.vs, L.vb, QWEN_KV_WIDTH, v_rows, nullptr, st);
+  launch_project_ordered(xn, T, QWEN_HIDDEN, L.qw, L.qs, L.qb, QWEN_HIDDEN, q, nullptr, st);
+  launch_rope_prefill(q, k_rows, rope, T, st);
+  launch_attention_ordered(q, k_rows, v_rows, 0, nullptr, T, true, ctx, st);
+  launch_project_ordered(ctx, T, QWEN_HIDDEN, L.ow, L.os, nullptr, QWEN_HIDDEN, att, nullptr, st);
+  QWEN_HIP(hipGetLastError());
+}
+
+void run_prefill_mlp(const DevLayer& L, const float* att, int T, float* out, Arena& a, Mode m, hipStream_t st) {
+  (void)m;
+  float* pn = a.alloc_n<float>((size_t)T * QWEN_HIDDEN);
+  float* g = a.alloc_n<float>((size_t)T * QWEN_INTERMEDIATE);
+  float* u = a.alloc_n<float>((size_t)T * QWEN_INTERMEDIATE);
+  float* s = a.alloc_n<float>((size_t)T * QWEN_INTERMEDIATE);
+  launch_rmsnorm_ordered(att, L.post_ln, pn, T, true, st);
+  launch_project_ordered(pn, T, QWEN_HIDDEN, L.gw, L.gs, nullptr, QWEN_INTERMEDIATE, g, nullptr, st);
+  launch_project_ordered(pn, T, QWEN_HIDDEN, L.uw, L.us, nullptr, QWEN_INTERMEDIATE, u, nullptr, st);
+  launch_silu_mul(g, u, s, (size_t)T * QWEN_INTERMEDIATE, true, st);
+  launch_project_ordered(s, T, QWEN_INTERMEDIATE, L.dw, L.ds, nullptr, QWEN_HIDDEN, out, att, st);
+  QWEN_HIP(hipGetLastError());
+}
+
+}  // namespace qwen
