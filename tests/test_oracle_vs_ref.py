@@ -89,13 +89,16 @@ def test_decode_top_descriptor_errors(layer_id, past, code):
         assert st == code
 
 
-def test_decode_stub_bitexact():
+def test_decode_stub_closed_form():
+    """The reference stub (qwen_decode_host_wrapper.cpp:12-71) hands its 1536-row Q/O buffers to
+    the MLP as the 8960-row gate/up/down weights and scales (:60-68), so its success path reads
+    past the end of those vectors: undefined behaviour that crashes the process at random.  Only
+    its early-return error path is called here; the success path is pinned by its closed form
+    (zero weights make every projection 0, so the output is exactly +0)."""
     o = oracle()
     x = random_hidden(5, 1)
     out_o = np.ones(HIDDEN, np.float32)
-    out_r = np.ones(HIDDEN, np.float32)
     assert o.oracle_decode_stub_forward(x, 4, out_o) == 0
-    assert REF.qwen_decode_stub_forward(x, 4, out_r) == 0
-    assert bits_equal(out_o, out_r)
-    assert not np.any(out_o)
+    assert bits_equal(out_o, np.zeros(HIDDEN, np.float32))
+    out_r = np.ones(HIDDEN, np.float32)
     assert o.oracle_decode_stub_forward(x, -1, out_o) == REF.qwen_decode_stub_forward(x, -1, out_r) == 1
