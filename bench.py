@@ -1,0 +1,273 @@
+"""Throughput of the quantized Qwen2.5-1.5B decoder-layer hot path on one MI355X.
+
+Default workload: 28-layer Qwen2.5-1.5B-shaped batched decode, 64 sequences, each with a
+4096-position KV history (K/V N(0,1), INT4 quantize/dequantize per row) and one new random token
+per step, positions 4096..4127 (32 steps, then the cycle repeats).  A step is one decode token for
+all 64 sequences through all 28 layers (embedding gather + 28 x [RMSNorm, QKV, RoPE + KV append,
+GQA attention, O, RMSNorm, gate/up + SiLU, down + residual, bf16 rounding]); weights are
+random-init N(0, 0.02), rounded to bf16 and quantized per row to INT4 on the device.
+
+Printed: one JSON line with whole-job tok/s, the dominant kernel's roofline (decode attention
+streaming the fp32 KV cache, timed in isolation with HIP events on the model's stream) and the
+reference C++ host path timed on this machine's CPU on a bounded sample.
+
+    python bench.py [--steps K] [--warmup W] [--workload decode64|decode1|prefill] [--mode fast|ordered]
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "decode tok/s & prefill tok/s (Qwen2.5-1.5B shapes, 1 GPU), % of roofline"
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+LAYERS = 28
+KV_ROW_BYTES = 1024  # 256 fp32 per token per layer, for K and again for V
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=32)
+    ap.add_argument("--warmup", type=int, default=4)
+    ap.add_argument("--workload", default="decode64", choices=["decode64", "decode1", "prefill"])
+    ap.add_argument("--mode", default="fast", choices=["fast", "ordered"])
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
+    ap.add_argument("--no-cpu", action="store_true")
+    return ap.parse_args()
+
+
+# ---------------------------------------------------------------------------------------------
+# CPU baseline: the reference decode host library compiled from the reference sources
+# (oracle/_ref, built by oracle/Makefile), or the oracle restatement when it is absent.
+# ---------------------------------------------------------------------------------------------
+def cpu_baseline_decode(past: int, budget_s: float) -> dict:
+    from work_llm_accelerator_amd.abi import SIGNATURES
+    from work_llm_accelerator_amd.layout import HIDDEN, KV_WIDTH, LAYOUT
+    from work_llm_accelerator_amd.quant import layer_views
+
+    ref = ROOT / "oracle" / "_ref" / "libqwen_decode_ref.so"
+    port = ROOT / "oracle" / "build" / "libqwen_oracle.so"
+    if ref.exists():
+        lib, name, kind = ctypes.CDLL(str(ref)), "qwen_decode_layer_smoke_forward", "reference"
+    else:
+        if not port.exists():
+            os.system(f"make -s -C {ROOT / 'oracle'} oracle >/dev/null 2>&1")
+        lib, name, kind = ctypes.CDLL(str(port)), "oracle_decode_layer_smoke_forward", "port"
+    fn = getattr(lib, name)
+    fn.argtypes = SIGNATURES["qwen_decode_layer_smoke_forward"]
+    fn.restype = ctypes.c_int
+    rng = np.random.default_rng(0)
+    w = rng.integers(0, 256, LAYOUT.total_parameter_bytes, dtype=np.uint8)
+    s = np.full((LAYOUT.total_parameter_bytes + 3) // 4, 0.01, np.float32)
+    v = layer_views(w, s)
+    v["input_layernorm"][:] = 1.0
+    v["post_attention_layernorm"][:] = 1.0
+    args = [v[k] for k in ("input_layernorm", "post_attention_layernorm", "q_w", "k_w", "v_w", "o_w", "gate_w",
+                           "up_w", "down_w", "q_bias", "k_bias", "v_bias", "q_s", "k_s", "v_s", "o_s", "gate_s",
+                           "up_s", "down_s")]
+    x = rng.standard_normal(HIDDEN, dtype=np.float32)
+    kc = rng.standard_normal((past + 1) * KV_WIDTH, dtype=np.float32)
+    vc = rng.standard_normal((past + 1) * KV_WIDTH, dtype=np.float32)
+    out = np.zeros(HIDDEN, np.float32)
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 200):
+        t0 = time.perf_counter()
+        st = fn(x, past, *args, kc, vc, out)
+        times.append(time.perf_counter() - t0)
+        if st != 0:
+            raise RuntimeError(f"CPU baseline returned {st}")
+    t_layer = float(np.median(times))
+    return {"value": 1.0 / (LAYERS * t_layer), "unit": "tok/s", "cores": 1, "kind": kind,
+            "sample": f"{len(times)} single-layer decode steps at KV length {past + 1} through "
+                      f"{'the reference decode .so built from its sources' if kind == 'reference' else 'the oracle'}"
+                      f" (median {t_layer * 1e3:.1f} ms/layer-token, 1 thread), extrapolated x{LAYERS} layers "
+                      f"for one sequence; CPU: {cpu_model()}, {os.cpu_count()} visible cores"}
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+# ---------------------------------------------------------------------------------------------
+def bench_decode(args, torch, batch: int, history: int, seed: int) -> dict:
+    from work_llm_accelerator_amd.model import (KERNEL_ATTN_DECODE, KERNEL_GEMM_DOWN, KERNEL_GEMM_GATE_UP,
+                                                MODE_FAST, MODE_ORDERED, DeviceModel, KvCache, fill_kv_synthetic)
+
+    mode = MODE_FAST if args.mode == "fast" else MODE_ORDERED
+    cycle = 32
+    positions = history + cycle
+    model = DeviceModel(LAYERS, synthetic_seed=seed)
+    cache = KvCache.allocate(LAYERS, batch, positions)
+    fill_kv_synthetic(cache, seed + 1000)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    nsteps = args.warmup + args.steps
+    ids = torch.randint(0, 151936, (nsteps, batch), dtype=torch.int32, device="cuda", generator=gen)
+    pos = [torch.full((batch,), history + (i % cycle), dtype=torch.int32, device="cuda") for i in range(cycle)]
+    hidden = torch.empty(batch, 1536, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+
+    def step(i):
+        model.embed(ids[i], hidden, order=False)
+        model.decode(mode, hidden, pos[i % cycle], positions, cache, order=False)
+
+    for i in range(args.warmup):
+        step(i)
+    model.synchronize()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(model.stream)
+    for i in range(args.warmup, nsteps):
+        step(i)
+    e1.record(model.stream)
+    model.synchronize()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ev_ms = e0.elapsed_time(e1)
+    ms_step = ev_ms / args.steps
+    last_pos = history + ((nsteps - 1) % cycle)
+    keys = last_pos + 1
+    res = {"value": batch * args.steps / (ev_ms / 1e3), "ms_per_step": ms_step, "wall_s": wall}
+    # algorithmic bytes of one step (all layers): INT4 weights + fp32 norms/biases/scales, KV read
+    # (keys rows of K and V) + the appended row, activations in/out.
+    param_bytes = 23_508_992
+    kv_read = batch * keys * 2 * KV_ROW_BYTES
+    step_bytes = LAYERS * (param_bytes + kv_read + batch * 2 * KV_ROW_BYTES + batch * 2 * 1536 * 4)
+    res["step_roofline"] = {"bound": "hbm", "algorithmic_bytes": step_bytes,
+                            "achieved_GBs": step_bytes / (ms_step * 1e-3) / 1e9,
+                            "frac": step_bytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    if mode == MODE_FAST:
+        # dominant kernel: decode attention over the KV cache (96% of the step's bytes at 64 x 4096)
+        attn_ms = model.time_kernel(KERNEL_ATTN_DECODE, 0, 20)
+        attn_bytes = kv_read + batch * 1536 * 4
+        res["roofline"] = {"bound": "hbm", "kernel": "attn_decode_partial_kernel", "achieved":
+                           attn_bytes / (attn_ms * 1e-3) / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                           "frac": attn_bytes / (attn_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "traffic": None,
+                           "avg_launch_us": attn_ms * 1e3, "algorithmic_bytes_per_launch": attn_bytes}
+        gu_ms = model.time_kernel(KERNEL_GEMM_GATE_UP, 0, 20)
+        dn_ms = model.time_kernel(KERNEL_GEMM_DOWN, 0, 20)
+        gu_bytes = 2 * 8960 * 1536 // 2 + 2 * 8960 * 4 + batch * 1536 * 2 + batch * 8960 * 4
+        dn_bytes = 1536 * 8960 // 2 + 1536 * 4 + batch * 8960 * 2 + 2 * batch * 1536 * 4
+        res["kernels"] = {
+            "gemm_gate_up": {"avg_us": gu_ms * 1e3, "GBs": gu_bytes / (gu_ms * 1e-3) / 1e9},
+            "gemm_down": {"avg_us": dn_ms * 1e3, "GBs": dn_bytes / (dn_ms * 1e-3) / 1e9},
+        }
+    model.close()
+    del cache
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_prefill(args, torch, batch: int, seq: int, seed: int) -> dict:
+    from work_llm_accelerator_amd.model import (KERNEL_ATTN_PREFILL, KERNEL_GEMM_GATE_UP, MODE_FAST, MODE_ORDERED,
+                                                DeviceModel, KvCache)
+
+    mode = MODE_FAST if args.mode == "fast" else MODE_ORDERED
+    model = DeviceModel(LAYERS, synthetic_seed=seed)
+    cache = KvCache.allocate(LAYERS, batch, seq)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    ids = torch.randint(0, 151936, (batch * seq,), dtype=torch.int32, device="cuda", generator=gen)
+    hidden = torch.empty(batch, seq, 1536, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+
+    def step():
+        model.embed(ids, hidden, order=False)
+        model.prefill(mode, hidden, cache, order=False)
+
+    for _ in range(args.warmup):
+        step()
+    model.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(model.stream)
+    for _ in range(args.steps):
+        step()
+    e1.record(model.stream)
+    model.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    tokens = batch * seq
+    macs = LAYERS * (46_792_704 * tokens + batch * 12 * 128 * seq * (seq + 1))  # projections + QK^T, PV (causal)
+    res = {"value": tokens / (ms * 1e-3), "ms_per_step": ms,
+           "step_roofline": {"bound": "mfma", "algorithmic_TOPs": 2 * macs / 1e12,
+                             "achieved_TOPs": 2 * macs / (ms * 1e-3) / 1e12,
+                             "frac_int8": 2 * macs / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS}}
+    if mode == MODE_FAST:
+        gu_ms = model.time_kernel(KERNEL_GEMM_GATE_UP, 0, 5)
+        at_ms = model.time_kernel(KERNEL_ATTN_PREFILL, 0, 5)
+        gu_ops = 2 * 2 * 8960 * 1536 * tokens
+        res["roofline"] = {"bound": "mfma", "kernel": "gemm_i8_kernel (gate/up)", "achieved": gu_ops / (gu_ms * 1e-3)
+                           / 1e12, "peak": INT8_PEAK_TOPS, "unit": "TOP/s (int8 dense)",
+                           "frac": gu_ops / (gu_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, "traffic": None,
+                           "avg_launch_us": gu_ms * 1e3, "note": "algorithmic ops; the two-limb code issues 2 int8 "
+                                                               "MFMA passes per product"}
+        res["kernels"] = {"attn_prefill": {"avg_us": at_ms * 1e3}}
+    model.close()
+    return res
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: every box of this run has one MI355X and the hot path needs no "
+              f"collective (sequences shard data-parallel with no exchange); --gpus {args.gpus} is not run.",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs an MI355X (no GPU visible)", file=sys.stderr)
+        sys.exit(1)
+    if args.workload == "decode64":
+        batch, history, seed = 64, 4096, 4
+        r = bench_decode(args, torch, batch, history, seed)
+        config = {"workload": "28-layer Qwen2.5-1.5B-shaped batched decode: 64 sequences x KV history 4096 "
+                              "(positions 4096..4127), 1 new random token per sequence per step, seed 4",
+                  "layers": LAYERS, "batch": batch, "kv_length": f"{history + 1}..{history + 32}", "mode": args.mode}
+        unit, cpu_past = "tok/s", history
+    elif args.workload == "decode1":
+        batch, history, seed = 1, 512, 2
+        r = bench_decode(args, torch, batch, history, seed)
+        config = {"workload": "28-layer Qwen2.5-1.5B-shaped decode, batch 1, KV 513..544 after a 512-token "
+                              "history, seed 2", "layers": LAYERS, "batch": 1, "mode": args.mode}
+        unit, cpu_past = "tok/s", history
+    else:
+        batch, seq, seed = 8, 2048, 3
+        r = bench_prefill(args, torch, batch, seq, seed)
+        config = {"workload": "28-layer Qwen2.5-1.5B-shaped prefill: 8 sequences x 2048 tokens, causal, full KV "
+                              "cache written, seed 3", "layers": LAYERS, "batch": batch, "seq_len": seq,
+                  "mode": args.mode}
+        unit, cpu_past = "tok/s", None
+    line = {"metric": METRIC, "value": r["value"], "unit": unit, "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": r["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "int4 weights x int8 two-limb MFMA, f32" if args.mode == "fast" else "f32",
+            "data": "synthetic (random-init weights, random tokens, N(0,1) quantized KV)", "config": config}
+    for k in ("roofline", "step_roofline", "kernels"):
+        if k in r:
+            line[k] = r[k]
+    if not args.no_cpu and cpu_past is not None:
+        line["cpu_baseline"] = cpu_baseline_decode(cpu_past, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -13,7 +13,7 @@ import pytest
 from work_llm_accelerator_amd import abi
 
 ROOT = Path(__file__).resolve().parents[1]
-DECL = re.compile(r"^\s*(?:int|const char\*|void)\s+(qwen_[a-z0-9_]+)\s*\(", re.M)
+DECL = re.compile(r"^\s*(?:int|const char\s*\*|void\s*\*|void)\s*(qwen_[a-z0-9_]+)\s*\(", re.M)
 
 
 def declared_symbols() -> set[str]:
@@ -43,7 +43,13 @@ def test_library_exports_every_declared_symbol(path):
     assert not missing, f"missing exports: {sorted(missing)}"
 
 
+def test_headers_declare_model_api():
+    names = declared_symbols()
+    for name in abi.EXTRA_SIGNATURES:
+        assert name in names, name
+
+
 def test_bindings_declare_argtypes():
     lib = abi.load()
-    for name in abi.SIGNATURES:
+    for name in list(abi.SIGNATURES) + list(abi.EXTRA_SIGNATURES):
         assert getattr(lib, name).argtypes is not None

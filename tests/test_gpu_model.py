@@ -1,0 +1,266 @@
+"""GPU parity of the device-resident model API (include/qwen_hip_model.h).
+
+* ORDERED decode/prefill over several layers and sequences equals the oracle bit for bit: per
+  layer oracle_decode_layer_block / oracle_prefill_layer_uncapped (the reference host arithmetic)
+  followed by the driver's bf16 rounding (verification/real_host_top_backend.py:260,334).
+* FAST decode/prefill agrees with the oracle within the stated tolerance:
+      max |y - y_ref| <= 1e-3 * max |y_ref|   per layer output and per K/V cache tensor
+  (checked on one layer without the inter-layer bf16 rounding, which would otherwise quantize a
+  1e-6 difference into a whole bf16 step), and within 1e-2 * max over two rounded layers.
+* The device INT4 quantizer equals the reference scheme (verification/real_host_top_backend.py:31-41,
+  restated in work_llm_accelerator_amd.quant) bit for bit, including all-zero rows and exact ties.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from _cases import bits_equal, first_mismatch, quantized_kv_history, random_hidden, random_layer
+from _oracle import oracle
+from work_llm_accelerator_amd.layout import HIDDEN, KV_WIDTH
+from work_llm_accelerator_amd.quant import quantize_int4_per_channel, round_bfloat16_array
+
+pytestmark = pytest.mark.gpu
+
+FAST_TOL = 1e-3        # one layer, fp32 output: |y - y_ref| <= FAST_TOL * max|y_ref|
+FAST_TOL_ROUNDED = 1e-2  # two layers with bf16 rounding between them
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch as t
+
+    return t
+
+
+@pytest.fixture(scope="module")
+def layers2():
+    return [random_layer(seed=61), random_layer(seed=62)]
+
+
+def images(layers):
+    w = np.concatenate([c.weight_ddr for c in layers])
+    s = np.concatenate([c.scale_ddr for c in layers])
+    return w, s
+
+
+@pytest.fixture(scope="module")
+def model2(torch, layers2):
+    from work_llm_accelerator_amd.model import DeviceModel
+
+    w, s = images(layers2)
+    m = DeviceModel(2, w, s)
+    yield m
+    m.close()
+
+
+def oracle_decode(layers, x, past, k_hist, v_hist, rounding=True):
+    """Per-layer oracle decode of one sequence; k_hist/v_hist[l] hold past+1 rows (row `past` is written)."""
+    o = oracle()
+    h = x.copy()
+    for l, case in enumerate(layers):
+        out = np.zeros(HIDDEN, np.float32)
+        assert o.oracle_decode_layer_block(h, past, case.weight_ddr, case.scale_ddr, k_hist[l], v_hist[l], out) == 0
+        h = round_bfloat16_array(out) if rounding else out
+    return h
+
+
+def oracle_prefill(layers, x, S, rounding=True):
+    o = oracle()
+    h = x.copy()
+    ks, vs = [], []
+    for case in layers:
+        kc = np.zeros(S * KV_WIDTH, np.float32)
+        vc = np.zeros(S * KV_WIDTH, np.float32)
+        out = np.zeros(S * HIDDEN, np.float32)
+        assert o.oracle_prefill_layer_uncapped(h, S, case.weight_ddr, case.scale_ddr, kc, vc, out) == 0
+        h = round_bfloat16_array(out) if rounding else out
+        ks.append(kc)
+        vs.append(vc)
+    return h, ks, vs
+
+
+def rel_err(got, ref):
+    scale = float(np.max(np.abs(ref)))
+    return float(np.max(np.abs(got.astype(np.float64) - ref.astype(np.float64)))) / max(scale, 1e-30)
+
+
+def decode_setup(torch, n_layers, pasts, positions_cap, seed):
+    from work_llm_accelerator_amd.model import KvCache
+
+    B = len(pasts)
+    cache = KvCache.allocate(n_layers, B, positions_cap)
+    hist = {}
+    for l in range(n_layers):
+        for b, past in enumerate(pasts):
+            k, v = quantized_kv_history(seed + 10 * l + b, past + 1)
+            k = k.reshape(past + 1, KV_WIDTH)
+            v = v.reshape(past + 1, KV_WIDTH)
+            k[past] = 0.0
+            v[past] = 0.0
+            cache.k[l, b, :past + 1] = torch.from_numpy(k)
+            cache.v[l, b, :past + 1] = torch.from_numpy(v)
+            hist[(l, b)] = (k.reshape(-1).copy(), v.reshape(-1).copy())
+    x = np.stack([round_bfloat16_array(random_hidden(seed + 100 + b, 1)) for b in range(B)])
+    return cache, hist, x
+
+
+@pytest.mark.parametrize("mode_name", ["ordered", "fast"])
+def test_model_decode(torch, layers2, model2, mode_name):
+    from work_llm_accelerator_amd.model import FLAG_NO_BF16_ROUND, MODE_FAST, MODE_ORDERED
+
+    pasts = [0, 5, 300]
+    print(f"model decode {mode_name} pasts={pasts}", flush=True)
+    cache, hist, x = decode_setup(torch, 2, pasts, 320, seed=7)
+    hidden = torch.from_numpy(x).cuda()
+    pos = torch.tensor(pasts, dtype=torch.int32, device="cuda")
+    if mode_name == "ordered":
+        model2.decode(MODE_ORDERED, hidden, pos, max(pasts) + 1, cache)
+        model2.synchronize()
+        got = hidden.cpu().numpy()
+        for b, past in enumerate(pasts):
+            kl = [hist[(l, b)][0].copy() for l in range(2)]
+            vl = [hist[(l, b)][1].copy() for l in range(2)]
+            ref = oracle_decode(layers2, x[b], past, kl, vl)
+            assert bits_equal(got[b], ref), f"seq {b}: " + first_mismatch(got[b], ref)
+            for l in range(2):
+                gk = cache.k[l, b, :past + 1].cpu().numpy().reshape(-1)
+                gv = cache.v[l, b, :past + 1].cpu().numpy().reshape(-1)
+                assert bits_equal(gk, kl[l]), first_mismatch(gk, kl[l])
+                assert bits_equal(gv, vl[l]), first_mismatch(gv, vl[l])
+    else:
+        # one layer without rounding: the per-layer tolerance
+        from work_llm_accelerator_amd.model import DeviceModel
+
+        m1 = DeviceModel(1, layers2[0].weight_ddr, layers2[0].scale_ddr)
+        try:
+            cache1, hist1, _ = decode_setup(torch, 1, pasts, 320, seed=7)
+            h1 = torch.from_numpy(x).cuda()
+            m1.decode(MODE_FAST | FLAG_NO_BF16_ROUND, h1, pos, max(pasts) + 1, cache1)
+            m1.synchronize()
+            got = h1.cpu().numpy()
+            for b, past in enumerate(pasts):
+                kl = [hist1[(0, b)][0].copy()]
+                vl = [hist1[(0, b)][1].copy()]
+                ref = oracle_decode(layers2[:1], x[b], past, kl, vl, rounding=False)
+                assert rel_err(got[b], ref) <= FAST_TOL, (b, rel_err(got[b], ref))
+                gk = cache1.k[0, b, past].cpu().numpy()
+                gv = cache1.v[0, b, past].cpu().numpy()
+                rk = kl[0].reshape(past + 1, KV_WIDTH)[past]
+                rv = vl[0].reshape(past + 1, KV_WIDTH)[past]
+                assert rel_err(gk, rk) <= FAST_TOL and rel_err(gv, rv) <= FAST_TOL
+                # untouched history rows stay bit-identical
+                assert bits_equal(cache1.k[0, b, :past].cpu().numpy().reshape(-1), kl[0][:past * KV_WIDTH])
+        finally:
+            m1.close()
+        # two layers with the driver's rounding
+        model2.decode(MODE_FAST, hidden, pos, max(pasts) + 1, cache)
+        model2.synchronize()
+        got = hidden.cpu().numpy()
+        for b, past in enumerate(pasts):
+            kl = [hist[(l, b)][0].copy() for l in range(2)]
+            vl = [hist[(l, b)][1].copy() for l in range(2)]
+            ref = oracle_decode(layers2, x[b], past, kl, vl)
+            assert rel_err(got[b], ref) <= FAST_TOL_ROUNDED, (b, rel_err(got[b], ref))
+
+
+@pytest.mark.parametrize("mode_name", ["ordered", "fast"])
+def test_model_prefill(torch, layers2, model2, mode_name):
+    from work_llm_accelerator_amd.model import FLAG_NO_BF16_ROUND, MODE_FAST, MODE_ORDERED, DeviceModel, KvCache
+
+    B, S = 2, 37
+    print(f"model prefill {mode_name} B={B} S={S}", flush=True)
+    xs = [round_bfloat16_array(random_hidden(900 + b, S)) for b in range(B)]
+    if mode_name == "ordered":
+        cache = KvCache.allocate(2, B, 48)
+        hidden = torch.from_numpy(np.stack(xs).reshape(B, S, HIDDEN)).cuda()
+        model2.prefill(MODE_ORDERED, hidden, cache)
+        model2.synchronize()
+        got = hidden.cpu().numpy().reshape(B, -1)
+        for b in range(B):
+            ref, ks, vs = oracle_prefill(layers2, xs[b], S)
+            assert bits_equal(got[b], ref), f"seq {b}: " + first_mismatch(got[b], ref)
+            for l in range(2):
+                gk = cache.k[l, b, :S].cpu().numpy().reshape(-1)
+                gv = cache.v[l, b, :S].cpu().numpy().reshape(-1)
+                assert bits_equal(gk, ks[l]), first_mismatch(gk, ks[l])
+                assert bits_equal(gv, vs[l]), first_mismatch(gv, vs[l])
+    else:
+        m1 = DeviceModel(1, layers2[0].weight_ddr, layers2[0].scale_ddr)
+        try:
+            cache = KvCache.allocate(1, B, 48)
+            hidden = torch.from_numpy(np.stack(xs).reshape(B, S, HIDDEN)).cuda()
+            m1.prefill(MODE_FAST | FLAG_NO_BF16_ROUND, hidden, cache)
+            m1.synchronize()
+            got = hidden.cpu().numpy().reshape(B, -1)
+            for b in range(B):
+                ref, ks, vs = oracle_prefill(layers2[:1], xs[b], S, rounding=False)
+                assert rel_err(got[b], ref) <= FAST_TOL, (b, rel_err(got[b], ref))
+                gk = cache.k[0, b, :S].cpu().numpy().reshape(-1)
+                gv = cache.v[0, b, :S].cpu().numpy().reshape(-1)
+                assert rel_err(gk, ks[0]) <= FAST_TOL and rel_err(gv, vs[0]) <= FAST_TOL
+        finally:
+            m1.close()
+
+
+def test_model_prefill_ordered_uncapped(torch, layers2):
+    """S = 133 > 128 (the reference's per-call cap): the per-token arithmetic is unchanged."""
+    from work_llm_accelerator_amd.model import FLAG_NO_BF16_ROUND, MODE_ORDERED, DeviceModel, KvCache
+
+    S = 133
+    print(f"model prefill ordered uncapped S={S}", flush=True)
+    x = round_bfloat16_array(random_hidden(77, S))
+    m1 = DeviceModel(1, layers2[1].weight_ddr, layers2[1].scale_ddr)
+    try:
+        cache = KvCache.allocate(1, 1, S)
+        hidden = torch.from_numpy(x.reshape(1, S, HIDDEN)).cuda()
+        m1.prefill(MODE_ORDERED | FLAG_NO_BF16_ROUND, hidden, cache)
+        m1.synchronize()
+        got = hidden.cpu().numpy().reshape(-1)
+        ref, ks, vs = oracle_prefill(layers2[1:], x, S, rounding=False)
+        assert bits_equal(got, ref), first_mismatch(got, ref)
+        assert bits_equal(cache.k[0, 0].cpu().numpy().reshape(-1), ks[0])
+    finally:
+        m1.close()
+
+
+def test_device_quantizer_bitexact(torch):
+    rng = np.random.default_rng(5)
+    w = (rng.standard_normal((64, 1536), dtype=np.float32) * np.float32(0.02))
+    w[3] = 0.0                       # all-zero row -> scale 1, all nibbles 0
+    w[5, :8] = [7.0, 3.5, -3.5, 2.5, -0.5, 0.5, 1.5, -8.0]  # exact ties of rint (half to even)
+    w = round_bfloat16_array(w).reshape(64, 1536)
+    packed_ref, scales_ref = quantize_int4_per_channel(w)
+    packed, scales = __import__("work_llm_accelerator_amd.model", fromlist=["x"]).quantize_int4_device(
+        torch.from_numpy(w).cuda())
+    torch.cuda.synchronize()
+    assert bits_equal(scales.cpu().numpy(), scales_ref)
+    assert np.array_equal(packed.cpu().numpy(), packed_ref)
+
+
+def test_synthetic_model_runs(torch):
+    """A synthetic 2-layer model decodes and prefills without error and gives finite outputs in
+    both modes; FAST stays within the rounded tolerance of ORDERED on the same synthetic model."""
+    from work_llm_accelerator_amd.model import MODE_FAST, MODE_ORDERED, DeviceModel, KvCache, fill_kv_synthetic
+
+    m = DeviceModel(2, synthetic_seed=4)
+    try:
+        cache = KvCache.allocate(2, 4, 600)
+        fill_kv_synthetic(cache, 11)
+        ids = torch.randint(0, 151936, (4,), dtype=torch.int32, device="cuda")
+        h0 = torch.empty(4, HIDDEN, dtype=torch.float32, device="cuda")
+        m.embed(ids, h0)
+        pos = torch.tensor([512, 513, 100, 599], dtype=torch.int32, device="cuda")
+        outs = []
+        for mode in (MODE_ORDERED, MODE_FAST):
+            c = KvCache(cache.k.clone(), cache.v.clone(), 2, 4, 600)
+            h = h0.clone()
+            m.decode(mode, h, pos, 600, c)
+            m.synchronize()
+            outs.append(h.cpu().numpy())
+        assert np.all(np.isfinite(outs[0])) and np.all(np.isfinite(outs[1]))
+        assert rel_err(outs[1], outs[0]) <= FAST_TOL_ROUNDED
+        assert m.time_kernel(1, 0, 3) > 0.0
+    finally:
+        m.close()

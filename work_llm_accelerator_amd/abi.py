@@ -50,9 +50,23 @@ SIGNATURES: dict[str, list] = {
     "qwen_prefill_dispatch_layers_forward": [c_void_p, c_int, U8P, F32P, F32P, F32P] + _SRAM + [c_void_p],
 }
 
-# Additive entry points of this build (no counterpart in the reference).
+# Additive entry points of this build (no counterpart in the reference): the device-resident
+# model API of include/qwen_hip_model.h.  Device pointers are passed as c_void_p.
+P = ctypes.c_void_p
 EXTRA_SIGNATURES: dict[str, tuple[list, object]] = {
     "qwen_hip_last_error": ([], ctypes.c_char_p),
+    "qwen_hip_model_create": ([c_int, U8P, F32P, ctypes.POINTER(P)], c_int),
+    "qwen_hip_model_create_synthetic": ([c_int, c_u64, ctypes.POINTER(P)], c_int),
+    "qwen_hip_model_destroy": ([P], c_int),
+    "qwen_hip_model_layers": ([P], c_int),
+    "qwen_hip_model_stream": ([P], P),
+    "qwen_hip_model_synchronize": ([P], c_int),
+    "qwen_hip_model_decode": ([P, c_int, c_int, P, P, c_int, P, P, c_u64, c_u64], c_int),
+    "qwen_hip_model_prefill": ([P, c_int, c_int, c_int, P, P, P, c_u64, c_u64], c_int),
+    "qwen_hip_model_embed": ([P, P, c_int, P], c_int),
+    "qwen_hip_model_time_kernel": ([P, c_int, c_int, c_int, ctypes.POINTER(ctypes.c_float)], c_int),
+    "qwen_hip_quantize_int4": ([P, c_int, c_int, P, P, P], c_int),
+    "qwen_hip_fill_kv_synthetic": ([P, c_u64, c_u64, P], c_int),
 }
 
 _LIB: ctypes.CDLL | None = None
@@ -74,10 +88,9 @@ def load(path: Path | str | None = None) -> ctypes.CDLL:
         fn.argtypes = argtypes
         fn.restype = c_int
     for name, (argtypes, restype) in EXTRA_SIGNATURES.items():
-        fn = getattr(lib, name, None)
-        if fn is not None:
-            fn.argtypes = argtypes
-            fn.restype = restype
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = restype
     if path is None:
         _LIB = lib
     return lib

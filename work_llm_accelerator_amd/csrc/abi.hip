@@ -21,18 +21,16 @@ using namespace qwen;
 
 namespace {
 
-thread_local std::string g_last_error;
-
 template <class Fn>
 int guarded(Fn&& fn) {
   try {
     return fn();
   } catch (const HipError& e) {
-    g_last_error = std::string(e.what) + ": " + hipGetErrorString(e.code);
+    set_last_error(std::string(e.what) + ": " + hipGetErrorString(e.code));
   } catch (const std::exception& e) {
-    g_last_error = e.what();
+    set_last_error(e.what());
   }
-  if (std::getenv("QWEN_HIP_VERBOSE")) std::fprintf(stderr, "qwen-mi355x: %s\n", g_last_error.c_str());
+  if (std::getenv("QWEN_HIP_VERBOSE")) std::fprintf(stderr, "qwen-mi355x: %s\n", last_error_cstr());
   return QWEN_ERR_DEVICE;
 }
 
@@ -105,7 +103,7 @@ int decode_layer_host(const HostLayer& h, const float* x, int past, float* k_cac
     float* kc_d = stage_in(A, k_cache, kv_n, st);
     float* vc_d = stage_in(A, v_cache, kv_n, st);
     float* att_d = A.alloc_n<float>(QWEN_HIDDEN);
-    DecodeBatch b{1, pos_d, rope_d, true, kc_d, vc_d, 0};
+    DecodeBatch b{1, pos_d, rope_d, true, kc_d, vc_d, 0, past + 1};
     run_decode_attention(d, x_d, b, att_d, A, m, st);
     const size_t row = (size_t)past * QWEN_KV_WIDTH;
     copy_out(k_cache + row, kc_d + row, QWEN_KV_WIDTH, st);
@@ -127,7 +125,7 @@ int decode_layer_host(const HostLayer& h, const float* x, int past, float* k_cac
 
 extern "C" {
 
-const char* qwen_hip_last_error(void) { return g_last_error.c_str(); }
+const char* qwen_hip_last_error(void) { return last_error_cstr(); }
 
 int qwen_decode_attention_smoke_forward(const float* x, int past, const float* ln, const uint8_t* qw, const uint8_t* kw,
                                         const uint8_t* vw, const uint8_t* ow, const float* qb, const float* kb,

@@ -14,10 +14,69 @@ void launch_project_ordered(const float* x, int tokens, int in_dim, const uint8_
 void launch_silu_mul(const float* g, const float* u, float* s, size_t n, bool prefill, hipStream_t st);
 void launch_rope_append_decode(float* q, const float* k, const float* v, const int* pos, const float* rope,
                                bool rope_rows_are_tokens, float* k_cache, float* v_cache, size_t cache_stride,
-                               int tokens, hipStream_t st);
+                               int max_keys, int tokens, hipStream_t st);
 void launch_rope_prefill(float* q, float* k_rows, const float* rope, int tokens, hipStream_t st);
 void launch_rope_table_prefill(float* rope, int first, int count, hipStream_t st);
 void launch_attention_ordered(const float* q, const float* k_cache, const float* v_cache, size_t cache_stride,
-                              const int* pos, int tokens, bool prefill, float* ctx, hipStream_t st);
+                              const int* pos, int max_keys, int tokens, bool prefill, float* ctx, hipStream_t st);
+
+// ---- FAST kernels: kernels_fast.hip ----
+constexpr int kKChunk = 128;        // K values per repacked weight chunk
+constexpr int kQuantMax = 32512;    // |X| bound of the two-limb activation code (127 * 256)
+constexpr int kMaxQuantRow = 8960;  // widest activation row that is quantized
+constexpr int kAttnChunk = 256;     // keys per decode-attention block
+constexpr int kNormNone = 0, kNormDecode = 1, kNormPrefill = 2;
+constexpr int kEpiStore = 0, kEpiSiluMul = 1, kEpiResidual = 2;
+
+// Bytes of the two-limb code of `rows` activation rows of width n.
+inline size_t xq_bytes(size_t rows, size_t n) { return rows * n * 2u; }
+
+struct GemmArgs {
+  const uint8_t* wp;    // repacked weights (tile layout)
+  const uint8_t* wp2;   // second matrix (gate/up pair) or null
+  const float* sw;      // per-row scales
+  const float* sw2;
+  const float* bias;    // kEpiStore: optional bias
+  const int8_t* xq;     // activation limbs [tokens][in/128][2][128]
+  const float* sx;      // per-token scale
+  const int* sums;      // per-token (sum H, sum L)
+  int tokens, in_dim, out_dim;
+  float* y;             // output [tokens][y_stride]
+  size_t y_stride;
+  const float* resid;   // kEpiResidual: residual [tokens][resid_stride]
+  size_t resid_stride;
+  float* y_raw;         // kEpiResidual: optional copy of the output before bf16 rounding
+  int round_bf16;       // kEpiResidual: round the output to bf16 (driver rounding)
+  int prefill_silu;     // kEpiSiluMul: 1 = approx_exp SiLU (prefill), 0 = expf SiLU (decode)
+};
+
+void launch_repack_int4(const uint8_t* W, int out_dim, int in_dim, uint8_t* WP, hipStream_t st);
+void launch_norm_quant(const float* x, size_t x_stride, int rows, int n, const float* w, int norm, int8_t* xq,
+                       float* sx, int* sums, float* xn, hipStream_t st);
+void launch_gemm_i8(const GemmArgs& a, int epi, hipStream_t st);
+void launch_rope_qkv(float* qkv, int qkv_stride, const int* pos, int seq_len, int limit, int tokens,
+                     const float* rope, float* k_cache, float* v_cache, size_t seq_stride, hipStream_t st);
+void launch_attn_decode(const float* qkv, int qkv_stride, const float* k_cache, const float* v_cache,
+                        size_t seq_stride, const int* pos, int batch, int max_keys, float* part, float2* pml,
+                        float* ctx, int8_t* xq, float* sx, int* sums, hipStream_t st);
+void launch_attn_decode_partial_only(const float* qkv, int qkv_stride, const float* k_cache, const float* v_cache,
+                                     size_t seq_stride, const int* pos, int batch, int max_keys, float* part,
+                                     float2* pml, hipStream_t st);
+void launch_attn_prefill(const float* qkv, int qkv_stride, const float* k_cache, const float* v_cache,
+                         size_t seq_stride, int S, int nseq, float* ctx, hipStream_t st);
+void launch_round_bf16(float* x, size_t n, hipStream_t st);
+
+}  // namespace qwen
+
+namespace qwen {
+
+// ---- device quantizer, synthetic inputs, embedding: kernels_init.hip ----
+uint64_t synth_stream_host(uint64_t seed, uint64_t key);
+void launch_quantize_rows(const float* src, int out_dim, int in_dim, uint64_t stream, float sigma, uint8_t* packed,
+                          float* scales, hipStream_t st);
+void launch_fill_vector(float* dst, size_t n, uint64_t stream, float sigma, int bf16, float constant, hipStream_t st);
+void launch_fill_bf16_table(uint16_t* dst, size_t n, uint64_t stream, float sigma, hipStream_t st);
+void launch_kv_synthetic(float* cache, uint64_t rows, uint64_t stream, hipStream_t st);
+void launch_embed(const uint16_t* table, const int* ids, int count, float* hidden, hipStream_t st);
 
 }  // namespace qwen

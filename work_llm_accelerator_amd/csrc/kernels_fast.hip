@@ -1,0 +1,765 @@
+// FAST kernels: the roofline-oriented path (gfx950 / CDNA4).
+//
+// These kernels compute the same layer as the reference (qwen_decode_*_kernel.cpp,
+// qwen_prefill_*_kernel.cpp host branch) but reorder every fp32 reduction, so their results
+// agree with the reference to a relative tolerance instead of bit for bit:
+//   * INT4 projections run on the int8 matrix cores (v_mfma_i32_16x16x64_i8).  Weights are
+//     repacked once into a lane-contiguous tile layout (each wave streams 1 KiB contiguous per
+//     128-wide K chunk) and enter the MFMA as q+8 in [0,15].  Activations are quantized per token
+//     into two int8 limbs X = 256*H + L with |X| <= 32512 (15 bits), so both limb products are
+//     accumulated exactly in int32; the row scale, the token scale and the -8*sum(X) offset
+//     correction are applied once after the K reduction.
+//   * Decode attention is split over the KV length (flash-decoding): one block per
+//     (KV chunk, KV head, sequence) streams each K/V row once for all 6 query heads of its group.
+//   * Prefill attention is a causal online-softmax kernel over LDS-staged K/V tiles.
+// Elementwise nonlinearities keep the reference's functions (host-compatible expf for decode
+// SiLU, approx_exp for prefill softmax and SiLU), so the tolerance only has to absorb reordering
+// and the 15-bit activation quantization.
+#include <hip/hip_runtime.h>
+
+#include "kernels.hpp"
+#include "qwen_device_math.hpp"
+
+namespace qwen {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// Streaming (non-temporal) loads: data read once per launch should not displace reused lines.
+__device__ __forceinline__ uint4 ld_stream(const uint4* p) {
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ float4 ld_stream(const float4* p) {
+  const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+  return make_float4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ float2 ld_stream(const float2* p) {
+  const f32x2 v = __builtin_nontemporal_load(reinterpret_cast<const f32x2*>(p));
+  return make_float2(v[0], v[1]);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Weight repack.  Reference layout: W[o][i] is the nibble at byte (o*in + i)/2, low nibble for
+// an even flat index, value q in [-8,7] stored as q & 15 (qwen_decode_attention_kernel.cpp:44-60).
+// Tile layout: [out/16 row tiles][in/128 K chunks][64 lanes][16 bytes].  Lane l covers row
+// 16*rt + (l & 15) and K = 128*kc + 32*(l >> 4) + [0, 32).  Inside the 16 bytes, 32-bit word w
+// covers K 8w..8w+7 of that range: byte b holds K 8w+b in its low nibble and K 8w+4+b in its high
+// nibble, each stored as q + 8.  Unpacking word w as (w & 0x0F0F0F0F, (w >> 4) & 0x0F0F0F0F)
+// then yields 8 int8 values in natural K order.
+// grid = (out/16, in/128), block = 64.
+// ---------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(64) repack_int4_kernel(const uint8_t* __restrict__ W, int in_dim,
+                                                         uint8_t* __restrict__ WP) {
+  const int rt = blockIdx.x;
+  const int kc = blockIdx.y;
+  const int l = threadIdx.x;
+  const int row = rt * 16 + (l & 15);
+  const int kbase = kc * kKChunk + 32 * (l >> 4);
+  const uint8_t* src = W + (size_t)row * (size_t)(in_dim / 2);
+  uint32_t words[4];
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int klo = kbase + 8 * w + b;
+      const int khi = klo + 4;
+      const uint32_t blo = src[klo >> 1];
+      const uint32_t bhi = src[khi >> 1];
+      const uint32_t nlo = (klo & 1) ? (blo >> 4) : (blo & 0xFu);
+      const uint32_t nhi = (khi & 1) ? (bhi >> 4) : (bhi & 0xFu);
+      word |= (((nlo ^ 8u) & 0xFu) | (((nhi ^ 8u) & 0xFu) << 4)) << (8 * b);
+    }
+    words[w] = word;
+  }
+  const size_t dst = (((size_t)rt * (size_t)(in_dim / kKChunk) + (size_t)kc) * 64u + (size_t)l) * 16u;
+  *reinterpret_cast<uint4*>(WP + dst) = make_uint4(words[0], words[1], words[2], words[3]);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Block reductions (256 threads = 4 waves of 64).
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// Reductions over the 4 waves of a 256-thread block; every thread receives the result.
+__device__ __forceinline__ float block_max4(float v, float* s4) {
+  v = wave_max(v);
+  if ((threadIdx.x & 63) == 0) s4[threadIdx.x >> 6] = v;
+  __syncthreads();
+  const float r = fmaxf(fmaxf(s4[0], s4[1]), fmaxf(s4[2], s4[3]));
+  __syncthreads();
+  return r;
+}
+__device__ __forceinline__ double block_sum4_d(double v, double* s4) {
+  v = wave_sum_d(v);
+  if ((threadIdx.x & 63) == 0) s4[threadIdx.x >> 6] = v;
+  __syncthreads();
+  const double r = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+  __syncthreads();
+  return r;
+}
+__device__ __forceinline__ float block_sum4(float v, float* s4) {
+  v = wave_sum(v);
+  if ((threadIdx.x & 63) == 0) s4[threadIdx.x >> 6] = v;
+  __syncthreads();
+  const float r = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+  __syncthreads();
+  return r;
+}
+__device__ __forceinline__ int block_sum4_i(int v, int* s4) {
+  v = wave_sum_i(v);
+  if ((threadIdx.x & 63) == 0) s4[threadIdx.x >> 6] = v;
+  __syncthreads();
+  const int r = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+  __syncthreads();
+  return r;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Two-limb activation quantization of one row held in LDS (n values, n % 128 == 0), done by a
+// 256-thread block.  Writes the limbs in the GEMM's layout ([K chunk][limb][128 bytes] per row),
+// the token scale and the two limb sums.
+// ---------------------------------------------------------------------------------------------
+__device__ void quantize_row_lds(const float* __restrict__ v, int n, int8_t* __restrict__ xq_row,
+                                 float* __restrict__ sx_out, int* __restrict__ sums_out, float* red_f, int* red_i) {
+  float amax = 0.0f;
+  for (int k = threadIdx.x; k < n; k += 256) amax = fmaxf(amax, fabsf(v[k]));
+  amax = block_max4(amax, red_f);
+  const float sx = amax > 0.0f ? amax / (float)kQuantMax : 1.0f;
+  const float inv = amax > 0.0f ? (float)kQuantMax / amax : 0.0f;
+  int sh = 0, sl = 0;
+  for (int k = threadIdx.x; k < n; k += 256) {
+    float xf = rintf(v[k] * inv);
+    xf = fminf(fmaxf(xf, -(float)kQuantMax), (float)kQuantMax);
+    const int X = (int)xf;
+    const int H = (X + 128) >> 8;
+    const int L = X - (H << 8);
+    const int chunk = k >> 7;
+    const int within = k & 127;
+    xq_row[chunk * 256 + within] = (int8_t)H;
+    xq_row[chunk * 256 + 128 + within] = (int8_t)L;
+    sh += H;
+    sl += L;
+  }
+  sh = block_sum4_i(sh, red_i);
+  sl = block_sum4_i(sl, red_i);
+  if (threadIdx.x == 0) {
+    *sx_out = sx;
+    sums_out[0] = sh;
+    sums_out[1] = sl;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// RMSNorm (optional) + quantization, one block per token row.
+//   NORM_DECODE: decode rmsnorm (double mean square, qwen_decode_attention_kernel.cpp:13-27)
+//   NORM_PREFILL: prefill rmsnorm (float, approx_sqrt, qwen_prefill_attention_kernel.cpp:112-126)
+//   NORM_NONE: quantize x as is.
+// Optionally writes the normalized fp32 row to xn.
+// ---------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) norm_quant_kernel(const float* __restrict__ x, size_t x_stride, int n,
+                                                         const float* __restrict__ w, int norm,
+                                                         int8_t* __restrict__ xq, float* __restrict__ sx,
+                                                         int* __restrict__ sums, float* __restrict__ xn) {
+  __shared__ float row[kMaxQuantRow];
+  __shared__ float red_f[4];
+  __shared__ double red_d[4];
+  __shared__ int red_i[4];
+  const int t = blockIdx.x;
+  const float* xr = x + (size_t)t * x_stride;
+  for (int k = threadIdx.x; k < n; k += 256) row[k] = xr[k];
+  __syncthreads();
+  if (norm == kNormDecode) {
+    double ss = 0.0;
+    for (int k = threadIdx.x; k < n; k += 256) ss += (double)row[k] * (double)row[k];
+    ss = block_sum4_d(ss, red_d);
+    const double inv = 1.0 / sqrt(ss / (double)n + (double)QWEN_RMS_EPS);
+    for (int k = threadIdx.x; k < n; k += 256) row[k] = (float)((double)row[k] * inv * (double)w[k]);
+  } else if (norm == kNormPrefill) {
+    float ss = 0.0f;
+    for (int k = threadIdx.x; k < n; k += 256) ss += row[k] * row[k];
+    ss = block_sum4(ss, red_f);
+    const float inv = 1.0f / approx_sqrt(ss / (float)n + QWEN_RMS_EPS);
+    for (int k = threadIdx.x; k < n; k += 256) row[k] = row[k] * inv * w[k];
+  }
+  __syncthreads();
+  if (xn)
+    for (int k = threadIdx.x; k < n; k += 256) xn[(size_t)t * n + k] = row[k];
+  quantize_row_lds(row, n, xq + (size_t)t * (size_t)(2 * n), sx + t, sums + 2 * t, red_f, red_i);
+}
+
+// ---------------------------------------------------------------------------------------------
+// INT4 x two-limb int8 GEMM on the matrix cores:
+//   y[t][o] = sw[o] * sx[t] * ( 256*(sum_k u(o,k) H(t,k) - 8 SH(t)) + (sum_k u(o,k) L(t,k) - 8 SL(t)) )
+// with u = q + 8.  A block has 4 waves.  KSPLIT waves share one 16-row tile and split its K
+// chunks (their int32 partial sums are added through LDS, exact); 4/KSPLIT row tiles per block.
+// Each wave covers NT column tiles of 16 tokens.  DUAL runs a second weight matrix over the same
+// activations (gate and up).  grid = (ceil(tokens / (16*NT)), out/16 / (4/KSPLIT)).
+// MFMA lane mapping (16x16 output tile): A row = lane & 15, B column = lane & 15, both taking
+// the same 16 K values per lane group (lane >> 4); D holds rows 4*(lane>>4)+r, column lane & 15.
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ void unpack16(const uint4 w, v4i& a1, v4i& a2) {
+  const uint32_t m = 0x0F0F0F0Fu;
+  a1[0] = (int)(w.x & m);
+  a1[1] = (int)((w.x >> 4) & m);
+  a1[2] = (int)(w.y & m);
+  a1[3] = (int)((w.y >> 4) & m);
+  a2[0] = (int)(w.z & m);
+  a2[1] = (int)((w.z >> 4) & m);
+  a2[2] = (int)(w.w & m);
+  a2[3] = (int)((w.w >> 4) & m);
+}
+
+template <int NT, int KSPLIT, bool DUAL>
+struct GemmAcc {
+  v4i h[NT], l[NT];
+  v4i h2[DUAL ? NT : 1], l2[DUAL ? NT : 1];
+};
+
+template <int NT, int KSPLIT, int EPI, bool DUAL>
+__global__ void __launch_bounds__(256) gemm_i8_kernel(GemmArgs a) {
+  constexpr int RTB = 4 / KSPLIT;  // row tiles per block
+  constexpr int NACC = NT * 8 * (DUAL ? 2 : 1);  // int32 accumulators per lane
+  __shared__ int red[KSPLIT > 1 ? (KSPLIT - 1) * 64 * NACC : 1];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int rt = blockIdx.y * RTB + wave / KSPLIT;
+  const int ks = wave % KSPLIT;
+  const int row_tiles = a.out_dim / 16;
+  const bool rt_ok = rt < row_tiles;
+  const int nkc = a.in_dim / kKChunk;
+  const int tok0 = blockIdx.x * (16 * NT);
+  const int g = lane >> 4;
+  const int col = lane & 15;
+
+  v4i accH[NT], accL[NT], accH2[NT], accL2[NT];
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+    accH[n] = v4i{0, 0, 0, 0};
+    accL[n] = v4i{0, 0, 0, 0};
+    accH2[n] = v4i{0, 0, 0, 0};
+    accL2[n] = v4i{0, 0, 0, 0};
+  }
+
+  // K chunks of this wave: [kc_begin, kc_end)
+  const int per = (nkc + KSPLIT - 1) / KSPLIT;
+  const int kc_begin = min(nkc, ks * per);
+  const int kc_end = min(nkc, kc_begin + per);
+  const size_t row_stride_x = (size_t)a.in_dim * 2u;  // bytes per token row of limbs
+
+  if (rt_ok) {
+    const uint4* wp = reinterpret_cast<const uint4*>(a.wp) + ((size_t)rt * nkc) * 64u + lane;
+    const uint4* wp2 = DUAL ? reinterpret_cast<const uint4*>(a.wp2) + ((size_t)rt * nkc) * 64u + lane : nullptr;
+    const int8_t* xbase[NT];
+    bool tok_ok[NT];
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+      const int tok = tok0 + n * 16 + col;
+      tok_ok[n] = tok < a.tokens;
+      xbase[n] = a.xq + (size_t)(tok_ok[n] ? tok : 0) * row_stride_x + 32 * g;
+    }
+    constexpr int U = 4;
+    for (int kc0 = kc_begin; kc0 < kc_end; kc0 += U) {
+      uint4 wv[U], wv2[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int kc = kc0 + u;
+        wv[u] = kc < kc_end ? ld_stream(wp + (size_t)kc * 64u) : make_uint4(0, 0, 0, 0);
+        if (DUAL) wv2[u] = kc < kc_end ? ld_stream(wp2 + (size_t)kc * 64u) : make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int kc = kc0 + u;
+        if (kc >= kc_end) break;
+        v4i a1, a2, c1, c2;
+        unpack16(wv[u], a1, a2);
+        if (DUAL) unpack16(wv2[u], c1, c2);
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+          v4i bh1 = v4i{0, 0, 0, 0}, bh2 = bh1, bl1 = bh1, bl2 = bh1;
+          if (tok_ok[n]) {
+            const v4i* p = reinterpret_cast<const v4i*>(xbase[n] + (size_t)kc * 256u);
+            bh1 = p[0];
+            bh2 = p[1];
+            bl1 = p[8];
+            bl2 = p[9];
+          }
+          accH[n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bh1, accH[n], 0, 0, 0);
+          accH[n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2, bh2, accH[n], 0, 0, 0);
+          accL[n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bl1, accL[n], 0, 0, 0);
+          accL[n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2, bl2, accL[n], 0, 0, 0);
+          if (DUAL) {
+            accH2[n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(c1, bh1, accH2[n], 0, 0, 0);
+            accH2[n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(c2, bh2, accH2[n], 0, 0, 0);
+            accL2[n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(c1, bl1, accL2[n], 0, 0, 0);
+            accL2[n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(c2, bl2, accL2[n], 0, 0, 0);
+          }
+        }
+      }
+    }
+  }
+
+  if (KSPLIT > 1) {
+    // Waves ks = 1..KSPLIT-1 of each row tile hand their partial sums to wave ks = 0 (exact int32).
+    // RTB == 1 whenever KSPLIT > 1, so the block holds one row tile.
+    if (ks > 0) {
+      int* dst = red + ((ks - 1) * NACC) * 64 + lane;
+      int idx = 0;
+#pragma unroll
+      for (int n = 0; n < NT; ++n)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          dst[(idx++) * 64] = accH[n][r];
+          dst[(idx++) * 64] = accL[n][r];
+          if (DUAL) {
+            dst[(idx++) * 64] = accH2[n][r];
+            dst[(idx++) * 64] = accL2[n][r];
+          }
+        }
+    }
+    __syncthreads();
+    if (ks > 0) return;
+#pragma unroll
+    for (int s = 0; s < KSPLIT - 1; ++s) {
+      const int* src = red + (s * NACC) * 64 + lane;
+      int idx = 0;
+#pragma unroll
+      for (int n = 0; n < NT; ++n)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          accH[n][r] += src[(idx++) * 64];
+          accL[n][r] += src[(idx++) * 64];
+          if (DUAL) {
+            accH2[n][r] += src[(idx++) * 64];
+            accL2[n][r] += src[(idx++) * 64];
+          }
+        }
+    }
+  }
+  if (!rt_ok) return;
+
+  // Epilogue: lane holds rows row0..row0+3 of token column `col` of each column tile.
+  const int row0 = rt * 16 + 4 * g;
+  float sw[4], sw2[4], bias[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    sw[r] = a.sw[row0 + r];
+    sw2[r] = DUAL ? a.sw2[row0 + r] : 0.0f;
+    bias[r] = a.bias ? a.bias[row0 + r] : 0.0f;
+  }
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+    const int tok = tok0 + n * 16 + col;
+    if (tok >= a.tokens) continue;
+    const double sx = (double)a.sx[tok];
+    const int sh8 = 8 * a.sums[2 * tok];
+    const int sl8 = 8 * a.sums[2 * tok + 1];
+    float out[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const double tot = (double)(accH[n][r] - sh8) * 256.0 + (double)(accL[n][r] - sl8);
+      const float v = (float)(tot * sx) * sw[r];
+      if (EPI == kEpiSiluMul) {
+        const double tot2 = (double)(accH2[n][r] - sh8) * 256.0 + (double)(accL2[n][r] - sl8);
+        const float u = (float)(tot2 * sx) * sw2[r];
+        const float sg = a.prefill_silu ? silu_prefill(v) : silu_decode(v);
+        out[r] = sg * u;
+      } else if (EPI == kEpiResidual) {
+        const float o = a.resid[(size_t)tok * a.resid_stride + row0 + r] + v;
+        out[r] = o;
+      } else {
+        out[r] = v + bias[r];
+      }
+    }
+    float* yp = a.y + (size_t)tok * a.y_stride + row0;
+    if (EPI == kEpiResidual && a.y_raw) {
+      float* rp = a.y_raw + (size_t)tok * a.y_stride + row0;
+      *reinterpret_cast<float4*>(rp) = make_float4(out[0], out[1], out[2], out[3]);
+    }
+    if (EPI == kEpiResidual && a.round_bf16)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) out[r] = round_bf16(out[r]);
+    *reinterpret_cast<float4*>(yp) = make_float4(out[0], out[1], out[2], out[3]);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// RoPE of q (in place) and k, plus the K/V cache append, for rows of a fused [q | k | v] buffer
+// (qkv_stride floats per token).  Decode: token b is sequence b at position pos[b].  Prefill:
+// token t is sequence t / seq_len at position t % seq_len.  rope: [position][cos 64 | sin 64].
+// Positions outside [0, limit) are skipped (limit = the cache rows the caller sized).
+// grid = tokens, block = 64 (one rotation pair per thread).
+// ---------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(64) rope_qkv_kernel(float* __restrict__ qkv, int qkv_stride,
+                                                      const int* __restrict__ pos, int seq_len, int limit,
+                                                      const float* __restrict__ rope, float* __restrict__ k_cache,
+                                                      float* __restrict__ v_cache, size_t seq_stride) {
+  const int t = blockIdx.x;
+  const int p = threadIdx.x;
+  const int seq = pos ? t : t / seq_len;
+  const int P = pos ? pos[t] : t % seq_len;
+  if (P < 0 || P >= limit) return;  // position outside the cache rows the caller sized
+  const float c = rope[(size_t)P * 128 + p];
+  const float sn = rope[(size_t)P * 128 + 64 + p];
+  float* row = qkv + (size_t)t * qkv_stride;
+#pragma unroll
+  for (int h = 0; h < QWEN_Q_HEADS; ++h) {
+    float* hp = row + h * QWEN_HEAD_DIM;
+    const float e = hp[p], od = hp[p + 64];
+    hp[p] = e * c - od * sn;
+    hp[p + 64] = od * c + e * sn;
+  }
+  const float* kr = row + QWEN_HIDDEN;
+  const float* vr = row + QWEN_HIDDEN + QWEN_KV_WIDTH;
+  float* kc = k_cache + (size_t)seq * seq_stride + (size_t)P * QWEN_KV_WIDTH;
+  float* vc = v_cache + (size_t)seq * seq_stride + (size_t)P * QWEN_KV_WIDTH;
+#pragma unroll
+  for (int h = 0; h < QWEN_KV_HEADS; ++h) {
+    const int base = h * QWEN_HEAD_DIM;
+    const float e = kr[base + p], od = kr[base + p + 64];
+    kc[base + p] = e * c - od * sn;
+    kc[base + p + 64] = od * c + e * sn;
+    vc[base + p] = vr[base + p];
+    vc[base + p + 64] = vr[base + p + 64];
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Decode attention, split over the KV length.  Block (chunk c, KV head kvh, sequence b) handles
+// keys [c*256, min(n, c*256+256)) of sequence b (n = pos[b] + 1) for the 6 query heads of kvh:
+//   m_h = max_t s_ht, l_h = sum_t exp(s_ht - m_h), acc_h = sum_t exp(s_ht - m_h) v_t,
+// with s_ht = (q_h . k_t) * 0.08838834764831845f.  Partials go to part[b][h][c][128] and
+// pml[b][h][c] = (m, l); attn_decode_combine merges the chunks.  block = 256.
+// ---------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) attn_decode_partial_kernel(const float* __restrict__ qkv, int qkv_stride,
+                                                                  const float* __restrict__ k_cache,
+                                                                  const float* __restrict__ v_cache,
+                                                                  size_t seq_stride, const int* __restrict__ pos,
+                                                                  float* __restrict__ part, float2* __restrict__ pml,
+                                                                  int nchunk, int max_keys) {
+  __shared__ __align__(16) float qs[QWEN_GROUPS][QWEN_HEAD_DIM];
+  __shared__ float ps[QWEN_GROUPS][kAttnChunk];
+  __shared__ float red[4][QWEN_GROUPS][QWEN_HEAD_DIM];
+  __shared__ float hm[QWEN_GROUPS], hl[QWEN_GROUPS];
+  const int c = blockIdx.x;
+  const int kvh = blockIdx.y;
+  const int b = blockIdx.z;
+  const int tid = threadIdx.x;
+  const int n = min(max(pos[b], 0) + 1, max_keys);
+  const int t0 = c * kAttnChunk;
+  if (t0 >= n) return;  // the combine step only reads chunks below ceil(n / 256)
+  const int cnt = min(kAttnChunk, n - t0);
+  const float scaling = 0.08838834764831845f;
+  for (int i = tid; i < QWEN_GROUPS * QWEN_HEAD_DIM; i += 256) {
+    const int h = i / QWEN_HEAD_DIM, d = i % QWEN_HEAD_DIM;
+    qs[h][d] = qkv[(size_t)b * qkv_stride + (kvh * QWEN_GROUPS + h) * QWEN_HEAD_DIM + d] * scaling;
+  }
+  __syncthreads();
+  const float* kbase = k_cache + (size_t)b * seq_stride + kvh * QWEN_HEAD_DIM;
+  const float* vbase = v_cache + (size_t)b * seq_stride + kvh * QWEN_HEAD_DIM;
+
+  // scores: thread tid owns key t0 + tid
+  float s[QWEN_GROUPS];
+#pragma unroll
+  for (int h = 0; h < QWEN_GROUPS; ++h) s[h] = 0.0f;
+  if (tid < cnt) {
+    const float4* kr = reinterpret_cast<const float4*>(kbase + (size_t)(t0 + tid) * QWEN_KV_WIDTH);
+#pragma unroll 8
+    for (int d4 = 0; d4 < QWEN_HEAD_DIM / 4; ++d4) {
+      const float4 k4 = ld_stream(kr + d4);
+#pragma unroll
+      for (int h = 0; h < QWEN_GROUPS; ++h) {
+        const float4 q4 = *reinterpret_cast<const float4*>(&qs[h][4 * d4]);
+        s[h] += q4.x * k4.x + q4.y * k4.y + q4.z * k4.z + q4.w * k4.w;
+      }
+    }
+  }
+  float* redf = &red[0][0][0];
+#pragma unroll
+  for (int h = 0; h < QWEN_GROUPS; ++h) {
+    const float m = block_max4(tid < cnt ? s[h] : -INFINITY, redf + 4 * h);
+    const float p = tid < cnt ? __expf(s[h] - m) : 0.0f;
+    ps[h][tid] = p;
+    const float l = block_sum4(p, redf + 32 + 4 * h);
+    if (tid == 0) {
+      hm[h] = m;
+      hl[h] = l;
+    }
+  }
+  __syncthreads();
+
+  // P.V: thread = (key group tg = tid/64, dims 2*lane, 2*lane+1)
+  const int tg = tid >> 6;
+  const int ln = tid & 63;
+  float acc[QWEN_GROUPS][2];
+#pragma unroll
+  for (int h = 0; h < QWEN_GROUPS; ++h) acc[h][0] = acc[h][1] = 0.0f;
+#pragma unroll 4
+  for (int t = tg; t < cnt; t += 4) {
+    const float2 v2 = ld_stream(reinterpret_cast<const float2*>(vbase + (size_t)(t0 + t) * QWEN_KV_WIDTH) + ln);
+#pragma unroll
+    for (int h = 0; h < QWEN_GROUPS; ++h) {
+      const float p = ps[h][t];
+      acc[h][0] += p * v2.x;
+      acc[h][1] += p * v2.y;
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < QWEN_GROUPS; ++h) {
+    red[tg][h][2 * ln] = acc[h][0];
+    red[tg][h][2 * ln + 1] = acc[h][1];
+  }
+  __syncthreads();
+  for (int i = tid; i < QWEN_GROUPS * QWEN_HEAD_DIM; i += 256) {
+    const int h = i / QWEN_HEAD_DIM, d = i % QWEN_HEAD_DIM;
+    const float v = (red[0][h][d] + red[1][h][d]) + (red[2][h][d] + red[3][h][d]);
+    const int qh = kvh * QWEN_GROUPS + h;
+    part[(((size_t)b * QWEN_Q_HEADS + qh) * nchunk + c) * QWEN_HEAD_DIM + d] = v;
+  }
+  if (tid < QWEN_GROUPS) {
+    const int qh = kvh * QWEN_GROUPS + tid;
+    pml[((size_t)b * QWEN_Q_HEADS + qh) * nchunk + c] = make_float2(hm[tid], hl[tid]);
+  }
+}
+
+// Merges the chunk partials of one sequence into ctx[b][1536] = acc / l and quantizes the row for
+// the O projection.  grid = batch, block = 256.
+__global__ void __launch_bounds__(256) attn_decode_combine_kernel(const float* __restrict__ part,
+                                                                  const float2* __restrict__ pml,
+                                                                  const int* __restrict__ pos, int nchunk, int max_keys,
+                                                                  float* __restrict__ ctx, int8_t* __restrict__ xq,
+                                                                  float* __restrict__ sx, int* __restrict__ sums) {
+  __shared__ float row[QWEN_HIDDEN];
+  __shared__ float gm[QWEN_Q_HEADS], ginv[QWEN_Q_HEADS];
+  __shared__ float red_f[4];
+  __shared__ int red_i[4];
+  const int b = blockIdx.x;
+  const int n = min(max(pos[b], 0) + 1, max_keys);
+  const int nc = min((n + kAttnChunk - 1) / kAttnChunk, nchunk);
+  if (threadIdx.x < QWEN_Q_HEADS) {
+    const float2* pm = pml + ((size_t)b * QWEN_Q_HEADS + threadIdx.x) * nchunk;
+    float m = -INFINITY;
+    for (int c = 0; c < nc; ++c) m = fmaxf(m, pm[c].x);
+    float l = 0.0f;
+    for (int c = 0; c < nc; ++c) l += pm[c].y * __expf(pm[c].x - m);
+    gm[threadIdx.x] = m;
+    ginv[threadIdx.x] = l > 0.0f ? 1.0f / l : 0.0f;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < QWEN_HIDDEN; i += 256) {
+    const int h = i / QWEN_HEAD_DIM, d = i % QWEN_HEAD_DIM;
+    const float2* pm = pml + ((size_t)b * QWEN_Q_HEADS + h) * nchunk;
+    const float* pa = part + ((size_t)b * QWEN_Q_HEADS + h) * nchunk * QWEN_HEAD_DIM + d;
+    float acc = 0.0f;
+    for (int c = 0; c < nc; ++c) acc += pa[(size_t)c * QWEN_HEAD_DIM] * __expf(pm[c].x - gm[h]);
+    const float v = acc * ginv[h];
+    row[i] = v;
+    if (ctx) ctx[(size_t)b * QWEN_HIDDEN + i] = v;
+  }
+  __syncthreads();
+  quantize_row_lds(row, QWEN_HIDDEN, xq + (size_t)b * (2 * QWEN_HIDDEN), sx + b, sums + 2 * b, red_f, red_i);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Causal prefill attention (qwen_prefill_attention_kernel.cpp:204-289 semantics, online softmax,
+// approx_exp).  Block (query tile qt of 64 queries, query head h, sequence sq): 4 threads per
+// query, each owning 32 of the 128 dims; K/V tiles of 64 keys are staged in LDS.
+// q rows: qkv + (sq*S + i)*qkv_stride + h*128; K/V rows: cache + sq*seq_stride + j*256 + kvh*128.
+// ctx: [sq*S + i][1536].  grid = (ceil(S/64), 12, nseq), block = 256.
+// ---------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) attn_prefill_kernel(const float* __restrict__ qkv, int qkv_stride,
+                                                           const float* __restrict__ k_cache,
+                                                           const float* __restrict__ v_cache, size_t seq_stride,
+                                                           int S, float* __restrict__ ctx) {
+  __shared__ __align__(16) float ks[64][QWEN_HEAD_DIM + 4];
+  __shared__ __align__(16) float vs[64][QWEN_HEAD_DIM + 4];
+  const int qt = blockIdx.x;
+  const int h = blockIdx.y;
+  const int sq = blockIdx.z;
+  const int kvh = h / QWEN_GROUPS;
+  const int tid = threadIdx.x;
+  const int qi = qt * 64 + (tid >> 2);  // query index within the sequence
+  const int part4 = tid & 3;            // dims [32*part4, 32*part4+32)
+  const bool q_ok = qi < S;
+  const float scaling = 0.08838834764831845f;
+  float q[32], acc[32];
+  {
+    const float* qp = qkv + ((size_t)sq * S + (q_ok ? qi : 0)) * qkv_stride + h * QWEN_HEAD_DIM + 32 * part4;
+#pragma unroll
+    for (int d = 0; d < 32; ++d) {
+      q[d] = q_ok ? qp[d] * scaling : 0.0f;
+      acc[d] = 0.0f;
+    }
+  }
+  float m = -INFINITY, l = 0.0f;
+  const int last_key = min(S, qt * 64 + 64);  // keys this tile can see
+  const float* kb = k_cache + (size_t)sq * seq_stride + kvh * QWEN_HEAD_DIM;
+  const float* vb = v_cache + (size_t)sq * seq_stride + kvh * QWEN_HEAD_DIM;
+  for (int j0 = 0; j0 < last_key; j0 += 64) {
+    __syncthreads();
+    for (int e = tid; e < 64 * 32; e += 256) {
+      const int r = e >> 5, c4 = e & 31;
+      const int j = j0 + r;
+      float4 kv = make_float4(0, 0, 0, 0), vv = kv;
+      if (j < S) {
+        kv = reinterpret_cast<const float4*>(kb + (size_t)j * QWEN_KV_WIDTH)[c4];
+        vv = reinterpret_cast<const float4*>(vb + (size_t)j * QWEN_KV_WIDTH)[c4];
+      }
+      *reinterpret_cast<float4*>(&ks[r][4 * c4]) = kv;
+      *reinterpret_cast<float4*>(&vs[r][4 * c4]) = vv;
+    }
+    __syncthreads();
+    const int jn = min(64, last_key - j0);
+    float s[64];
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int jj = 0; jj < 64; ++jj) {
+      float d0 = 0.0f;
+      if (jj < jn) {
+        const float* kr = &ks[jj][32 * part4];
+#pragma unroll
+        for (int d = 0; d < 32; d += 4) {
+          const float4 k4 = *reinterpret_cast<const float4*>(kr + d);
+          d0 += q[d] * k4.x + q[d + 1] * k4.y + q[d + 2] * k4.z + q[d + 3] * k4.w;
+        }
+      }
+      d0 += __shfl_xor(d0, 1, 64);
+      d0 += __shfl_xor(d0, 2, 64);
+      const bool ok = jj < jn && (j0 + jj) <= qi;
+      s[jj] = ok ? d0 : -INFINITY;
+      tmax = fmaxf(tmax, s[jj]);
+    }
+    if (tmax == -INFINITY) continue;  // every key of this tile is masked for this query
+    const float mnew = fmaxf(m, tmax);
+    const float corr = approx_exp_fast(m - mnew);
+    l *= corr;
+#pragma unroll
+    for (int d = 0; d < 32; ++d) acc[d] *= corr;
+    m = mnew;
+#pragma unroll
+    for (int jj = 0; jj < 64; ++jj) {
+      if (s[jj] == -INFINITY) continue;
+      const float p = approx_exp_fast(s[jj] - m);
+      l += p;
+      const float* vr = &vs[jj][32 * part4];
+#pragma unroll
+      for (int d = 0; d < 32; d += 4) {
+        const float4 v4 = *reinterpret_cast<const float4*>(vr + d);
+        acc[d] += p * v4.x;
+        acc[d + 1] += p * v4.y;
+        acc[d + 2] += p * v4.z;
+        acc[d + 3] += p * v4.w;
+      }
+    }
+  }
+  if (!q_ok) return;
+  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+  float* op = ctx + ((size_t)sq * S + qi) * QWEN_HIDDEN + h * QWEN_HEAD_DIM + 32 * part4;
+#pragma unroll
+  for (int d = 0; d < 32; d += 4)
+    *reinterpret_cast<float4*>(op + d) = make_float4(acc[d] * inv, acc[d + 1] * inv, acc[d + 2] * inv, acc[d + 3] * inv);
+}
+
+// bf16 rounding of the driver between layers (verification/reference_wrapper_backend.py:40-46).
+__global__ void round_bf16_kernel(float* __restrict__ x, size_t n) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) x[i] = round_bf16(x[i]);
+}
+
+// ---------------------------------------------------------------------------------------------
+// host launchers
+// ---------------------------------------------------------------------------------------------
+void launch_repack_int4(const uint8_t* W, int out_dim, int in_dim, uint8_t* WP, hipStream_t st) {
+  hipLaunchKernelGGL(repack_int4_kernel, dim3(out_dim / 16, in_dim / kKChunk), dim3(64), 0, st, W, in_dim, WP);
+}
+
+void launch_norm_quant(const float* x, size_t x_stride, int rows, int n, const float* w, int norm, int8_t* xq,
+                       float* sx, int* sums, float* xn, hipStream_t st) {
+  hipLaunchKernelGGL(norm_quant_kernel, dim3(rows), dim3(256), 0, st, x, x_stride, n, w, norm, xq, sx, sums, xn);
+}
+
+template <int NT, int KSPLIT, int EPI, bool DUAL>
+static void launch_gemm_t(const GemmArgs& a, hipStream_t st) {
+  constexpr int RTB = 4 / KSPLIT;
+  const int row_tiles = a.out_dim / 16;
+  const dim3 grid((a.tokens + 16 * NT - 1) / (16 * NT), (row_tiles + RTB - 1) / RTB);
+  hipLaunchKernelGGL((gemm_i8_kernel<NT, KSPLIT, EPI, DUAL>), grid, dim3(256), 0, st, a);
+}
+
+template <int EPI, bool DUAL>
+static void launch_gemm_epi(const GemmArgs& a, hipStream_t st) {
+  if (a.tokens <= 16) {
+    launch_gemm_t<1, 4, EPI, DUAL>(a, st);
+  } else if (a.tokens <= 64) {
+    launch_gemm_t<1, 4, EPI, DUAL>(a, st);
+  } else {
+    launch_gemm_t<4, 1, EPI, DUAL>(a, st);
+  }
+}
+
+void launch_gemm_i8(const GemmArgs& a, int epi, hipStream_t st) {
+  switch (epi) {
+    case kEpiStore: launch_gemm_epi<kEpiStore, false>(a, st); break;
+    case kEpiSiluMul: launch_gemm_epi<kEpiSiluMul, true>(a, st); break;
+    case kEpiResidual: launch_gemm_epi<kEpiResidual, false>(a, st); break;
+    default: break;
+  }
+}
+
+void launch_rope_qkv(float* qkv, int qkv_stride, const int* pos, int seq_len, int limit, int tokens,
+                     const float* rope, float* k_cache, float* v_cache, size_t seq_stride, hipStream_t st) {
+  hipLaunchKernelGGL(rope_qkv_kernel, dim3(tokens), dim3(64), 0, st, qkv, qkv_stride, pos, seq_len, limit, rope,
+                     k_cache, v_cache, seq_stride);
+}
+
+void launch_attn_decode(const float* qkv, int qkv_stride, const float* k_cache, const float* v_cache,
+                        size_t seq_stride, const int* pos, int batch, int max_keys, float* part, float2* pml,
+                        float* ctx, int8_t* xq, float* sx, int* sums, hipStream_t st) {
+  const int nchunk = (max_keys + kAttnChunk - 1) / kAttnChunk;
+  hipLaunchKernelGGL(attn_decode_partial_kernel, dim3(nchunk, QWEN_KV_HEADS, batch), dim3(256), 0, st, qkv,
+                     qkv_stride, k_cache, v_cache, seq_stride, pos, part, pml, nchunk, max_keys);
+  hipLaunchKernelGGL(attn_decode_combine_kernel, dim3(batch), dim3(256), 0, st, part, pml, pos, nchunk, max_keys, ctx,
+                     xq, sx, sums);
+}
+
+void launch_attn_decode_partial_only(const float* qkv, int qkv_stride, const float* k_cache, const float* v_cache,
+                                     size_t seq_stride, const int* pos, int batch, int max_keys, float* part,
+                                     float2* pml, hipStream_t st) {
+  const int nchunk = (max_keys + kAttnChunk - 1) / kAttnChunk;
+  hipLaunchKernelGGL(attn_decode_partial_kernel, dim3(nchunk, QWEN_KV_HEADS, batch), dim3(256), 0, st, qkv,
+                     qkv_stride, k_cache, v_cache, seq_stride, pos, part, pml, nchunk, max_keys);
+}
+
+void launch_attn_prefill(const float* qkv, int qkv_stride, const float* k_cache, const float* v_cache,
+                         size_t seq_stride, int S, int nseq, float* ctx, hipStream_t st) {
+  hipLaunchKernelGGL(attn_prefill_kernel, dim3((S + 63) / 64, QWEN_Q_HEADS, nseq), dim3(256), 0, st, qkv,
+                     qkv_stride, k_cache, v_cache, seq_stride, S, ctx);
+}
+
+void launch_round_bf16(float* x, size_t n, hipStream_t st) {
+  hipLaunchKernelGGL(round_bf16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, n);
+}
+
+}  // namespace qwen

@@ -155,16 +155,18 @@ __global__ void silu_mul_kernel(const float* __restrict__ g, const float* __rest
 // RoPE + KV append for decode (qwen_decode_attention_kernel.cpp:29-42, 100-111, 206-213).
 // One block of 64 threads per token b: pair p of every Q head and both K heads rotated with the
 // host-computed (cos, sin) row of position pos[b]; K (rotated) and V rows written to row pos[b]
-// of that token's cache.  rope: [positions][2][64] (cos row then sin row).
+// of that token's cache.  rope: [positions][2][64] (cos row then sin row).  Positions outside
+// [0, max_keys) are skipped (max_keys = the cache rows the caller sized).
 // ---------------------------------------------------------------------------------------------
 __global__ void __launch_bounds__(64) rope_append_decode_kernel(float* __restrict__ q, const float* __restrict__ k,
                                                                 const float* __restrict__ v, const int* __restrict__ pos,
                                                                 const float* __restrict__ rope, int rope_rows_are_tokens,
                                                                 float* __restrict__ k_cache, float* __restrict__ v_cache,
-                                                                size_t cache_stride) {
+                                                                size_t cache_stride, int max_keys) {
   const int b = blockIdx.x;
   const int p = threadIdx.x;
   const int P = pos[b];
+  if (P < 0 || P >= max_keys) return;  // position outside the cache rows the caller sized
   const float* cs = rope + (size_t)(rope_rows_are_tokens ? b : P) * 128;
   const float c = cs[p];
   const float sn = cs[64 + p];
@@ -243,11 +245,12 @@ __global__ void rope_table_prefill_kernel(float* __restrict__ rope, int first, i
 // lane 0 adds the denominators serially and lane d adds e*v[d] serially, so every sum keeps the
 // reference order.  The score is recomputed in pass 2 exactly as the reference does.
 // q: [tokens][1536]; cache of token b at k_cache + b*cache_stride (decode) or shared (prefill).
+// Decode key counts are clamped to max_keys (the cache rows the caller sized).
 // ---------------------------------------------------------------------------------------------
 __global__ void __launch_bounds__(128) attention_ordered_kernel(const float* __restrict__ q,
                                                                 const float* __restrict__ k_cache,
                                                                 const float* __restrict__ v_cache, size_t cache_stride,
-                                                                const int* __restrict__ pos, int prefill,
+                                                                const int* __restrict__ pos, int max_keys, int prefill,
                                                                 float* __restrict__ ctx) {
   __shared__ float qs[QWEN_HEAD_DIM];
   __shared__ float es[128];
@@ -257,7 +260,7 @@ __global__ void __launch_bounds__(128) attention_ordered_kernel(const float* __r
   const int b = blockIdx.y;
   const int tid = threadIdx.x;
   const int kvh = h / QWEN_GROUPS;
-  const int n = prefill ? b + 1 : pos[b] + 1;
+  const int n = prefill ? b + 1 : min(max(pos[b], 0) + 1, max_keys);
   // Decode's (float)(1.0/sqrt(128.0)) and prefill's 0.08838834764831845f are the same float
   // (bits 0x3db504f3; checked by tests/test_oracle_math.py).
   const float scaling = 0.08838834764831845f;
@@ -336,9 +339,9 @@ void launch_silu_mul(const float* g, const float* u, float* s, size_t n, bool pr
 
 void launch_rope_append_decode(float* q, const float* k, const float* v, const int* pos, const float* rope,
                                bool rope_rows_are_tokens, float* k_cache, float* v_cache, size_t cache_stride,
-                               int tokens, hipStream_t st) {
+                               int max_keys, int tokens, hipStream_t st) {
   hipLaunchKernelGGL(rope_append_decode_kernel, dim3(tokens), dim3(64), 0, st, q, k, v, pos, rope,
-                     rope_rows_are_tokens ? 1 : 0, k_cache, v_cache, cache_stride);
+                     rope_rows_are_tokens ? 1 : 0, k_cache, v_cache, cache_stride, max_keys);
 }
 
 void launch_rope_prefill(float* q, float* k_rows, const float* rope, int tokens, hipStream_t st) {
@@ -351,9 +354,9 @@ void launch_rope_table_prefill(float* rope, int first, int count, hipStream_t st
 }
 
 void launch_attention_ordered(const float* q, const float* k_cache, const float* v_cache, size_t cache_stride,
-                              const int* pos, int tokens, bool prefill, float* ctx, hipStream_t st) {
+                              const int* pos, int max_keys, int tokens, bool prefill, float* ctx, hipStream_t st) {
   hipLaunchKernelGGL(attention_ordered_kernel, dim3(QWEN_Q_HEADS, tokens), dim3(128), 0, st, q, k_cache, v_cache,
-                     cache_stride, pos, prefill ? 1 : 0, ctx);
+                     cache_stride, pos, max_keys, prefill ? 1 : 0, ctx);
 }
 
 }  // namespace qwen

@@ -1,0 +1,553 @@
+// Device-resident multi-layer model: weights uploaded once, every step queued on one stream.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <exception>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "kernels.hpp"
+#include "qwen_hip_model.h"
+#include "runtime.hpp"
+
+using namespace qwen;
+
+namespace {
+
+// Repacked (FAST) weights and parameter pointers of one layer.  Scales, biases and norm weights
+// point into the uploaded scale image (q/k/v scales and biases are contiguous there, so the
+// fused QKV projection reads them in place).
+struct FastLayer {
+  uint8_t *qkv, *o, *gate, *up, *down;
+  const float *sw_qkv, *b_qkv, *sw_o, *sw_gate, *sw_up, *sw_down, *ln, *post_ln;
+};
+
+constexpr size_t kQkvRows = QWEN_QKV_ROWS;  // 2048
+constexpr size_t kRepackedLayerBytes = QWEN_PACKED_WEIGHT_BYTES;
+
+// Device buffer that only grows (freed after a device synchronize).
+struct DevBuf {
+  void* p = nullptr;
+  size_t cap = 0;
+  void* get(size_t bytes) {
+    if (bytes <= cap) return p;
+    if (p) {
+      QWEN_HIP(hipDeviceSynchronize());
+      QWEN_HIP(hipFree(p));
+      p = nullptr;
+      cap = 0;
+    }
+    const size_t want = bytes + (bytes >> 3) + (1u << 20);
+    QWEN_HIP(hipMalloc(&p, want));
+    cap = want;
+    return p;
+  }
+};
+
+struct LastCall {
+  int kind = 0;  // 0 none, 1 decode, 2 prefill
+  int mode = 0, batch = 0, seq_len = 0, max_keys = 0;
+  const int* positions = nullptr;
+  float *k_cache = nullptr, *v_cache = nullptr;
+  uint64_t seq_stride = 0, layer_stride = 0;
+};
+
+}  // namespace
+
+struct qwen_hip_model {
+  int layers = 0;
+  std::mutex mu;
+  hipStream_t stream = nullptr;
+  uint8_t* raw_w = nullptr;  // layers x QWEN_LAYER_BYTES (weight images)
+  float* raw_s = nullptr;    // layers x QWEN_LAYER_BYTES/4 words (scale images)
+  uint8_t* wp = nullptr;     // layers x repacked weights
+  std::vector<FastLayer> fast;
+  float* rope_decode = nullptr;   // [QWEN_MAX_SEQ][128]
+  float* rope_prefill = nullptr;  // [QWEN_MAX_SEQ][128]
+  uint16_t* embed = nullptr;      // synthetic models: [QWEN_VOCAB][1536] bf16
+  Arena arena;                    // ORDERED per-layer intermediates
+  DevBuf ws;                      // FAST workspace and ORDERED attention output
+  LastCall last;
+
+  // FAST workspace carve-up for `tokens` rows (and `batch` x `nchunk` attention partials).
+  struct Ws {
+    int8_t* xq;
+    float* sx;
+    int* sums;
+    float *qkv, *ctx, *att, *s, *tmp, *part;
+    float2* pml;
+  };
+  Ws carve(size_t tokens, size_t batch, size_t nchunk) {
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+      const size_t o = off;
+      off = (off + bytes + 255u) & ~size_t(255u);
+      return o;
+    };
+    const size_t o_xq = take(xq_bytes(tokens, QWEN_INTERMEDIATE));
+    const size_t o_sx = take(tokens * 4u);
+    const size_t o_sums = take(tokens * 8u);
+    const size_t o_qkv = take(tokens * kQkvRows * 4u);
+    const size_t o_ctx = take(tokens * QWEN_HIDDEN * 4u);
+    const size_t o_att = take(tokens * QWEN_HIDDEN * 4u);
+    const size_t o_s = take(tokens * QWEN_INTERMEDIATE * 4u);
+    const size_t o_tmp = take(tokens * QWEN_INTERMEDIATE * 4u);
+    const size_t o_part = take(batch * QWEN_Q_HEADS * nchunk * QWEN_HEAD_DIM * 4u);
+    const size_t o_pml = take(batch * QWEN_Q_HEADS * nchunk * 8u);
+    char* b = static_cast<char*>(ws.get(off));
+    return Ws{reinterpret_cast<int8_t*>(b + o_xq), reinterpret_cast<float*>(b + o_sx),
+              reinterpret_cast<int*>(b + o_sums), reinterpret_cast<float*>(b + o_qkv),
+              reinterpret_cast<float*>(b + o_ctx), reinterpret_cast<float*>(b + o_att),
+              reinterpret_cast<float*>(b + o_s), reinterpret_cast<float*>(b + o_tmp),
+              reinterpret_cast<float*>(b + o_part), reinterpret_cast<float2*>(b + o_pml)};
+  }
+
+  DevLayer dev_layer(int l) const {
+    const uint8_t* w = raw_w + (size_t)l * QWEN_LAYER_BYTES;
+    const float* s = raw_s + (size_t)l * (QWEN_LAYER_BYTES / 4);
+    DevLayer d;
+    d.ln = s + QWEN_OFF_INPUT_LN / 4;
+    d.post_ln = s + QWEN_OFF_POST_LN / 4;
+    d.qw = w + QWEN_OFF_Q_W;
+    d.kw = w + QWEN_OFF_K_W;
+    d.vw = w + QWEN_OFF_V_W;
+    d.ow = w + QWEN_OFF_O_W;
+    d.gw = w + QWEN_OFF_GATE_W;
+    d.uw = w + QWEN_OFF_UP_W;
+    d.dw = w + QWEN_OFF_DOWN_W;
+    d.qb = s + QWEN_OFF_Q_B / 4;
+    d.kb = s + QWEN_OFF_K_B / 4;
+    d.vb = s + QWEN_OFF_V_B / 4;
+    d.qs = s + QWEN_OFF_Q_S / 4;
+    d.ks = s + QWEN_OFF_K_S / 4;
+    d.vs = s + QWEN_OFF_V_S / 4;
+    d.os = s + QWEN_OFF_O_S / 4;
+    d.gs = s + QWEN_OFF_GATE_S / 4;
+    d.us = s + QWEN_OFF_UP_S / 4;
+    d.ds = s + QWEN_OFF_DOWN_S / 4;
+    return d;
+  }
+
+  // Allocates images, tables and the repacked weights; raw images are filled by the caller.
+  void allocate(int n) {
+    layers = n;
+    QWEN_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
+    QWEN_HIP(hipMalloc(reinterpret_cast<void**>(&raw_w), (size_t)n * QWEN_LAYER_BYTES));
+    QWEN_HIP(hipMalloc(reinterpret_cast<void**>(&raw_s), (size_t)n * QWEN_LAYER_BYTES));
+    QWEN_HIP(hipMalloc(reinterpret_cast<void**>(&wp), (size_t)n * kRepackedLayerBytes));
+    // RoPE tables for every position: decode from host libm (qwen_decode_attention_kernel.cpp:29-42),
+    // prefill on the device (qwen_prefill_attention_kernel.cpp:128-143).
+    std::vector<float> host((size_t)QWEN_MAX_SEQ * 128u);
+    for (int r = 0; r < QWEN_MAX_SEQ; ++r) decode_rope_row_host(r, &host[(size_t)r * 128u]);
+    QWEN_HIP(hipMalloc(reinterpret_cast<void**>(&rope_decode), host.size() * 4u));
+    QWEN_HIP(hipMemcpy(rope_decode, host.data(), host.size() * 4u, hipMemcpyHostToDevice));
+    QWEN_HIP(hipMalloc(reinterpret_cast<void**>(&rope_prefill), host.size() * 4u));
+    launch_rope_table_prefill(rope_prefill, 0, QWEN_MAX_SEQ, stream);
+    QWEN_HIP(hipGetLastError());
+  }
+
+  // Repacks every layer's INT4 matrices from the raw images into the MFMA tile layout.
+  void build_fast() {
+    fast.resize(layers);
+    for (int l = 0; l < layers; ++l) {
+      const DevLayer d = dev_layer(l);
+      uint8_t* base = wp + (size_t)l * kRepackedLayerBytes;
+      FastLayer& f = fast[l];
+      f.qkv = base;
+      f.o = f.qkv + kQkvRows * QWEN_HIDDEN / 2;
+      f.gate = f.o + (size_t)QWEN_HIDDEN * QWEN_HIDDEN / 2;
+      f.up = f.gate + (size_t)QWEN_INTERMEDIATE * QWEN_HIDDEN / 2;
+      f.down = f.up + (size_t)QWEN_INTERMEDIATE * QWEN_HIDDEN / 2;
+      // q, k and v rows are contiguous in the layer image, so one repack covers all 2048 rows.
+      launch_repack_int4(d.qw, (int)kQkvRows, QWEN_HIDDEN, f.qkv, stream);
+      launch_repack_int4(d.ow, QWEN_HIDDEN, QWEN_HIDDEN, f.o, stream);
+      launch_repack_int4(d.gw, QWEN_INTERMEDIATE, QWEN_HIDDEN, f.gate, stream);
+      launch_repack_int4(d.uw, QWEN_INTERMEDIATE, QWEN_HIDDEN, f.up, stream);
+      launch_repack_int4(d.dw, QWEN_HIDDEN, QWEN_INTERMEDIATE, f.down, stream);
+      f.sw_qkv = d.qs;  // q_s, k_s, v_s contiguous
+      f.b_qkv = d.qb;   // q_b, k_b, v_b contiguous
+      f.sw_o = d.os;
+      f.sw_gate = d.gs;
+      f.sw_up = d.us;
+      f.sw_down = d.ds;
+      f.ln = d.ln;
+      f.post_ln = d.post_ln;
+    }
+    QWEN_HIP(hipGetLastError());
+    QWEN_HIP(hipStreamSynchronize(stream));
+  }
+
+  ~qwen_hip_model() {
+    if (stream) (void)hipStreamSynchronize(stream);
+    for (void* p : {static_cast<void*>(raw_w), static_cast<void*>(raw_s), static_cast<void*>(wp),
+                    static_cast<void*>(rope_decode), static_cast<void*>(rope_prefill), static_cast<void*>(embed),
+                    ws.p})
+      if (p) (void)hipFree(p);
+    if (stream) (void)hipStreamDestroy(stream);
+  }
+
+  // ---- one step -------------------------------------------------------------------------
+  void gemm(const Ws& w, int tokens, int in, int out, const uint8_t* wpm, const float* sw, const float* bias,
+            float* y, size_t ys, int epi, const uint8_t* wp2 = nullptr, const float* sw2 = nullptr,
+            const float* resid = nullptr, int round = 0, int prefill_silu = 0) {
+    GemmArgs g{};
+    g.wp = wpm;
+    g.wp2 = wp2;
+    g.sw = sw;
+    g.sw2 = sw2;
+    g.bias = bias;
+    g.xq = w.xq;
+    g.sx = w.sx;
+    g.sums = w.sums;
+    g.tokens = tokens;
+    g.in_dim = in;
+    g.out_dim = out;
+    g.y = y;
+    g.y_stride = ys;
+    g.resid = resid;
+    g.resid_stride = QWEN_HIDDEN;
+    g.y_raw = nullptr;
+    g.round_bf16 = round;
+    g.prefill_silu = prefill_silu;
+    launch_gemm_i8(g, epi, stream);
+  }
+
+  void decode_fast(int B, float* hidden, const int* pos, int max_keys, float* kc0, float* vc0, uint64_t ss,
+                   uint64_t ls, int round) {
+    const int nchunk = (max_keys + kAttnChunk - 1) / kAttnChunk;
+    const Ws w = carve(B, B, nchunk);
+    for (int l = 0; l < layers; ++l) {
+      const FastLayer& f = fast[l];
+      float* kc = kc0 + (size_t)l * ls;
+      float* vc = vc0 + (size_t)l * ls;
+      launch_norm_quant(hidden, QWEN_HIDDEN, B, QWEN_HIDDEN, f.ln, kNormDecode, w.xq, w.sx, w.sums, nullptr, stream);
+      gemm(w, B, QWEN_HIDDEN, (int)kQkvRows, f.qkv, f.sw_qkv, f.b_qkv, w.qkv, kQkvRows, kEpiStore);
+      launch_rope_qkv(w.qkv, (int)kQkvRows, pos, 1, max_keys, B, rope_decode, kc, vc, ss, stream);
+      launch_attn_decode(w.qkv, (int)kQkvRows, kc, vc, ss, pos, B, max_keys, w.part, w.pml, w.ctx, w.xq, w.sx,
+                         w.sums, stream);
+      gemm(w, B, QWEN_HIDDEN, QWEN_HIDDEN, f.o, f.sw_o, nullptr, w.att, QWEN_HIDDEN, kEpiStore);
+      launch_norm_quant(w.att, QWEN_HIDDEN, B, QWEN_HIDDEN, f.post_ln, kNormDecode, w.xq, w.sx, w.sums, nullptr,
+                        stream);
+      gemm(w, B, QWEN_HIDDEN, QWEN_INTERMEDIATE, f.gate, f.sw_gate, nullptr, w.s, QWEN_INTERMEDIATE, kEpiSiluMul,
+           f.up, f.sw_up, nullptr, 0, 0);
+      launch_norm_quant(w.s, QWEN_INTERMEDIATE, B, QWEN_INTERMEDIATE, nullptr, kNormNone, w.xq, w.sx, w.sums,
+                        nullptr, stream);
+      gemm(w, B, QWEN_INTERMEDIATE, QWEN_HIDDEN, f.down, f.sw_down, nullptr, hidden, QWEN_HIDDEN, kEpiResidual,
+           nullptr, nullptr, w.att, round, 0);
+    }
+    QWEN_HIP(hipGetLastError());
+  }
+
+  void prefill_fast(int B, int S, float* hidden, float* kc0, float* vc0, uint64_t ss, uint64_t ls, int round) {
+    const int T = B * S;
+    const Ws w = carve(T, 1, 1);
+    for (int l = 0; l < layers; ++l) {
+      const FastLayer& f = fast[l];
+      float* kc = kc0 + (size_t)l * ls;
+      float* vc = vc0 + (size_t)l * ls;
+      launch_norm_quant(hidden, QWEN_HIDDEN, T, QWEN_HIDDEN, f.ln, kNormPrefill, w.xq, w.sx, w.sums, nullptr,
+                        stream);
+      gemm(w, T, QWEN_HIDDEN, (int)kQkvRows, f.qkv, f.sw_qkv, f.b_qkv, w.qkv, kQkvRows, kEpiStore);
+      launch_rope_qkv(w.qkv, (int)kQkvRows, nullptr, S, S, T, rope_prefill, kc, vc, ss, stream);
+      launch_attn_prefill(w.qkv, (int)kQkvRows, kc, vc, ss, S, B, w.ctx, stream);
+      launch_norm_quant(w.ctx, QWEN_HIDDEN, T, QWEN_HIDDEN, nullptr, kNormNone, w.xq, w.sx, w.sums, nullptr, stream);
+      gemm(w, T, QWEN_HIDDEN, QWEN_HIDDEN, f.o, f.sw_o, nullptr, w.att, QWEN_HIDDEN, kEpiStore);
+      launch_norm_quant(w.att, QWEN_HIDDEN, T, QWEN_HIDDEN, f.post_ln, kNormPrefill, w.xq, w.sx, w.sums, nullptr,
+                        stream);
+      gemm(w, T, QWEN_HIDDEN, QWEN_INTERMEDIATE, f.gate, f.sw_gate, nullptr, w.s, QWEN_INTERMEDIATE, kEpiSiluMul,
+           f.up, f.sw_up, nullptr, 0, 1);
+      launch_norm_quant(w.s, QWEN_INTERMEDIATE, T, QWEN_INTERMEDIATE, nullptr, kNormNone, w.xq, w.sx, w.sums,
+                        nullptr, stream);
+      gemm(w, T, QWEN_INTERMEDIATE, QWEN_HIDDEN, f.down, f.sw_down, nullptr, hidden, QWEN_HIDDEN, kEpiResidual,
+           nullptr, nullptr, w.att, round, 0);
+    }
+    QWEN_HIP(hipGetLastError());
+  }
+
+  void decode_ordered(int B, float* hidden, const int* pos, int max_keys, float* kc0, float* vc0, uint64_t ss,
+                      uint64_t ls, int round) {
+    float* att = static_cast<float*>(ws.get((size_t)B * QWEN_HIDDEN * 4u));
+    for (int l = 0; l < layers; ++l) {
+      const DevLayer d = dev_layer(l);
+      arena.reset();
+      arena.reserve(decode_workspace_bytes(B));
+      DecodeBatch b{B, pos, rope_decode, false, kc0 + (size_t)l * ls, vc0 + (size_t)l * ls, (size_t)ss, max_keys};
+      run_decode_attention(d, hidden, b, att, arena, Mode::Ordered, stream);
+      run_decode_mlp(d, att, B, hidden, arena, Mode::Ordered, stream);
+      if (round) launch_round_bf16(hidden, (size_t)B * QWEN_HIDDEN, stream);
+    }
+    arena.reset();
+    QWEN_HIP(hipGetLastError());
+  }
+
+  void prefill_ordered(int B, int S, float* hidden, float* kc0, float* vc0, uint64_t ss, uint64_t ls, int round) {
+    float* att = static_cast<float*>(ws.get((size_t)S * QWEN_HIDDEN * 4u));
+    for (int l = 0; l < layers; ++l) {
+      const DevLayer d = dev_layer(l);
+      for (int b = 0; b < B; ++b) {
+        float* x = hidden + (size_t)b * S * QWEN_HIDDEN;
+        arena.reset();
+        arena.reserve(prefill_workspace_bytes(S));
+        run_prefill_attention(d, x, S, rope_prefill, kc0 + (size_t)l * ls + (size_t)b * ss,
+                              vc0 + (size_t)l * ls + (size_t)b * ss, att, arena, Mode::Ordered, stream);
+        run_prefill_mlp(d, att, S, x, arena, Mode::Ordered, stream);
+      }
+      if (round) launch_round_bf16(hidden, (size_t)B * S * QWEN_HIDDEN, stream);
+    }
+    arena.reset();
+    QWEN_HIP(hipGetLastError());
+  }
+};
+
+namespace {
+
+template <class Fn>
+int guarded_model(Fn&& fn) {
+  try {
+    return fn();
+  } catch (const HipError& e) {
+    set_last_error(std::string(e.what) + ": " + hipGetErrorString(e.code));
+  } catch (const std::exception& e) {
+    set_last_error(e.what());
+  }
+  if (std::getenv("QWEN_HIP_VERBOSE")) std::fprintf(stderr, "qwen-mi355x: %s\n", last_error_cstr());
+  return QWEN_ERR_DEVICE;
+}
+
+int invalid(const char* why) {
+  set_last_error(why);
+  return QWEN_ERR_KERNEL;
+}
+
+// Tensor keys of the synthetic generator: 16 per layer, then the embedding table.
+enum : uint64_t { kTQ = 0, kTK, kTV, kTO, kTGate, kTUp, kTDown, kTQb, kTKb, kTVb };
+constexpr uint64_t kEmbedKey = 1u << 20;
+
+}  // namespace
+
+extern "C" {
+
+int qwen_hip_model_create(int layers, const uint8_t* weight_ddr, const float* scale_ddr, qwen_hip_model** out) {
+  if (!out || !weight_ddr || !scale_ddr || layers <= 0 || layers > 1024) return invalid("invalid model arguments");
+  *out = nullptr;
+  return guarded_model([&]() -> int {
+    qwen_hip_model* m = new qwen_hip_model();
+    try {
+      m->allocate(layers);
+      QWEN_HIP(hipMemcpy(m->raw_w, weight_ddr, (size_t)layers * QWEN_LAYER_BYTES, hipMemcpyHostToDevice));
+      QWEN_HIP(hipMemcpy(m->raw_s, scale_ddr, (size_t)layers * QWEN_LAYER_BYTES, hipMemcpyHostToDevice));
+      m->build_fast();
+    } catch (...) {
+      delete m;
+      throw;
+    }
+    *out = m;
+    return QWEN_OK;
+  });
+}
+
+int qwen_hip_model_create_synthetic(int layers, uint64_t seed, qwen_hip_model** out) {
+  if (!out || layers <= 0 || layers > 1024) return invalid("invalid model arguments");
+  *out = nullptr;
+  return guarded_model([&]() -> int {
+    qwen_hip_model* m = new qwen_hip_model();
+    try {
+      m->allocate(layers);
+      const hipStream_t st = m->stream;
+      QWEN_HIP(hipMemsetAsync(m->raw_w, 0, (size_t)layers * QWEN_LAYER_BYTES, st));
+      QWEN_HIP(hipMemsetAsync(m->raw_s, 0, (size_t)layers * QWEN_LAYER_BYTES, st));
+      struct Mat {
+        uint64_t key;
+        uint64_t w_off, s_off;
+        int out, in;
+      };
+      const Mat mats[] = {{kTQ, QWEN_OFF_Q_W, QWEN_OFF_Q_S, QWEN_HIDDEN, QWEN_HIDDEN},
+                          {kTK, QWEN_OFF_K_W, QWEN_OFF_K_S, QWEN_KV_WIDTH, QWEN_HIDDEN},
+                          {kTV, QWEN_OFF_V_W, QWEN_OFF_V_S, QWEN_KV_WIDTH, QWEN_HIDDEN},
+                          {kTO, QWEN_OFF_O_W, QWEN_OFF_O_S, QWEN_HIDDEN, QWEN_HIDDEN},
+                          {kTGate, QWEN_OFF_GATE_W, QWEN_OFF_GATE_S, QWEN_INTERMEDIATE, QWEN_HIDDEN},
+                          {kTUp, QWEN_OFF_UP_W, QWEN_OFF_UP_S, QWEN_INTERMEDIATE, QWEN_HIDDEN},
+                          {kTDown, QWEN_OFF_DOWN_W, QWEN_OFF_DOWN_S, QWEN_HIDDEN, QWEN_INTERMEDIATE}};
+      for (int l = 0; l < layers; ++l) {
+        uint8_t* w = m->raw_w + (size_t)l * QWEN_LAYER_BYTES;
+        float* s = m->raw_s + (size_t)l * (QWEN_LAYER_BYTES / 4);
+        for (const Mat& mt : mats)
+          launch_quantize_rows(nullptr, mt.out, mt.in, synth_stream_host(seed, (uint64_t)l * 16u + mt.key), 0.02f,
+                               w + mt.w_off, s + mt.s_off / 4, st);
+        launch_fill_vector(s + QWEN_OFF_Q_B / 4, QWEN_HIDDEN, synth_stream_host(seed, (uint64_t)l * 16u + kTQb),
+                           0.02f, 1, 0.0f, st);
+        launch_fill_vector(s + QWEN_OFF_K_B / 4, QWEN_KV_WIDTH, synth_stream_host(seed, (uint64_t)l * 16u + kTKb),
+                           0.02f, 1, 0.0f, st);
+        launch_fill_vector(s + QWEN_OFF_V_B / 4, QWEN_KV_WIDTH, synth_stream_host(seed, (uint64_t)l * 16u + kTVb),
+                           0.02f, 1, 0.0f, st);
+        launch_fill_vector(s + QWEN_OFF_INPUT_LN / 4, QWEN_HIDDEN, 0, 0.0f, 0, 1.0f, st);
+        launch_fill_vector(s + QWEN_OFF_POST_LN / 4, QWEN_HIDDEN, 0, 0.0f, 0, 1.0f, st);
+      }
+      const size_t table = (size_t)QWEN_VOCAB * QWEN_HIDDEN;
+      QWEN_HIP(hipMalloc(reinterpret_cast<void**>(&m->embed), table * 2u));
+      launch_fill_bf16_table(m->embed, table, synth_stream_host(seed, kEmbedKey), 0.02f, st);
+      QWEN_HIP(hipGetLastError());
+      m->build_fast();
+    } catch (...) {
+      delete m;
+      throw;
+    }
+    *out = m;
+    return QWEN_OK;
+  });
+}
+
+int qwen_hip_model_destroy(qwen_hip_model* m) {
+  delete m;
+  return QWEN_OK;
+}
+
+int qwen_hip_model_layers(const qwen_hip_model* m) { return m ? m->layers : 0; }
+
+void* qwen_hip_model_stream(qwen_hip_model* m) { return m ? static_cast<void*>(m->stream) : nullptr; }
+
+int qwen_hip_model_synchronize(qwen_hip_model* m) {
+  if (!m) return invalid("null model");
+  return guarded_model([&]() -> int {
+    QWEN_HIP(hipStreamSynchronize(m->stream));
+    return QWEN_OK;
+  });
+}
+
+int qwen_hip_model_decode(qwen_hip_model* m, int mode, int batch, float* hidden, const int* positions, int max_keys,
+                          float* k_cache, float* v_cache, uint64_t seq_stride, uint64_t layer_stride) {
+  if (!m || !hidden || !positions || !k_cache || !v_cache) return invalid("null argument");
+  const int round = (mode & QWEN_FLAG_NO_BF16_ROUND) ? 0 : 1;
+  mode &= ~QWEN_FLAG_NO_BF16_ROUND;
+  if (batch <= 0 || max_keys <= 0 || max_keys > QWEN_MAX_SEQ || (mode != QWEN_MODE_ORDERED && mode != QWEN_MODE_FAST))
+    return invalid("invalid decode shape or mode");
+  if (seq_stride < (uint64_t)max_keys * QWEN_KV_WIDTH || (batch > 1 && layer_stride < (uint64_t)batch * seq_stride) ||
+      (m->layers > 1 && layer_stride == 0))
+    return invalid("KV strides too small for max_keys / batch");
+  std::lock_guard<std::mutex> lock(m->mu);
+  return guarded_model([&]() -> int {
+    if (mode == QWEN_MODE_FAST)
+      m->decode_fast(batch, hidden, positions, max_keys, k_cache, v_cache, seq_stride, layer_stride, round);
+    else
+      m->decode_ordered(batch, hidden, positions, max_keys, k_cache, v_cache, seq_stride, layer_stride, round);
+    m->last = LastCall{1, mode, batch, 1, max_keys, positions, k_cache, v_cache, seq_stride, layer_stride};
+    return QWEN_OK;
+  });
+}
+
+int qwen_hip_model_prefill(qwen_hip_model* m, int mode, int batch, int seq_len, float* hidden, float* k_cache,
+                           float* v_cache, uint64_t seq_stride, uint64_t layer_stride) {
+  if (!m || !hidden || !k_cache || !v_cache) return invalid("null argument");
+  const int round = (mode & QWEN_FLAG_NO_BF16_ROUND) ? 0 : 1;
+  mode &= ~QWEN_FLAG_NO_BF16_ROUND;
+  if (batch <= 0 || seq_len <= 0 || seq_len > QWEN_MAX_SEQ || (mode != QWEN_MODE_ORDERED && mode != QWEN_MODE_FAST))
+    return invalid("invalid prefill shape or mode");
+  if (seq_stride < (uint64_t)seq_len * QWEN_KV_WIDTH || (batch > 1 && layer_stride < (uint64_t)batch * seq_stride) ||
+      (m->layers > 1 && layer_stride == 0))
+    return invalid("KV strides too small for seq_len / batch");
+  std::lock_guard<std::mutex> lock(m->mu);
+  return guarded_model([&]() -> int {
+    if (mode == QWEN_MODE_FAST)
+      m->prefill_fast(batch, seq_len, hidden, k_cache, v_cache, seq_stride, layer_stride, round);
+    else
+      m->prefill_ordered(batch, seq_len, hidden, k_cache, v_cache, seq_stride, layer_stride, round);
+    m->last = LastCall{2, mode, batch, seq_len, seq_len, nullptr, k_cache, v_cache, seq_stride, layer_stride};
+    return QWEN_OK;
+  });
+}
+
+int qwen_hip_model_embed(qwen_hip_model* m, const int* token_ids, int count, float* hidden) {
+  if (!m || !token_ids || !hidden || count <= 0) return invalid("invalid embed arguments");
+  if (!m->embed) return invalid("model has no embedding table (only synthetic models carry one)");
+  std::lock_guard<std::mutex> lock(m->mu);
+  return guarded_model([&]() -> int {
+    launch_embed(m->embed, token_ids, count, hidden, m->stream);
+    QWEN_HIP(hipGetLastError());
+    return QWEN_OK;
+  });
+}
+
+int qwen_hip_model_time_kernel(qwen_hip_model* m, int kernel, int layer, int reps, float* avg_ms) {
+  if (!m || !avg_ms || reps <= 0 || layer < 0 || layer >= m->layers) return invalid("invalid timing arguments");
+  std::lock_guard<std::mutex> lock(m->mu);
+  const LastCall c = m->last;
+  if (c.kind == 0 || c.mode != QWEN_MODE_FAST) return invalid("time_kernel needs a preceding FAST decode/prefill");
+  const bool decode = c.kind == 1;
+  if ((kernel == QWEN_KERNEL_ATTN_DECODE && !decode) || (kernel == QWEN_KERNEL_ATTN_PREFILL && decode))
+    return invalid("kernel does not belong to the last call");
+  return guarded_model([&]() -> int {
+    const int T = c.batch * c.seq_len;
+    const int nchunk = (c.max_keys + kAttnChunk - 1) / kAttnChunk;
+    const qwen_hip_model::Ws w = m->carve(T, decode ? c.batch : 1, decode ? nchunk : 1);
+    const FastLayer& f = m->fast[layer];
+    float* kc = c.k_cache + (size_t)layer * c.layer_stride;
+    float* vc = c.v_cache + (size_t)layer * c.layer_stride;
+    auto once = [&]() {
+      switch (kernel) {
+        case QWEN_KERNEL_ATTN_DECODE:
+          launch_attn_decode_partial_only(w.qkv, (int)kQkvRows, kc, vc, c.seq_stride, c.positions, c.batch,
+                                          c.max_keys, w.part, w.pml, m->stream);
+          break;
+        case QWEN_KERNEL_GEMM_GATE_UP:
+          m->gemm(w, T, QWEN_HIDDEN, QWEN_INTERMEDIATE, f.gate, f.sw_gate, nullptr, w.tmp, QWEN_INTERMEDIATE,
+                  kEpiSiluMul, f.up, f.sw_up, nullptr, 0, decode ? 0 : 1);
+          break;
+        case QWEN_KERNEL_GEMM_DOWN:
+          m->gemm(w, T, QWEN_INTERMEDIATE, QWEN_HIDDEN, f.down, f.sw_down, nullptr, w.tmp, QWEN_HIDDEN, kEpiResidual,
+                  nullptr, nullptr, w.att, 1, 0);
+          break;
+        case QWEN_KERNEL_GEMM_QKV:
+          m->gemm(w, T, QWEN_HIDDEN, (int)kQkvRows, f.qkv, f.sw_qkv, f.b_qkv, w.tmp, kQkvRows, kEpiStore);
+          break;
+        case QWEN_KERNEL_GEMM_O:
+          m->gemm(w, T, QWEN_HIDDEN, QWEN_HIDDEN, f.o, f.sw_o, nullptr, w.tmp, QWEN_HIDDEN, kEpiStore);
+          break;
+        case QWEN_KERNEL_ATTN_PREFILL:
+          launch_attn_prefill(w.qkv, (int)kQkvRows, kc, vc, c.seq_stride, c.seq_len, c.batch, w.ctx, m->stream);
+          break;
+        default:
+          throw std::runtime_error("unknown kernel id");
+      }
+    };
+    once();  // warm
+    hipEvent_t e0, e1;
+    QWEN_HIP(hipEventCreate(&e0));
+    QWEN_HIP(hipEventCreate(&e1));
+    QWEN_HIP(hipEventRecord(e0, m->stream));
+    for (int i = 0; i < reps; ++i) once();
+    QWEN_HIP(hipEventRecord(e1, m->stream));
+    QWEN_HIP(hipEventSynchronize(e1));
+    float ms = 0.0f;
+    QWEN_HIP(hipEventElapsedTime(&ms, e0, e1));
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    QWEN_HIP(hipGetLastError());
+    *avg_ms = ms / (float)reps;
+    return QWEN_OK;
+  });
+}
+
+int qwen_hip_quantize_int4(const float* w, int out_dim, int in_dim, uint8_t* packed, float* scales, void* stream) {
+  if (!w || !packed || !scales || out_dim <= 0 || in_dim <= 0 || in_dim % 2 || in_dim > kMaxQuantRow)
+    return invalid("invalid quantizer arguments (in_dim must be even and <= 8960)");
+  return guarded_model([&]() -> int {
+    launch_quantize_rows(w, out_dim, in_dim, 0, 0.0f, packed, scales, static_cast<hipStream_t>(stream));
+    QWEN_HIP(hipGetLastError());
+    return QWEN_OK;
+  });
+}
+
+int qwen_hip_fill_kv_synthetic(float* cache, uint64_t rows, uint64_t seed, void* stream) {
+  if (!cache) return invalid("null cache");
+  if (rows == 0) return QWEN_OK;
+  return guarded_model([&]() -> int {
+    launch_kv_synthetic(cache, rows, synth_stream_host(seed, 1u << 21), static_cast<hipStream_t>(stream));
+    QWEN_HIP(hipGetLastError());
+    return QWEN_OK;
+  });
+}
+
+}  // extern "C"

@@ -123,6 +123,22 @@ QWEN_HD float approx_exp(float v) {  // :87-110; `term *= s / deg` divides first
   return series > 0.0f ? series : 0.0f;
 }
 
+// approx_exp evaluated in Horner form with reciprocal constants (no divisions): the same
+// halving ladder and degree-6 series, within a few ulp of approx_exp.  FAST kernels only.
+QWEN_HD float approx_exp_fast(float v) {
+  if (v <= -16.0f) return 0.0f;
+  int halves = 0;
+  float s = v;
+  while (s < -1.0f) {
+    s *= 0.5f;
+    ++halves;
+  }
+  float r = 1.0f + s * (1.0f + s * (0.5f + s * (1.0f / 6.0f + s * (1.0f / 24.0f + s * (1.0f / 120.0f +
+                                                                                        s * (1.0f / 720.0f))))));
+  for (int k = 0; k < halves; ++k) r *= r;
+  return r > 0.0f ? r : 0.0f;
+}
+
 __device__ __forceinline__ float silu_decode(float v) { return v / (1.0f + glibc_expf(-v)); }  // mlp :79-81
 QWEN_HD float silu_prefill(float v) { return v / (1.0f + approx_exp(-v)); }                   // mlp :256-258
 

@@ -17,6 +17,12 @@ Mode mode_from_env() {
   return Mode::Ordered;
 }
 
+namespace {
+thread_local std::string g_last_error;
+}
+void set_last_error(const std::string& msg) { g_last_error = msg; }
+const char* last_error_cstr() { return g_last_error.c_str(); }
+
 void hip_check(hipError_t e, const char* what) {
   if (e != hipSuccess) throw HipError{e, what};
 }
@@ -174,8 +180,9 @@ void run_decode_attention(const DevLayer& L, const float* x, const DecodeBatch& 
   launch_project_ordered(xn, T, QWEN_HIDDEN, L.qw, L.qs, L.qb, QWEN_HIDDEN, q, nullptr, st);
   launch_project_ordered(xn, T, QWEN_HIDDEN, L.kw, L.ks, L.kb, QWEN_KV_WIDTH, k, nullptr, st);
   launch_project_ordered(xn, T, QWEN_HIDDEN, L.vw, L.vs, L.vb, QWEN_KV_WIDTH, v, nullptr, st);
-  launch_rope_append_decode(q, k, v, b.pos, b.rope, b.rope_per_token, b.k_cache, b.v_cache, b.cache_stride, T, st);
-  launch_attention_ordered(q, b.k_cache, b.v_cache, b.cache_stride, b.pos, T, false, ctx, st);
+  launch_rope_append_decode(q, k, v, b.pos, b.rope, b.rope_per_token, b.k_cache, b.v_cache, b.cache_stride,
+                            b.max_keys, T, st);
+  launch_attention_ordered(q, b.k_cache, b.v_cache, b.cache_stride, b.pos, b.max_keys, T, false, ctx, st);
   launch_project_ordered(ctx, T, QWEN_HIDDEN, L.ow, L.os, nullptr, QWEN_HIDDEN, att, nullptr, st);
   QWEN_HIP(hipGetLastError());
 }
@@ -205,7 +212,7 @@ void run_prefill_attention(const DevLayer& L, const float* x, int T, const float
   launch_project_ordered(xn, T, QWEN_HIDDEN, L.vw, L.vs, L.vb, QWEN_KV_WIDTH, v_rows, nullptr, st);
   launch_project_ordered(xn, T, QWEN_HIDDEN, L.qw, L.qs, L.qb, QWEN_HIDDEN, q, nullptr, st);
   launch_rope_prefill(q, k_rows, rope, T, st);
-  launch_attention_ordered(q, k_rows, v_rows, 0, nullptr, T, true, ctx, st);
+  launch_attention_ordered(q, k_rows, v_rows, 0, nullptr, T, T, true, ctx, st);
   launch_project_ordered(ctx, T, QWEN_HIDDEN, L.ow, L.os, nullptr, QWEN_HIDDEN, att, nullptr, st);
   QWEN_HIP(hipGetLastError());
 }

@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include <mutex>
+#include <string>
 #include <vector>
 
 #include "qwen_layout.h"
@@ -21,6 +22,10 @@ struct HipError {
   hipError_t code;
   const char* what;
 };
+
+// Message of the last failure on the calling thread (qwen_hip_last_error).
+void set_last_error(const std::string& msg);
+const char* last_error_cstr();
 
 // Throws HipError on failure; the C-ABI boundary turns it into status QWEN_ERR_DEVICE.
 void hip_check(hipError_t e, const char* what);
@@ -113,6 +118,7 @@ struct DecodeBatch {
   float* k_cache;          // device; sequence b at k_cache + b*cache_stride
   float* v_cache;
   size_t cache_stride;     // floats between sequences
+  int max_keys;            // cache rows per sequence the caller sized (key counts are clamped to it)
 };
 
 // Arena bytes the executors below need for `tokens` tokens.

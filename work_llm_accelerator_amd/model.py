@@ -1,0 +1,172 @@
+"""Device-resident multi-layer model (include/qwen_hip_model.h) driven from Python.
+
+This is the host side of the 28-layer drivers of the reference
+(verification/real_host_top_backend.py:208-351: per-layer DDR images, layer loop, bf16 rounding
+between layers) on top of the HIP library's device-resident API.  torch is used only to own
+device memory and to wrap the model's HIP stream; every layer runs in the HIP library.  There is
+no CPU fallback: without the built library or a GPU the constructor raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import abi
+from .layout import HIDDEN, KV_WIDTH, LAYOUT
+
+MODE_ORDERED = 0
+MODE_FAST = 1
+FLAG_NO_BF16_ROUND = 0x100  # skip the driver's bf16 rounding between layers
+
+KERNEL_ATTN_DECODE = 1
+KERNEL_GEMM_GATE_UP = 2
+KERNEL_GEMM_DOWN = 3
+KERNEL_GEMM_QKV = 4
+KERNEL_GEMM_O = 5
+KERNEL_ATTN_PREFILL = 6
+
+
+def _ptr(t) -> ctypes.c_void_p:
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _check(lib, status: int, what: str) -> None:
+    if status != 0:
+        raise RuntimeError(f"{what} failed with status {status}: {abi.last_error(lib)}")
+
+
+@dataclass
+class KvCache:
+    """Token-major fp32 K and V caches, [layers][sequences][positions][256] each."""
+
+    k: "object"  # torch.Tensor on the GPU
+    v: "object"
+    layers: int
+    sequences: int
+    positions: int
+
+    @property
+    def seq_stride(self) -> int:
+        return self.positions * KV_WIDTH
+
+    @property
+    def layer_stride(self) -> int:
+        return self.sequences * self.seq_stride
+
+    @classmethod
+    def allocate(cls, layers: int, sequences: int, positions: int, device="cuda:0"):
+        import torch
+
+        shape = (layers, sequences, positions, KV_WIDTH)
+        return cls(torch.zeros(shape, dtype=torch.float32, device=device),
+                   torch.zeros(shape, dtype=torch.float32, device=device), layers, sequences, positions)
+
+
+class DeviceModel:
+    """A stack of quantized decoder layers resident in HBM."""
+
+    def __init__(self, layers: int, weight_ddr: np.ndarray | None = None, scale_ddr: np.ndarray | None = None,
+                 synthetic_seed: int | None = None):
+        import torch
+
+        if not torch.cuda.is_available():
+            raise RuntimeError("DeviceModel needs a GPU (the HIP path has no CPU fallback)")
+        self.lib = abi.load()
+        handle = ctypes.c_void_p()
+        if synthetic_seed is not None:
+            st = self.lib.qwen_hip_model_create_synthetic(layers, synthetic_seed, ctypes.byref(handle))
+        else:
+            if weight_ddr is None or scale_ddr is None:
+                raise ValueError("weight_ddr and scale_ddr are required unless synthetic_seed is given")
+            if weight_ddr.size != layers * LAYOUT.total_parameter_bytes or scale_ddr.size * 4 != weight_ddr.size:
+                raise ValueError("images must hold `layers` blocks of QWEN_LAYER_BYTES each")
+            st = self.lib.qwen_hip_model_create(layers, np.ascontiguousarray(weight_ddr),
+                                                np.ascontiguousarray(scale_ddr), ctypes.byref(handle))
+        _check(self.lib, st, "qwen_hip_model_create")
+        self.handle = handle
+        self.layers = layers
+        self.stream = torch.cuda.ExternalStream(self.lib.qwen_hip_model_stream(handle))
+
+    def close(self) -> None:
+        if getattr(self, "handle", None) is not None and self.handle.value:
+            self.lib.qwen_hip_model_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def synchronize(self) -> None:
+        _check(self.lib, self.lib.qwen_hip_model_synchronize(self.handle), "synchronize")
+
+    def _enter(self):
+        """Orders the model's stream after work already queued on torch's current stream."""
+        import torch
+
+        ev = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream())
+        self.stream.wait_event(ev)
+
+    def decode(self, mode: int, hidden, positions, max_keys: int, cache: KvCache, order: bool = True) -> None:
+        """hidden [B,1536] fp32 (in/out), positions [B] int32 on the GPU."""
+        if order:
+            self._enter()
+        B = hidden.shape[0]
+        st = self.lib.qwen_hip_model_decode(self.handle, mode, B, _ptr(hidden), _ptr(positions), int(max_keys),
+                                            _ptr(cache.k), _ptr(cache.v), cache.seq_stride, cache.layer_stride)
+        _check(self.lib, st, "qwen_hip_model_decode")
+
+    def prefill(self, mode: int, hidden, cache: KvCache, order: bool = True) -> None:
+        """hidden [B,S,1536] fp32 (in/out); cache rows 0..S-1 of sequences 0..B-1 are written."""
+        if order:
+            self._enter()
+        B, S = hidden.shape[0], hidden.shape[1]
+        st = self.lib.qwen_hip_model_prefill(self.handle, mode, B, S, _ptr(hidden), _ptr(cache.k), _ptr(cache.v),
+                                             cache.seq_stride, cache.layer_stride)
+        _check(self.lib, st, "qwen_hip_model_prefill")
+
+    def embed(self, token_ids, hidden, order: bool = True) -> None:
+        if order:
+            self._enter()
+        st = self.lib.qwen_hip_model_embed(self.handle, _ptr(token_ids), int(token_ids.numel()), _ptr(hidden))
+        _check(self.lib, st, "qwen_hip_model_embed")
+
+    def time_kernel(self, kernel: int, layer: int = 0, reps: int = 20) -> float:
+        """Mean milliseconds of one launch of `kernel`, re-run in isolation with the shapes of the
+        last FAST call (HIP events on the model's stream)."""
+        ms = ctypes.c_float(0.0)
+        st = self.lib.qwen_hip_model_time_kernel(self.handle, kernel, layer, reps, ctypes.byref(ms))
+        _check(self.lib, st, "qwen_hip_model_time_kernel")
+        return float(ms.value)
+
+
+def fill_kv_synthetic(cache: KvCache, seed: int) -> None:
+    """N(0,1) K/V rows quantized per row to INT4 and dequantized, generated on the device."""
+    lib = abi.load()
+    rows = cache.layers * cache.sequences * cache.positions
+    _check(lib, lib.qwen_hip_fill_kv_synthetic(_ptr(cache.k), rows, seed, None), "fill K")
+    _check(lib, lib.qwen_hip_fill_kv_synthetic(_ptr(cache.v), rows, seed + 0x5bd1e995, None), "fill V")
+
+
+def quantize_int4_device(w) -> tuple:
+    """Device INT4 quantizer (verification/real_host_top_backend.py:31-41) of an fp32 [out,in]
+    torch tensor on the GPU; returns (packed uint8 [out*in/2], scales fp32 [out])."""
+    import torch
+
+    out_dim, in_dim = w.shape
+    packed = torch.empty(out_dim * in_dim // 2, dtype=torch.uint8, device=w.device)
+    scales = torch.empty(out_dim, dtype=torch.float32, device=w.device)
+    lib = abi.load()
+    st = lib.qwen_hip_quantize_int4(_ptr(w.contiguous()), out_dim, in_dim, _ptr(packed), _ptr(scales),
+                                    ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    _check(lib, st, "qwen_hip_quantize_int4")
+    return packed, scales
+
+
+__all__ = ["DeviceModel", "KvCache", "fill_kv_synthetic", "quantize_int4_device", "MODE_ORDERED", "MODE_FAST",
+           "HIDDEN"]
