@@ -264,3 +264,49 @@ def test_synthetic_model_runs(torch):
         assert m.time_kernel(1, 0, 3) > 0.0
     finally:
         m.close()
+
+
+@pytest.mark.parametrize("batch", [20, 64])
+def test_model_decode_fast_batched(torch, layers2, batch):
+    """Batches of 17..64 tokens take the LDS-staged, K-split GEMM path; every sequence of the
+    batch stays within the per-layer tolerance of the oracle."""
+    from work_llm_accelerator_amd.model import FLAG_NO_BF16_ROUND, MODE_FAST, DeviceModel
+
+    rng = np.random.default_rng(batch)
+    pasts = [int(p) for p in rng.integers(0, 40, batch)]
+    print(f"model decode fast batch={batch}", flush=True)
+    m1 = DeviceModel(1, layers2[1].weight_ddr, layers2[1].scale_ddr)
+    try:
+        cache, hist, x = decode_setup(torch, 1, pasts, 48, seed=31)
+        hidden = torch.from_numpy(x).cuda()
+        pos = torch.tensor(pasts, dtype=torch.int32, device="cuda")
+        m1.decode(MODE_FAST | FLAG_NO_BF16_ROUND, hidden, pos, max(pasts) + 1, cache)
+        m1.synchronize()
+        got = hidden.cpu().numpy()
+        for b, past in enumerate(pasts):
+            kl = [hist[(0, b)][0].copy()]
+            vl = [hist[(0, b)][1].copy()]
+            ref = oracle_decode(layers2[1:], x[b], past, kl, vl, rounding=False)
+            assert rel_err(got[b], ref) <= FAST_TOL, (b, rel_err(got[b], ref))
+    finally:
+        m1.close()
+
+
+def test_model_prefill_fast_mid(torch, layers2):
+    """40 tokens: the 17..64-token GEMM path on prefill shapes."""
+    from work_llm_accelerator_amd.model import FLAG_NO_BF16_ROUND, MODE_FAST, DeviceModel, KvCache
+
+    S = 40
+    x = round_bfloat16_array(random_hidden(444, S))
+    m1 = DeviceModel(1, layers2[0].weight_ddr, layers2[0].scale_ddr)
+    try:
+        cache = KvCache.allocate(1, 1, S)
+        hidden = torch.from_numpy(x.reshape(1, S, HIDDEN)).cuda()
+        m1.prefill(MODE_FAST | FLAG_NO_BF16_ROUND, hidden, cache)
+        m1.synchronize()
+        got = hidden.cpu().numpy().reshape(-1)
+        ref, ks, vs = oracle_prefill(layers2[:1], x, S, rounding=False)
+        assert rel_err(got, ref) <= FAST_TOL
+        assert rel_err(cache.k[0, 0].cpu().numpy().reshape(-1), ks[0]) <= FAST_TOL
+    finally:
+        m1.close()

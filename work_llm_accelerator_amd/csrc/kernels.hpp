@@ -25,6 +25,7 @@ constexpr int kKChunk = 128;        // K values per repacked weight chunk
 constexpr int kQuantMax = 32512;    // |X| bound of the two-limb activation code (127 * 256)
 constexpr int kMaxQuantRow = 8960;  // widest activation row that is quantized
 constexpr int kAttnChunk = 256;     // keys per decode-attention block
+constexpr int kMaxChunks = (32768 + kAttnChunk - 1) / kAttnChunk;  // chunks of the longest KV
 constexpr int kNormNone = 0, kNormDecode = 1, kNormPrefill = 2;
 constexpr int kEpiStore = 0, kEpiSiluMul = 1, kEpiResidual = 2;
 

@@ -406,6 +406,210 @@ __global__ void __launch_bounds__(256) gemm_i8_kernel(GemmArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------
+// The same GEMM for many tokens: the activation tile of a K chunk (16*NT tokens x 256 bytes of
+// limbs) is staged once per block in LDS (double-buffered, rows padded by 16 bytes so the 16
+// token rows a lane group reads fall on distinct banks) and shared by all waves; each wave covers
+// RTW row tiles, so every B operand read from LDS feeds RTW (x2 for DUAL) matrix-core products.
+// KSPLIT groups of waves split the K chunks; their int32 partial sums are added through LDS
+// (exact).  Block: 4 waves = (4/KSPLIT) row groups x KSPLIT; rows per block = 16*RTW*(4/KSPLIT).
+// grid = (ceil(tokens / (16*NT)), ceil(row_tiles / (RTW*4/KSPLIT))).  Requires (in/128) % KSPLIT == 0.
+// ---------------------------------------------------------------------------------------------
+constexpr int kXRowPitch = 256 + 16;  // LDS bytes per staged token row (two limbs of one K chunk)
+
+template <int NT, int RTW, int KSPLIT, int EPI, bool DUAL>
+__global__ void __launch_bounds__(256) gemm_i8_lds_kernel(GemmArgs a) {
+  constexpr int GROUPS = 4 / KSPLIT;                 // row groups per block
+  constexpr int TOK = 16 * NT;                       // tokens per block
+  constexpr int STAGE = TOK * kXRowPitch;            // bytes of one staged chunk
+  constexpr int D = DUAL ? 2 : 1;
+  __shared__ __align__(16) uint8_t xs[KSPLIT][2][STAGE];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int grp = wave / KSPLIT;   // row group
+  const int ks = wave % KSPLIT;    // K split of this wave
+  const int g = lane >> 4;
+  const int col = lane & 15;
+  const int row_tiles = a.out_dim / 16;
+  const int rt0 = (blockIdx.y * GROUPS + grp) * RTW;
+  const int nkc = a.in_dim / kKChunk;
+  const int per = nkc / KSPLIT;
+  const int kc_begin = ks * per;
+  const int tok0 = blockIdx.x * TOK;
+  const size_t row_stride_x = (size_t)a.in_dim * 2u;
+
+  v4i accH[D][RTW][NT], accL[D][RTW][NT];
+#pragma unroll
+  for (int d = 0; d < D; ++d)
+#pragma unroll
+    for (int r = 0; r < RTW; ++r)
+#pragma unroll
+      for (int n = 0; n < NT; ++n) accH[d][r][n] = accL[d][r][n] = v4i{0, 0, 0, 0};
+
+  // Staging: the waves of split ks (KSPLIT == 1: all 4 waves; else the GROUPS waves with this ks)
+  // copy TOK rows x 256 bytes of chunk kc into xs[ks][buf]: loads are issued before the products
+  // of the current chunk and stored to LDS after them, so their latency overlaps the MFMAs.
+  constexpr int STAGERS = 64 * GROUPS;
+  constexpr int SPT = (TOK * 16 + STAGERS - 1) / STAGERS;  // 16-byte pieces per thread
+  const int stager_id = grp * 64 + lane;
+  uint4 sreg[SPT];
+  auto stage_load = [&](int kc) {
+#pragma unroll
+    for (int j = 0; j < SPT; ++j) {
+      const int e = stager_id + j * STAGERS;
+      const int t = e >> 4, part = e & 15;
+      const int tok = tok0 + t;
+      sreg[j] = (e < TOK * 16 && tok < a.tokens)
+                    ? *reinterpret_cast<const uint4*>(a.xq + (size_t)tok * row_stride_x + (size_t)kc * 256u + part * 16)
+                    : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto stage_store = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < SPT; ++j) {
+      const int e = stager_id + j * STAGERS;
+      if (e < TOK * 16) *reinterpret_cast<uint4*>(&xs[ks][buf][(e >> 4) * kXRowPitch + (e & 15) * 16]) = sreg[j];
+    }
+  };
+  const uint4* wp[D][RTW];
+  bool rt_ok[RTW];
+#pragma unroll
+  for (int r = 0; r < RTW; ++r) {
+    rt_ok[r] = rt0 + r < row_tiles;
+    const size_t off = ((size_t)(rt_ok[r] ? rt0 + r : 0) * nkc) * 64u + lane;
+    wp[0][r] = reinterpret_cast<const uint4*>(a.wp) + off;
+    if (DUAL) wp[D - 1][r] = reinterpret_cast<const uint4*>(a.wp2) + off;
+  }
+  uint4 wcur[D][RTW], wnext[D][RTW];
+#pragma unroll
+  for (int d = 0; d < D; ++d)
+#pragma unroll
+    for (int r = 0; r < RTW; ++r) wcur[d][r] = ld_stream(wp[d][r] + (size_t)kc_begin * 64u);
+  stage_load(kc_begin);
+  stage_store(0);
+  __syncthreads();
+  for (int i = 0; i < per; ++i) {
+    const int kc = kc_begin + i;
+    const int buf = i & 1;
+    if (i + 1 < per) {
+      stage_load(kc + 1);
+#pragma unroll
+      for (int d = 0; d < D; ++d)
+#pragma unroll
+        for (int r = 0; r < RTW; ++r) wnext[d][r] = ld_stream(wp[d][r] + (size_t)(kc + 1) * 64u);
+    }
+    v4i a1[D][RTW], a2[D][RTW];
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+#pragma unroll
+      for (int r = 0; r < RTW; ++r) unpack16(wcur[d][r], a1[d][r], a2[d][r]);
+    const uint8_t* xb = &xs[ks][buf][col * kXRowPitch + 32 * g];
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+      const v4i* p = reinterpret_cast<const v4i*>(xb + n * 16 * kXRowPitch);
+      const v4i bh1 = p[0], bh2 = p[1], bl1 = p[8], bl2 = p[9];
+#pragma unroll
+      for (int d = 0; d < D; ++d)
+#pragma unroll
+        for (int r = 0; r < RTW; ++r) {
+          accH[d][r][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[d][r], bh1, accH[d][r][n], 0, 0, 0);
+          accH[d][r][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2[d][r], bh2, accH[d][r][n], 0, 0, 0);
+          accL[d][r][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[d][r], bl1, accL[d][r][n], 0, 0, 0);
+          accL[d][r][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2[d][r], bl2, accL[d][r][n], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+#pragma unroll
+      for (int r = 0; r < RTW; ++r) wcur[d][r] = wnext[d][r];
+    if (i + 1 < per) stage_store(buf ^ 1);
+    __syncthreads();
+  }
+
+  if (KSPLIT > 1) {
+    // splits 1.. hand their partial sums to split 0 of the same row group through LDS.
+    constexpr int NACC = D * RTW * NT * 8;
+    static_assert((KSPLIT - 1) * GROUPS * NACC * 64 * 4 <= (int)sizeof(xs), "reduction does not fit");
+    int* red = reinterpret_cast<int*>(&xs[0][0][0]);
+    if (ks > 0) {
+      int* dst = red + (((ks - 1) * GROUPS + grp) * NACC) * 64 + lane;
+      int idx = 0;
+#pragma unroll
+      for (int d = 0; d < D; ++d)
+#pragma unroll
+        for (int r = 0; r < RTW; ++r)
+#pragma unroll
+          for (int n = 0; n < NT; ++n)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              dst[(idx++) * 64] = accH[d][r][n][q];
+              dst[(idx++) * 64] = accL[d][r][n][q];
+            }
+    }
+    __syncthreads();
+    if (ks > 0) return;
+#pragma unroll
+    for (int s2 = 0; s2 < KSPLIT - 1; ++s2) {
+      const int* src = red + ((s2 * GROUPS + grp) * NACC) * 64 + lane;
+      int idx = 0;
+#pragma unroll
+      for (int d = 0; d < D; ++d)
+#pragma unroll
+        for (int r = 0; r < RTW; ++r)
+#pragma unroll
+          for (int n = 0; n < NT; ++n)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              accH[d][r][n][q] += src[(idx++) * 64];
+              accL[d][r][n][q] += src[(idx++) * 64];
+            }
+    }
+  }
+
+#pragma unroll
+  for (int r = 0; r < RTW; ++r) {
+    if (!rt_ok[r]) continue;
+    const int row0 = (rt0 + r) * 16 + 4 * g;
+    float sw[4], sw2[4], bias[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      sw[q] = a.sw[row0 + q];
+      sw2[q] = DUAL ? a.sw2[row0 + q] : 0.0f;
+      bias[q] = a.bias ? a.bias[row0 + q] : 0.0f;
+    }
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+      const int tok = tok0 + n * 16 + col;
+      if (tok >= a.tokens) continue;
+      const double sx = (double)a.sx[tok];
+      const int sh8 = 8 * a.sums[2 * tok];
+      const int sl8 = 8 * a.sums[2 * tok + 1];
+      float out[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const double tot = (double)(accH[0][r][n][q] - sh8) * 256.0 + (double)(accL[0][r][n][q] - sl8);
+        const float v = (float)(tot * sx) * sw[q];
+        if (EPI == kEpiSiluMul) {
+          const double tot2 = (double)(accH[D - 1][r][n][q] - sh8) * 256.0 + (double)(accL[D - 1][r][n][q] - sl8);
+          const float u = (float)(tot2 * sx) * sw2[q];
+          const float sg = a.prefill_silu ? silu_prefill(v) : silu_decode(v);
+          out[q] = sg * u;
+        } else if (EPI == kEpiResidual) {
+          out[q] = a.resid[(size_t)tok * a.resid_stride + row0 + q] + v;
+        } else {
+          out[q] = v + bias[q];
+        }
+      }
+      if (EPI == kEpiResidual && a.y_raw)
+        *reinterpret_cast<float4*>(a.y_raw + (size_t)tok * a.y_stride + row0) = make_float4(out[0], out[1], out[2], out[3]);
+      if (EPI == kEpiResidual && a.round_bf16)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) out[q] = round_bf16(out[q]);
+      *reinterpret_cast<float4*>(a.y + (size_t)tok * a.y_stride + row0) = make_float4(out[0], out[1], out[2], out[3]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 // RoPE of q (in place) and k, plus the K/V cache append, for rows of a fused [q | k | v] buffer
 // (qkv_stride floats per token).  Decode: token b is sequence b at position pos[b].  Prefill:
 // token t is sequence t / seq_len at position t % seq_len.  rope: [position][cos 64 | sin 64].
@@ -544,6 +748,157 @@ __global__ void __launch_bounds__(256) attn_decode_partial_kernel(const float* _
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Decode attention partials on the fp32 matrix cores (v_mfma_f32_16x16x4_f32): same partials as
+// attn_decode_partial_kernel, but the K/V rows are read straight into MFMA operand registers with
+// 64-byte-contiguous row segments, and the probabilities never leave registers.
+// Block (chunk c, KV head kvh, sequence b), 4 waves; wave w covers keys t0 + 64w + [0, 64) in
+// tiles of 16.  Per tile (lane l: col = l & 15, g = l >> 4):
+//   S = K_tile . Q^T:  A = K[token col][dims], B = Q[head col][dims] (heads >= 6 are zero),
+//                      32 MFMAs over the 128 dims (dim 4g + 16j + e for MFMA 4j + e);
+//                      lane gets S[token 4g + r][head col], r = 0..3.
+//   online softmax per head col (max over the 16 tokens: registers + xor-shuffles 16, 32);
+//   O += P . V:        MFMA (r, h, e): A = P[head col][token 4g + r] (the lane's own p[r]),
+//                      B = V[token 4g + r][dim 4 col + e + 64h]; lane holds O[head 4g + r'][dim].
+// The 4 waves are merged in LDS and one (m, l, acc[128]) partial per query head is written.
+// ---------------------------------------------------------------------------------------------
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+__global__ void __launch_bounds__(256) attn_decode_mfma_kernel(const float* __restrict__ qkv, int qkv_stride,
+                                                               const float* __restrict__ k_cache,
+                                                               const float* __restrict__ v_cache, size_t seq_stride,
+                                                               const int* __restrict__ pos, float* __restrict__ part,
+                                                               float2* __restrict__ pml, int nchunk, int max_keys) {
+  __shared__ float s_m[4][QWEN_GROUPS], s_l[4][QWEN_GROUPS];
+  __shared__ float s_acc[4][QWEN_GROUPS][QWEN_HEAD_DIM];
+  const int c = blockIdx.x;
+  const int kvh = blockIdx.y;
+  const int b = blockIdx.z;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int col = lane & 15;
+  const int g = lane >> 4;
+  const int n = min(max(pos[b], 0) + 1, max_keys);
+  const int t0 = c * kAttnChunk;
+  if (t0 >= n) return;  // block-uniform; the combine step only reads chunks below ceil(n / 256)
+  const float scaling = 0.08838834764831845f;
+
+  float qr[32];
+  {
+    const bool hv = col < QWEN_GROUPS;
+    const float* qp = qkv + (size_t)b * qkv_stride + (kvh * QWEN_GROUPS + (hv ? col : 0)) * QWEN_HEAD_DIM + 4 * g;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float4 q4 = hv ? *reinterpret_cast<const float4*>(qp + 16 * j) : make_float4(0, 0, 0, 0);
+      qr[4 * j + 0] = q4.x * scaling;
+      qr[4 * j + 1] = q4.y * scaling;
+      qr[4 * j + 2] = q4.z * scaling;
+      qr[4 * j + 3] = q4.w * scaling;
+    }
+  }
+  const float* kb = k_cache + (size_t)b * seq_stride + kvh * QWEN_HEAD_DIM;
+  const float* vb = v_cache + (size_t)b * seq_stride + kvh * QWEN_HEAD_DIM;
+  float m = -INFINITY;
+  float lp = 0.0f;
+  v4f acc[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) acc[k] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+  const int wbase = t0 + wave * 64;
+#pragma unroll 1
+  for (int tile = 0; tile < 4; ++tile) {
+    const int tb = wbase + tile * 16;
+    if (tb >= n) break;  // wave-uniform
+    float4 kr[8];
+    const int tk = tb + col;
+    const float* krow = kb + (size_t)tk * QWEN_KV_WIDTH + 4 * g;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      kr[j] = tk < n ? ld_stream(reinterpret_cast<const float4*>(krow + 16 * j)) : make_float4(0, 0, 0, 0);
+    float4 vr[4][2];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int tv = tb + 4 * g + r;
+      const float* vrow = vb + (size_t)tv * QWEN_KV_WIDTH + 4 * col;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        vr[r][h] = tv < n ? ld_stream(reinterpret_cast<const float4*>(vrow + 64 * h)) : make_float4(0, 0, 0, 0);
+    }
+    v4f sc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      sc = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[j].x, qr[4 * j + 0], sc, 0, 0, 0);
+      sc = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[j].y, qr[4 * j + 1], sc, 0, 0, 0);
+      sc = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[j].z, qr[4 * j + 2], sc, 0, 0, 0);
+      sc = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[j].w, qr[4 * j + 3], sc, 0, 0, 0);
+    }
+    float mt = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      if (tb + 4 * g + r >= n) sc[r] = -INFINITY;
+      mt = fmaxf(mt, sc[r]);
+    }
+    mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    const float mn = fmaxf(m, mt);  // finite: token tb < n is in the tile
+    const float corr = __expf(m - mn);
+    float p[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) p[r] = __expf(sc[r] - mn);
+    lp = lp * corr + ((p[0] + p[1]) + (p[2] + p[3]));
+    m = mn;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const float cr = __shfl(corr, 4 * g + rr, 64);  // lane 4g + rr holds head 4g + rr
+#pragma unroll
+      for (int k = 0; k < 8; ++k) acc[k][rr] *= cr;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        acc[4 * h + 0] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[r], vr[r][h].x, acc[4 * h + 0], 0, 0, 0);
+        acc[4 * h + 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[r], vr[r][h].y, acc[4 * h + 1], 0, 0, 0);
+        acc[4 * h + 2] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[r], vr[r][h].z, acc[4 * h + 2], 0, 0, 0);
+        acc[4 * h + 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[r], vr[r][h].w, acc[4 * h + 3], 0, 0, 0);
+      }
+    }
+  }
+  lp += __shfl_xor(lp, 16, 64);
+  lp += __shfl_xor(lp, 32, 64);
+  if (g == 0 && col < QWEN_GROUPS) {
+    s_m[wave][col] = m;
+    s_l[wave][col] = lp;
+  }
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) {
+    const int head = 4 * g + rr;
+    if (head < QWEN_GROUPS) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s_acc[wave][head][4 * col + e + 64 * h] = acc[4 * h + e][rr];
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < QWEN_GROUPS * QWEN_HEAD_DIM; i += 256) {
+    const int head = i / QWEN_HEAD_DIM, d = i % QWEN_HEAD_DIM;
+    float M = s_m[0][head];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) M = fmaxf(M, s_m[w][head]);
+    float L = 0.0f, A = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float f = s_m[w][head] == -INFINITY ? 0.0f : __expf(s_m[w][head] - M);
+      L += s_l[w][head] * f;
+      A += s_acc[w][head][d] * f;
+    }
+    const int qh = kvh * QWEN_GROUPS + head;
+    part[(((size_t)b * QWEN_Q_HEADS + qh) * nchunk + c) * QWEN_HEAD_DIM + d] = A;
+    if (d == 0) pml[((size_t)b * QWEN_Q_HEADS + qh) * nchunk + c] = make_float2(M, L);
+  }
+}
+
 // Merges the chunk partials of one sequence into ctx[b][1536] = acc / l and quantizes the row for
 // the O projection.  grid = batch, block = 256.
 __global__ void __launch_bounds__(256) attn_decode_combine_kernel(const float* __restrict__ part,
@@ -552,31 +907,36 @@ __global__ void __launch_bounds__(256) attn_decode_combine_kernel(const float* _
                                                                   float* __restrict__ ctx, int8_t* __restrict__ xq,
                                                                   float* __restrict__ sx, int* __restrict__ sums) {
   __shared__ float row[QWEN_HIDDEN];
+  __shared__ float wgt[QWEN_Q_HEADS][kMaxChunks];
   __shared__ float gm[QWEN_Q_HEADS], ginv[QWEN_Q_HEADS];
   __shared__ float red_f[4];
   __shared__ int red_i[4];
   const int b = blockIdx.x;
   const int n = min(max(pos[b], 0) + 1, max_keys);
   const int nc = min((n + kAttnChunk - 1) / kAttnChunk, nchunk);
+  const float2* pb = pml + (size_t)b * QWEN_Q_HEADS * nchunk;
   if (threadIdx.x < QWEN_Q_HEADS) {
-    const float2* pm = pml + ((size_t)b * QWEN_Q_HEADS + threadIdx.x) * nchunk;
-    float m = -INFINITY;
-    for (int c = 0; c < nc; ++c) m = fmaxf(m, pm[c].x);
-    float l = 0.0f;
-    for (int c = 0; c < nc; ++c) l += pm[c].y * __expf(pm[c].x - m);
-    gm[threadIdx.x] = m;
-    ginv[threadIdx.x] = l > 0.0f ? 1.0f / l : 0.0f;
+    const float2* pm = pb + threadIdx.x * nchunk;
+    float M = -INFINITY;
+    for (int c = 0; c < nc; ++c) M = fmaxf(M, pm[c].x);
+    float L = 0.0f;
+    for (int c = 0; c < nc; ++c) L += pm[c].y * __expf(pm[c].x - M);
+    gm[threadIdx.x] = M;
+    ginv[threadIdx.x] = L > 0.0f ? 1.0f / L : 0.0f;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < QWEN_Q_HEADS * nc; i += 256) {
+    const int h = i / nc, c = i % nc;
+    wgt[h][c] = __expf(pb[h * nchunk + c].x - gm[h]) * ginv[h];
   }
   __syncthreads();
   for (int i = threadIdx.x; i < QWEN_HIDDEN; i += 256) {
     const int h = i / QWEN_HEAD_DIM, d = i % QWEN_HEAD_DIM;
-    const float2* pm = pml + ((size_t)b * QWEN_Q_HEADS + h) * nchunk;
     const float* pa = part + ((size_t)b * QWEN_Q_HEADS + h) * nchunk * QWEN_HEAD_DIM + d;
     float acc = 0.0f;
-    for (int c = 0; c < nc; ++c) acc += pa[(size_t)c * QWEN_HEAD_DIM] * __expf(pm[c].x - gm[h]);
-    const float v = acc * ginv[h];
-    row[i] = v;
-    if (ctx) ctx[(size_t)b * QWEN_HIDDEN + i] = v;
+    for (int c = 0; c < nc; ++c) acc += pa[(size_t)c * QWEN_HEAD_DIM] * wgt[h][c];
+    row[i] = acc;
+    if (ctx) ctx[(size_t)b * QWEN_HIDDEN + i] = acc;
   }
   __syncthreads();
   quantize_row_lds(row, QWEN_HIDDEN, xq + (size_t)b * (2 * QWEN_HIDDEN), sx + b, sums + 2 * b, red_f, red_i);
@@ -708,14 +1068,30 @@ static void launch_gemm_t(const GemmArgs& a, hipStream_t st) {
   hipLaunchKernelGGL((gemm_i8_kernel<NT, KSPLIT, EPI, DUAL>), grid, dim3(256), 0, st, a);
 }
 
+template <int NT, int RTW, int KSPLIT, int EPI, bool DUAL>
+static void launch_gemm_lds_t(const GemmArgs& a, hipStream_t st) {
+  constexpr int GROUPS = 4 / KSPLIT;
+  const int row_tiles = a.out_dim / 16;
+  const int rows_per_block = RTW * GROUPS;
+  const dim3 grid((a.tokens + 16 * NT - 1) / (16 * NT), (row_tiles + rows_per_block - 1) / rows_per_block);
+  hipLaunchKernelGGL((gemm_i8_lds_kernel<NT, RTW, KSPLIT, EPI, DUAL>), grid, dim3(256), 0, st, a);
+}
+
+// Shape dispatch.  <= 16 tokens: direct-load kernel, 4-way K split per row tile (many small
+// blocks, weights streamed once).  17..64 tokens: LDS-staged activations for all tokens of the
+// block, 2 row groups x 2-way K split.  More tokens (prefill): 4 row tiles per wave.
 template <int EPI, bool DUAL>
 static void launch_gemm_epi(const GemmArgs& a, hipStream_t st) {
+  const int nkc = a.in_dim / kKChunk;
   if (a.tokens <= 16) {
     launch_gemm_t<1, 4, EPI, DUAL>(a, st);
-  } else if (a.tokens <= 64) {
-    launch_gemm_t<1, 4, EPI, DUAL>(a, st);
+  } else if (a.tokens <= 64 && nkc % 2 == 0) {
+    launch_gemm_lds_t<4, 1, 2, EPI, DUAL>(a, st);
   } else {
-    launch_gemm_t<4, 1, EPI, DUAL>(a, st);
+    if constexpr (DUAL)
+      launch_gemm_lds_t<4, 2, 1, EPI, DUAL>(a, st);
+    else
+      launch_gemm_lds_t<4, 4, 1, EPI, DUAL>(a, st);
   }
 }
 
@@ -738,7 +1114,7 @@ void launch_attn_decode(const float* qkv, int qkv_stride, const float* k_cache, 
                         size_t seq_stride, const int* pos, int batch, int max_keys, float* part, float2* pml,
                         float* ctx, int8_t* xq, float* sx, int* sums, hipStream_t st) {
   const int nchunk = (max_keys + kAttnChunk - 1) / kAttnChunk;
-  hipLaunchKernelGGL(attn_decode_partial_kernel, dim3(nchunk, QWEN_KV_HEADS, batch), dim3(256), 0, st, qkv,
+  hipLaunchKernelGGL(attn_decode_mfma_kernel, dim3(nchunk, QWEN_KV_HEADS, batch), dim3(256), 0, st, qkv,
                      qkv_stride, k_cache, v_cache, seq_stride, pos, part, pml, nchunk, max_keys);
   hipLaunchKernelGGL(attn_decode_combine_kernel, dim3(batch), dim3(256), 0, st, part, pml, pos, nchunk, max_keys, ctx,
                      xq, sx, sums);
@@ -748,7 +1124,7 @@ void launch_attn_decode_partial_only(const float* qkv, int qkv_stride, const flo
                                      size_t seq_stride, const int* pos, int batch, int max_keys, float* part,
                                      float2* pml, hipStream_t st) {
   const int nchunk = (max_keys + kAttnChunk - 1) / kAttnChunk;
-  hipLaunchKernelGGL(attn_decode_partial_kernel, dim3(nchunk, QWEN_KV_HEADS, batch), dim3(256), 0, st, qkv,
+  hipLaunchKernelGGL(attn_decode_mfma_kernel, dim3(nchunk, QWEN_KV_HEADS, batch), dim3(256), 0, st, qkv,
                      qkv_stride, k_cache, v_cache, seq_stride, pos, part, pml, nchunk, max_keys);
 }
 
