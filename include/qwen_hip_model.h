@@ -107,6 +107,12 @@ int qwen_hip_quantize_int4(const float* w, int out_dim, int in_dim, uint8_t* pac
  * (max|x|/7) and dequantized, keyed by seed.  Device pointer. */
 int qwen_hip_fill_kv_synthetic(float* cache, uint64_t rows, uint64_t seed, void* stream);
 
+/* Test hook (no counterpart in the reference): y[i] = the device's host-compatible expf, the
+ * function the ORDERED decode softmax and SiLU use in place of glibc's expf
+ * (qwen_decode_attention_kernel.cpp:149, qwen_decode_mlp_kernel.cpp:80), of the float whose bit
+ * pattern is first_bits + i*stride (mod 2^32), for i < n.  Device pointer; queued on `stream`. */
+int qwen_hip_eval_expf(uint32_t first_bits, uint32_t stride, uint64_t n, float* y, void* stream);
+
 /* Message of the last failure on this thread (empty when none). */
 const char* qwen_hip_last_error(void);
 

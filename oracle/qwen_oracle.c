@@ -687,3 +687,25 @@ int oracle_prefill_layer_uncapped(const float* x, int S, const uint8_t* wd, cons
   free(att);
   return QWEN_OK;
 }
+
+/* Compares y[i] with the host expf of the float whose bit pattern is first + i*stride (mod 2^32);
+ * NaN results compare equal to NaN.  Returns the number of mismatches; *first_bad receives the
+ * first mismatching bit pattern (test infrastructure for the device expf). */
+uint64_t oracle_count_expf_mismatches(uint32_t first, uint32_t stride, uint64_t n, const float* y,
+                                      uint32_t* first_bad) {
+  uint64_t bad = 0;
+  for (uint64_t i = 0; i < n; ++i) {
+    const uint32_t bits = first + (uint32_t)i * stride;
+    float x;
+    memcpy(&x, &bits, 4);
+    const float r = expf(x);
+    uint32_t rb, yb;
+    memcpy(&rb, &r, 4);
+    memcpy(&yb, &y[i], 4);
+    if (rb != yb && !(r != r && y[i] != y[i])) {
+      if (bad == 0 && first_bad) *first_bad = bits;
+      ++bad;
+    }
+  }
+  return bad;
+}

@@ -133,6 +133,10 @@ int oracle_decode_layer_block(
     const float* input_token, int past_seq_len, const uint8_t* weight_ddr, const float* scale_ddr,
     float* k_cache, float* v_cache, float* output_token);
 
+/* Mismatch count of y[i] against the host expf of bit pattern first + i*stride (NaN == NaN). */
+uint64_t oracle_count_expf_mismatches(uint32_t first, uint32_t stride, uint64_t n, const float* y,
+                                      uint32_t* first_bad);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,83 @@
+"""Committed golden fixture of config 1 (tests/golden/decode_c1.npz, written by
+tests/golden/make_decode_golden.py from the reference decode library compiled from its own
+sources): one decode layer, seed-0 weights, KV length 65.
+
+CPU: the oracle reproduces the reference outputs bit for bit (pins the oracle where the reference
+tree is absent).  GPU: the drop-in decode layer (ORDERED) reproduces them bit for bit, and the
+FAST model path stays within 1e-3 of max.
+"""
+
+from __future__ import annotations
+
+import hashlib
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+sys.path.insert(0, str(Path(__file__).resolve().parent / "golden"))
+from make_decode_golden import PAST, case_inputs  # noqa: E402
+
+from _cases import bits_equal, decode_layer, first_mismatch  # noqa: E402
+from _oracle import oracle  # noqa: E402
+
+FIXTURE = Path(__file__).resolve().parent / "golden" / "decode_c1.npz"
+
+
+@pytest.fixture(scope="module")
+def golden():
+    data = np.load(FIXTURE, allow_pickle=False)
+    layer, x, k, v = case_inputs()
+    assert hashlib.sha256(layer.weight_ddr.tobytes()).hexdigest() == str(data["weight_sha256"])
+    assert hashlib.sha256(layer.scale_ddr.tobytes()).hexdigest() == str(data["scale_sha256"])
+    assert bits_equal(x, data["x"]) and bits_equal(k[:PAST * 256], data["k_hist"])
+    return data, layer, x, k, v
+
+
+def test_oracle_matches_reference_fixture(golden):
+    data, layer, x, k, v = golden
+    kc, vc = k.copy(), v.copy()
+    st, out = decode_layer(oracle().oracle_decode_layer_smoke_forward, layer, x, PAST, kc, vc)
+    assert st == 0
+    assert bits_equal(out, data["out"]), first_mismatch(out, data["out"])
+    assert bits_equal(kc[PAST * 256:], data["k_row"]) and bits_equal(vc[PAST * 256:], data["v_row"])
+
+
+@pytest.mark.gpu
+def test_hip_dropin_matches_reference_fixture(golden):
+    from work_llm_accelerator_amd import abi
+
+    data, layer, x, k, v = golden
+    lib = abi.load(abi.DECODE_STUB_PATH)
+    kc, vc = k.copy(), v.copy()
+    st, out = decode_layer(lib.qwen_decode_layer_smoke_forward, layer, x, PAST, kc, vc)
+    assert st == 0, abi.last_error(lib)
+    assert bits_equal(out, data["out"]), first_mismatch(out, data["out"])
+    assert bits_equal(kc[PAST * 256:], data["k_row"]) and bits_equal(vc[PAST * 256:], data["v_row"])
+
+
+@pytest.mark.gpu
+def test_hip_fast_model_within_tolerance_of_fixture(golden):
+    import torch
+
+    from work_llm_accelerator_amd.layout import HIDDEN, KV_WIDTH
+    from work_llm_accelerator_amd.model import FLAG_NO_BF16_ROUND, MODE_FAST, DeviceModel, KvCache
+
+    data, layer, x, k, v = golden
+    m = DeviceModel(1, layer.weight_ddr, layer.scale_ddr)
+    try:
+        cache = KvCache.allocate(1, 1, PAST + 1)
+        cache.k[0, 0] = torch.from_numpy(k.reshape(PAST + 1, KV_WIDTH))
+        cache.v[0, 0] = torch.from_numpy(v.reshape(PAST + 1, KV_WIDTH))
+        hidden = torch.from_numpy(x.reshape(1, HIDDEN)).cuda()
+        m.decode(MODE_FAST | FLAG_NO_BF16_ROUND, hidden, torch.tensor([PAST], dtype=torch.int32, device="cuda"),
+                 PAST + 1, cache)
+        m.synchronize()
+        out = hidden.cpu().numpy().reshape(-1)
+        ref = data["out"]
+        assert np.max(np.abs(out - ref)) <= 1e-3 * np.max(np.abs(ref))
+        krow = cache.k[0, 0, PAST].cpu().numpy()
+        assert np.max(np.abs(krow - data["k_row"])) <= 1e-3 * np.max(np.abs(data["k_row"]))
+    finally:
+        m.close()

@@ -67,6 +67,7 @@ EXTRA_SIGNATURES: dict[str, tuple[list, object]] = {
     "qwen_hip_model_time_kernel": ([P, c_int, c_int, c_int, ctypes.POINTER(ctypes.c_float)], c_int),
     "qwen_hip_quantize_int4": ([P, c_int, c_int, P, P, P], c_int),
     "qwen_hip_fill_kv_synthetic": ([P, c_u64, c_u64, P], c_int),
+    "qwen_hip_eval_expf": ([ctypes.c_uint32, ctypes.c_uint32, c_u64, P, P], c_int),
 }
 
 _LIB: ctypes.CDLL | None = None

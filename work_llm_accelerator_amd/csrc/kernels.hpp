@@ -79,5 +79,6 @@ void launch_fill_vector(float* dst, size_t n, uint64_t stream, float sigma, int 
 void launch_fill_bf16_table(uint16_t* dst, size_t n, uint64_t stream, float sigma, hipStream_t st);
 void launch_kv_synthetic(float* cache, uint64_t rows, uint64_t stream, hipStream_t st);
 void launch_embed(const uint16_t* table, const int* ids, int count, float* hidden, hipStream_t st);
+void launch_eval_expf(uint32_t first, uint32_t stride, uint64_t n, float* y, hipStream_t st);
 
 }  // namespace qwen

@@ -110,7 +110,19 @@ __global__ void embed_kernel(const uint16_t* __restrict__ table, const int* __re
     hidden[(size_t)t * QWEN_HIDDEN + d] = bits_f32((uint32_t)table[row + d] << 16);
 }
 
+// Host-compatible expf over a strided sweep of bit patterns (test hook).
+__global__ void eval_expf_kernel(uint32_t first, uint32_t stride, uint64_t n, float* __restrict__ y) {
+  const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const uint32_t bits = first + (uint32_t)i * stride;
+  y[i] = glibc_expf(bits_f32(bits));
+}
+
 // ---------------------------------------------------------------------------------------------
+void launch_eval_expf(uint32_t first, uint32_t stride, uint64_t n, float* y, hipStream_t st) {
+  hipLaunchKernelGGL(eval_expf_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, first, stride, n, y);
+}
+
 void launch_quantize_rows(const float* src, int out_dim, int in_dim, uint64_t stream, float sigma, uint8_t* packed,
                           float* scales, hipStream_t st) {
   hipLaunchKernelGGL(quantize_rows_kernel, dim3(out_dim), dim3(256), 0, st, src, in_dim, stream, sigma, packed, scales);

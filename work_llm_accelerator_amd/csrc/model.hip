@@ -550,4 +550,15 @@ int qwen_hip_fill_kv_synthetic(float* cache, uint64_t rows, uint64_t seed, void*
   });
 }
 
+int qwen_hip_eval_expf(uint32_t first_bits, uint32_t stride, uint64_t n, float* y, void* stream) {
+  if (!y) return invalid("null output");
+  if (n == 0) return QWEN_OK;
+  if (n > (1ull << 32)) return invalid("n exceeds 2^32");
+  return guarded_model([&]() -> int {
+    launch_eval_expf(first_bits, stride, n, y, static_cast<hipStream_t>(stream));
+    QWEN_HIP(hipGetLastError());
+    return QWEN_OK;
+  });
+}
+
 }  // extern "C"

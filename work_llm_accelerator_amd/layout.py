@@ -269,3 +269,21 @@ def to_c_prefill(descs: list[PrefillLayerDescriptor]):
             else:
                 setattr(c, f, getattr(d, f))
     return arr
+
+
+def kv_to_head_major(flat_cache, seq_len: int):
+    """ABI token-major KV rows [seq_len][kv_head][128] (flat fp32) -> HF cache layout
+    [kv_head][seq_len][128] (verification/real_host_top_backend.py:199-201)."""
+    import numpy as np
+
+    token_major = np.asarray(flat_cache, dtype=np.float32).reshape(seq_len, KV_HEADS, HEAD_DIM)
+    return np.ascontiguousarray(np.transpose(token_major, (1, 0, 2)))
+
+
+def kv_to_token_major(head_major, seq_len: int):
+    """HF cache layout [kv_head][seq_len][128] -> flat ABI token-major rows
+    (verification/real_host_top_backend.py:203-206)."""
+    import numpy as np
+
+    hm = np.asarray(head_major, dtype=np.float32).reshape(KV_HEADS, seq_len, HEAD_DIM)
+    return np.ascontiguousarray(np.transpose(hm, (1, 0, 2)).reshape(-1))
