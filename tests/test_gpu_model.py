@@ -292,12 +292,14 @@ def test_model_decode_fast_batched(torch, layers2, batch):
         m1.close()
 
 
-def test_model_prefill_fast_mid(torch, layers2):
-    """40 tokens: the 17..64-token GEMM path on prefill shapes."""
+@pytest.mark.parametrize("S", [40, 150])
+def test_model_prefill_fast_mid(torch, layers2, S):
+    """40 tokens: the 17..64-token GEMM path on prefill shapes; 150 tokens: the many-token GEMM
+    path and ten causal key tiles of the prefill attention (partial last tile)."""
     from work_llm_accelerator_amd.model import FLAG_NO_BF16_ROUND, MODE_FAST, DeviceModel, KvCache
 
-    S = 40
-    x = round_bfloat16_array(random_hidden(444, S))
+    print(f"model prefill fast S={S}", flush=True)
+    x = round_bfloat16_array(random_hidden(444 + S, S))
     m1 = DeviceModel(1, layers2[0].weight_ddr, layers2[0].scale_ddr)
     try:
         cache = KvCache.allocate(1, 1, S)

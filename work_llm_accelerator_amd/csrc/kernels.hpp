@@ -49,7 +49,14 @@ struct GemmArgs {
   float* y_raw;         // kEpiResidual: optional copy of the output before bf16 rounding
   int round_bf16;       // kEpiResidual: round the output to bf16 (driver rounding)
   int prefill_silu;     // kEpiSiluMul: 1 = approx_exp SiLU (prefill), 0 = expf SiLU (decode)
+  float* part;          // optional fp32 workspace for K splits across blocks: [splits][tokens][out]
 };
+
+// K splits across blocks: at most kMaxSplits splits, only for GEMMs of at most kSplitTokens tokens;
+// the workspace holds kMaxSplits x kSplitTokens x out floats.
+constexpr int kMaxSplits = 16;
+constexpr int kSplitTokens = 256;
+inline size_t splitk_bytes(size_t out) { return (size_t)kMaxSplits * kSplitTokens * out * 4u; }
 
 void launch_repack_int4(const uint8_t* W, int out_dim, int in_dim, uint8_t* WP, hipStream_t st);
 void launch_norm_quant(const float* x, size_t x_stride, int rows, int n, const float* w, int norm, int8_t* xq,

@@ -179,35 +179,102 @@ __device__ void quantize_row_lds(const float* __restrict__ v, int n, int8_t* __r
 //   NORM_NONE: quantize x as is.
 // Optionally writes the normalized fp32 row to xn.
 // ---------------------------------------------------------------------------------------------
+constexpr int kQuantVecs = (kMaxQuantRow / 4 + 255) / 256;  // float4 per thread for the widest row
+
 __global__ void __launch_bounds__(256) norm_quant_kernel(const float* __restrict__ x, size_t x_stride, int n,
                                                          const float* __restrict__ w, int norm,
                                                          int8_t* __restrict__ xq, float* __restrict__ sx,
                                                          int* __restrict__ sums, float* __restrict__ xn) {
-  __shared__ float row[kMaxQuantRow];
   __shared__ float red_f[4];
   __shared__ double red_d[4];
   __shared__ int red_i[4];
   const int t = blockIdx.x;
-  const float* xr = x + (size_t)t * x_stride;
-  for (int k = threadIdx.x; k < n; k += 256) row[k] = xr[k];
-  __syncthreads();
+  const int n4 = n >> 2;
+  const float4* xr = reinterpret_cast<const float4*>(x + (size_t)t * x_stride);
+  float4 v[kQuantVecs];
+#pragma unroll
+  for (int j = 0; j < kQuantVecs; ++j) {
+    const int k = threadIdx.x + 256 * j;
+    v[j] = k < n4 ? xr[k] : make_float4(0, 0, 0, 0);
+  }
   if (norm == kNormDecode) {
     double ss = 0.0;
-    for (int k = threadIdx.x; k < n; k += 256) ss += (double)row[k] * (double)row[k];
+#pragma unroll
+    for (int j = 0; j < kQuantVecs; ++j)
+      ss += (double)v[j].x * v[j].x + (double)v[j].y * v[j].y + (double)v[j].z * v[j].z + (double)v[j].w * v[j].w;
     ss = block_sum4_d(ss, red_d);
     const double inv = 1.0 / sqrt(ss / (double)n + (double)QWEN_RMS_EPS);
-    for (int k = threadIdx.x; k < n; k += 256) row[k] = (float)((double)row[k] * inv * (double)w[k]);
+    const float4* w4 = reinterpret_cast<const float4*>(w);
+#pragma unroll
+    for (int j = 0; j < kQuantVecs; ++j) {
+      const int k = threadIdx.x + 256 * j;
+      if (k < n4) {
+        const float4 ww = w4[k];
+        v[j] = make_float4((float)((double)v[j].x * inv * ww.x), (float)((double)v[j].y * inv * ww.y),
+                           (float)((double)v[j].z * inv * ww.z), (float)((double)v[j].w * inv * ww.w));
+      }
+    }
   } else if (norm == kNormPrefill) {
     float ss = 0.0f;
-    for (int k = threadIdx.x; k < n; k += 256) ss += row[k] * row[k];
+#pragma unroll
+    for (int j = 0; j < kQuantVecs; ++j) ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
     ss = block_sum4(ss, red_f);
     const float inv = 1.0f / approx_sqrt(ss / (float)n + QWEN_RMS_EPS);
-    for (int k = threadIdx.x; k < n; k += 256) row[k] = row[k] * inv * w[k];
+    const float4* w4 = reinterpret_cast<const float4*>(w);
+#pragma unroll
+    for (int j = 0; j < kQuantVecs; ++j) {
+      const int k = threadIdx.x + 256 * j;
+      if (k < n4) {
+        const float4 ww = w4[k];
+        v[j] = make_float4(v[j].x * inv * ww.x, v[j].y * inv * ww.y, v[j].z * inv * ww.z, v[j].w * inv * ww.w);
+      }
+    }
   }
-  __syncthreads();
-  if (xn)
-    for (int k = threadIdx.x; k < n; k += 256) xn[(size_t)t * n + k] = row[k];
-  quantize_row_lds(row, n, xq + (size_t)t * (size_t)(2 * n), sx + t, sums + 2 * t, red_f, red_i);
+  if (xn) {
+    float4* xo = reinterpret_cast<float4*>(xn + (size_t)t * n);
+#pragma unroll
+    for (int j = 0; j < kQuantVecs; ++j) {
+      const int k = threadIdx.x + 256 * j;
+      if (k < n4) xo[k] = v[j];
+    }
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < kQuantVecs; ++j)
+    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
+  amax = block_max4(amax, red_f);
+  const float inv = amax > 0.0f ? (float)kQuantMax / amax : 0.0f;
+  int8_t* row = xq + (size_t)t * (size_t)(2 * n);
+  int sh = 0, sl = 0;
+#pragma unroll
+  for (int j = 0; j < kQuantVecs; ++j) {
+    const int k = threadIdx.x + 256 * j;
+    if (k < n4) {
+      const float e[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+      uint32_t hw = 0, lw = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float xf = fminf(fmaxf(rintf(e[q] * inv), -(float)kQuantMax), (float)kQuantMax);
+        const int X = (int)xf;
+        const int H = (X + 128) >> 8;
+        const int L = X - (H << 8);
+        hw |= (uint32_t)(H & 0xFF) << (8 * q);
+        lw |= (uint32_t)(L & 0xFF) << (8 * q);
+        sh += H;
+        sl += L;
+      }
+      const int base = ((4 * k) >> 7) * 256 + ((4 * k) & 127);
+      *reinterpret_cast<uint32_t*>(row + base) = hw;
+      *reinterpret_cast<uint32_t*>(row + base + 128) = lw;
+    }
+  }
+  sh = block_sum4_i(sh, red_i);
+  sl = block_sum4_i(sl, red_i);
+  if (threadIdx.x == 0) {
+    sx[t] = amax > 0.0f ? amax / (float)kQuantMax : 1.0f;
+    sums[2 * t] = sh;
+    sums[2 * t + 1] = sl;
+  }
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -406,36 +473,90 @@ __global__ void __launch_bounds__(256) gemm_i8_kernel(GemmArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// The same GEMM for many tokens: the activation tile of a K chunk (16*NT tokens x 256 bytes of
-// limbs) is staged once per block in LDS (double-buffered, rows padded by 16 bytes so the 16
-// token rows a lane group reads fall on distinct banks) and shared by all waves; each wave covers
-// RTW row tiles, so every B operand read from LDS feeds RTW (x2 for DUAL) matrix-core products.
-// KSPLIT groups of waves split the K chunks; their int32 partial sums are added through LDS
-// (exact).  Block: 4 waves = (4/KSPLIT) row groups x KSPLIT; rows per block = 16*RTW*(4/KSPLIT).
-// grid = (ceil(tokens / (16*NT)), ceil(row_tiles / (RTW*4/KSPLIT))).  Requires (in/128) % KSPLIT == 0.
+// Pipelined many-token GEMM.  Both operands of every K chunk reach LDS through direct
+// global->LDS loads (global_load_lds_dwordx4, 16 bytes per lane, no VGPR round trip), NBUF
+// chunks deep, so one wave keeps NBUF-1 chunks in flight while the matrix cores consume the
+// oldest.  Per chunk and wave: NT loads of activation rows (the block's TOK rows are split over
+// the 4 waves, 4 rows of 256 bytes per load) and RTW*D loads of the wave's own weight tiles.
+// Activation rows are XOR-swizzled by 16-byte segment (LDS segment s holds global segment
+// s ^ (row & 15)), so the 16 lanes of a lane group read 16 token rows on 16 distinct bank groups.
+// Every vector-memory instruction of the loop is one of these loads, issued in chunk order, so
+// `s_waitcnt vmcnt(n)` with n = loads issued after chunk i is exactly "chunk i has landed"; a
+// barrier then makes every wave's part visible and frees the buffer refilled next.
+// gridDim.z > 1 splits the K chunks over blocks: each block writes fp32 partials
+// sw*sx*(256*sumH + sumL) of its chunks to a.part[z][tok][row], and gemm_splitk_reduce_kernel adds
+// them in z order, applies the -8*sum(X) correction and the epilogue.
+// grid = (ceil(tokens/(16*NT)), ceil(row_tiles/(4*RTW)), splits), block = 256.
 // ---------------------------------------------------------------------------------------------
-constexpr int kXRowPitch = 256 + 16;  // LDS bytes per staged token row (two limbs of one K chunk)
+template <int VMCNT>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(VMCNT >= 0 && VMCNT < 64, "vmcnt out of range");
+  // gfx9 s_waitcnt: vmcnt[3:0] | expcnt[6:4] (7 = no wait) | lgkmcnt[11:8] (15 = no wait) | vmcnt[5:4] << 14
+  __builtin_amdgcn_s_waitcnt((VMCNT & 0xF) | (0x7 << 4) | (0xF << 8) | ((VMCNT >> 4) << 14));
+}
 
-template <int NT, int RTW, int KSPLIT, int EPI, bool DUAL>
-__global__ void __launch_bounds__(256) gemm_i8_lds_kernel(GemmArgs a) {
-  constexpr int GROUPS = 4 / KSPLIT;                 // row groups per block
-  constexpr int TOK = 16 * NT;                       // tokens per block
-  constexpr int STAGE = TOK * kXRowPitch;            // bytes of one staged chunk
+template <int NT, int RTW, int NBUF, int EPI, bool DUAL>
+__global__ void __launch_bounds__(256) gemm_i8_pipe_kernel(GemmArgs a) {
   constexpr int D = DUAL ? 2 : 1;
-  __shared__ __align__(16) uint8_t xs[KSPLIT][2][STAGE];
+  constexpr int TOK = 16 * NT;
+  constexpr int XB = TOK * 256;                 // activation bytes per stage
+  constexpr int WB = 4 * RTW * D * 1024;        // weight bytes per stage (4 waves)
+  constexpr int OPS = NT + RTW * D;             // direct loads per chunk per wave
+  static_assert(NBUF == 4, "the stage arrays below are written out for 4 stages");
+  static_assert((NBUF - 2) * OPS < 64, "pipeline depth");
+  // One LDS object per stage and operand: the compiler tracks direct-load writes per object, so
+  // reads of one stage do not wait for loads still landing in the others.
+  __shared__ __align__(16) uint8_t xs0[XB], xs1[XB], xs2[XB], xs3[XB];
+  __shared__ __align__(16) uint8_t ws0[WB], ws1[WB], ws2[WB], ws3[WB];
+  uint8_t* const XS[4] = {xs0, xs1, xs2, xs3};
+  uint8_t* const WS[4] = {ws0, ws1, ws2, ws3};
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int grp = wave / KSPLIT;   // row group
-  const int ks = wave % KSPLIT;    // K split of this wave
   const int g = lane >> 4;
   const int col = lane & 15;
   const int row_tiles = a.out_dim / 16;
-  const int rt0 = (blockIdx.y * GROUPS + grp) * RTW;
-  const int nkc = a.in_dim / kKChunk;
-  const int per = nkc / KSPLIT;
-  const int kc_begin = ks * per;
+  const int rt0 = (blockIdx.y * 4 + wave) * RTW;
+  const int nkc_all = a.in_dim / kKChunk;
+  const int nch = nkc_all / gridDim.z;
+  const int kc0 = blockIdx.z * nch;
   const int tok0 = blockIdx.x * TOK;
   const size_t row_stride_x = (size_t)a.in_dim * 2u;
+
+  // per-lane global sources (chunk offsets are added per issue)
+  const uint8_t* xsrc[NT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+    const int r = (wave * NT + j) * 4 + (lane >> 4);  // activation row (token) this lane loads
+    const int seg = (lane & 15) ^ (r & 15);
+    const int tok = min(tok0 + r, a.tokens - 1);      // rows past the last token reload a valid row
+    xsrc[j] = reinterpret_cast<const uint8_t*>(a.xq) + (size_t)tok * row_stride_x + seg * 16;
+  }
+  const uint8_t* wsrc[D][RTW];
+  bool rt_ok[RTW];
+#pragma unroll
+  for (int r = 0; r < RTW; ++r) {
+    rt_ok[r] = rt0 + r < row_tiles;
+    const size_t off = (((size_t)(rt_ok[r] ? rt0 + r : 0) * nkc_all) * 64u + lane) * 16u;
+    wsrc[0][r] = a.wp + off;
+    if (DUAL) wsrc[D - 1][r] = a.wp2 + off;
+  }
+  // chunk kc0 + i into one stage; past the last chunk the last one is loaded again into a stage
+  // nobody reads, which keeps the number of loads per iteration constant (and the waits exact)
+  auto issue = [&](int i, uint8_t* xst, uint8_t* wst) {
+    const int kc = kc0 + min(i, nch - 1);
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(xsrc[j] + (size_t)kc * 256u),
+                                       (__attribute__((address_space(3))) void*)(xst + (wave * NT + j) * 1024), 16, 0,
+                                       0);
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+#pragma unroll
+      for (int r = 0; r < RTW; ++r)
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(wsrc[d][r] + (size_t)kc * 1024u),
+                                         (__attribute__((address_space(3))) void*)(wst + ((wave * D + d) * RTW + r) * 1024),
+                                         16, 0, 0);
+  };
 
   v4i accH[D][RTW][NT], accL[D][RTW][NT];
 #pragma unroll
@@ -445,126 +566,51 @@ __global__ void __launch_bounds__(256) gemm_i8_lds_kernel(GemmArgs a) {
 #pragma unroll
       for (int n = 0; n < NT; ++n) accH[d][r][n] = accL[d][r][n] = v4i{0, 0, 0, 0};
 
-  // Staging: the waves of split ks (KSPLIT == 1: all 4 waves; else the GROUPS waves with this ks)
-  // copy TOK rows x 256 bytes of chunk kc into xs[ks][buf]: loads are issued before the products
-  // of the current chunk and stored to LDS after them, so their latency overlaps the MFMAs.
-  constexpr int STAGERS = 64 * GROUPS;
-  constexpr int SPT = (TOK * 16 + STAGERS - 1) / STAGERS;  // 16-byte pieces per thread
-  const int stager_id = grp * 64 + lane;
-  uint4 sreg[SPT];
-  auto stage_load = [&](int kc) {
 #pragma unroll
-    for (int j = 0; j < SPT; ++j) {
-      const int e = stager_id + j * STAGERS;
-      const int t = e >> 4, part = e & 15;
-      const int tok = tok0 + t;
-      sreg[j] = (e < TOK * 16 && tok < a.tokens)
-                    ? *reinterpret_cast<const uint4*>(a.xq + (size_t)tok * row_stride_x + (size_t)kc * 256u + part * 16)
-                    : make_uint4(0, 0, 0, 0);
-    }
-  };
-  auto stage_store = [&](int buf) {
+  for (int i = 0; i < NBUF - 1; ++i) issue(i, XS[i], WS[i]);
+  for (int i0 = 0; i0 < nch; i0 += NBUF) {
 #pragma unroll
-    for (int j = 0; j < SPT; ++j) {
-      const int e = stager_id + j * STAGERS;
-      if (e < TOK * 16) *reinterpret_cast<uint4*>(&xs[ks][buf][(e >> 4) * kXRowPitch + (e & 15) * 16]) = sreg[j];
-    }
-  };
-  const uint4* wp[D][RTW];
-  bool rt_ok[RTW];
+    for (int sidx = 0; sidx < NBUF; ++sidx) {
+      const int i = i0 + sidx;
+      if (i < nch) {
+        // exactly NBUF-2 chunks were issued after chunk i: waiting for all but their loads means
+        // chunk i has landed (this wave's part); the barrier covers the other waves' parts and
+        // frees stage sidx-1, which the next issue refills.
+        wait_vmcnt<(NBUF - 2) * OPS>();
+        __builtin_amdgcn_s_barrier();
+        issue(i + NBUF - 1, XS[(sidx + NBUF - 1) % NBUF], WS[(sidx + NBUF - 1) % NBUF]);
+        const uint8_t* xst = XS[sidx];
+        const uint8_t* wst = WS[sidx];
+        v4i a1[D][RTW], a2[D][RTW];
 #pragma unroll
-  for (int r = 0; r < RTW; ++r) {
-    rt_ok[r] = rt0 + r < row_tiles;
-    const size_t off = ((size_t)(rt_ok[r] ? rt0 + r : 0) * nkc) * 64u + lane;
-    wp[0][r] = reinterpret_cast<const uint4*>(a.wp) + off;
-    if (DUAL) wp[D - 1][r] = reinterpret_cast<const uint4*>(a.wp2) + off;
-  }
-  uint4 wcur[D][RTW], wnext[D][RTW];
+        for (int d = 0; d < D; ++d)
 #pragma unroll
-  for (int d = 0; d < D; ++d)
+          for (int r = 0; r < RTW; ++r)
+            unpack16(*reinterpret_cast<const uint4*>(wst + ((wave * D + d) * RTW + r) * 1024 + lane * 16), a1[d][r],
+                     a2[d][r]);
 #pragma unroll
-    for (int r = 0; r < RTW; ++r) wcur[d][r] = ld_stream(wp[d][r] + (size_t)kc_begin * 64u);
-  stage_load(kc_begin);
-  stage_store(0);
-  __syncthreads();
-  for (int i = 0; i < per; ++i) {
-    const int kc = kc_begin + i;
-    const int buf = i & 1;
-    if (i + 1 < per) {
-      stage_load(kc + 1);
+        for (int n = 0; n < NT; ++n) {
+          const uint8_t* xr = xst + (n * 16 + col) * 256;
+          const v4i bh1 = *reinterpret_cast<const v4i*>(xr + (((2 * g) ^ col) << 4));
+          const v4i bh2 = *reinterpret_cast<const v4i*>(xr + (((2 * g + 1) ^ col) << 4));
+          const v4i bl1 = *reinterpret_cast<const v4i*>(xr + (((8 + 2 * g) ^ col) << 4));
+          const v4i bl2 = *reinterpret_cast<const v4i*>(xr + (((9 + 2 * g) ^ col) << 4));
 #pragma unroll
-      for (int d = 0; d < D; ++d)
+          for (int d = 0; d < D; ++d)
 #pragma unroll
-        for (int r = 0; r < RTW; ++r) wnext[d][r] = ld_stream(wp[d][r] + (size_t)(kc + 1) * 64u);
-    }
-    v4i a1[D][RTW], a2[D][RTW];
-#pragma unroll
-    for (int d = 0; d < D; ++d)
-#pragma unroll
-      for (int r = 0; r < RTW; ++r) unpack16(wcur[d][r], a1[d][r], a2[d][r]);
-    const uint8_t* xb = &xs[ks][buf][col * kXRowPitch + 32 * g];
-#pragma unroll
-    for (int n = 0; n < NT; ++n) {
-      const v4i* p = reinterpret_cast<const v4i*>(xb + n * 16 * kXRowPitch);
-      const v4i bh1 = p[0], bh2 = p[1], bl1 = p[8], bl2 = p[9];
-#pragma unroll
-      for (int d = 0; d < D; ++d)
-#pragma unroll
-        for (int r = 0; r < RTW; ++r) {
-          accH[d][r][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[d][r], bh1, accH[d][r][n], 0, 0, 0);
-          accH[d][r][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2[d][r], bh2, accH[d][r][n], 0, 0, 0);
-          accL[d][r][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[d][r], bl1, accL[d][r][n], 0, 0, 0);
-          accL[d][r][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2[d][r], bl2, accL[d][r][n], 0, 0, 0);
+            for (int r = 0; r < RTW; ++r) {
+              accH[d][r][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[d][r], bh1, accH[d][r][n], 0, 0, 0);
+              accH[d][r][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2[d][r], bh2, accH[d][r][n], 0, 0, 0);
+              accL[d][r][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[d][r], bl1, accL[d][r][n], 0, 0, 0);
+              accL[d][r][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2[d][r], bl2, accL[d][r][n], 0, 0, 0);
+            }
         }
-    }
-#pragma unroll
-    for (int d = 0; d < D; ++d)
-#pragma unroll
-      for (int r = 0; r < RTW; ++r) wcur[d][r] = wnext[d][r];
-    if (i + 1 < per) stage_store(buf ^ 1);
-    __syncthreads();
-  }
-
-  if (KSPLIT > 1) {
-    // splits 1.. hand their partial sums to split 0 of the same row group through LDS.
-    constexpr int NACC = D * RTW * NT * 8;
-    static_assert((KSPLIT - 1) * GROUPS * NACC * 64 * 4 <= (int)sizeof(xs), "reduction does not fit");
-    int* red = reinterpret_cast<int*>(&xs[0][0][0]);
-    if (ks > 0) {
-      int* dst = red + (((ks - 1) * GROUPS + grp) * NACC) * 64 + lane;
-      int idx = 0;
-#pragma unroll
-      for (int d = 0; d < D; ++d)
-#pragma unroll
-        for (int r = 0; r < RTW; ++r)
-#pragma unroll
-          for (int n = 0; n < NT; ++n)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              dst[(idx++) * 64] = accH[d][r][n][q];
-              dst[(idx++) * 64] = accL[d][r][n][q];
-            }
-    }
-    __syncthreads();
-    if (ks > 0) return;
-#pragma unroll
-    for (int s2 = 0; s2 < KSPLIT - 1; ++s2) {
-      const int* src = red + ((s2 * GROUPS + grp) * NACC) * 64 + lane;
-      int idx = 0;
-#pragma unroll
-      for (int d = 0; d < D; ++d)
-#pragma unroll
-        for (int r = 0; r < RTW; ++r)
-#pragma unroll
-          for (int n = 0; n < NT; ++n)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              accH[d][r][n][q] += src[(idx++) * 64];
-              accL[d][r][n][q] += src[(idx++) * 64];
-            }
+      }
     }
   }
+  wait_vmcnt<0>();  // the trailing reloads land before the wave moves on
 
+  const bool partial = gridDim.z > 1;
 #pragma unroll
   for (int r = 0; r < RTW; ++r) {
     if (!rt_ok[r]) continue;
@@ -581,9 +627,17 @@ __global__ void __launch_bounds__(256) gemm_i8_lds_kernel(GemmArgs a) {
       const int tok = tok0 + n * 16 + col;
       if (tok >= a.tokens) continue;
       const double sx = (double)a.sx[tok];
+      float out[4];
+      if (partial) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          out[q] = (float)(((double)accH[0][r][n][q] * 256.0 + (double)accL[0][r][n][q]) * sx) * sw[q];
+        *reinterpret_cast<float4*>(a.part + ((size_t)blockIdx.z * a.tokens + tok) * a.out_dim + row0) =
+            make_float4(out[0], out[1], out[2], out[3]);
+        continue;
+      }
       const int sh8 = 8 * a.sums[2 * tok];
       const int sl8 = 8 * a.sums[2 * tok + 1];
-      float out[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const double tot = (double)(accH[0][r][n][q] - sh8) * 256.0 + (double)(accL[0][r][n][q] - sl8);
@@ -607,6 +661,38 @@ __global__ void __launch_bounds__(256) gemm_i8_lds_kernel(GemmArgs a) {
       *reinterpret_cast<float4*>(a.y + (size_t)tok * a.y_stride + row0) = make_float4(out[0], out[1], out[2], out[3]);
     }
   }
+}
+
+// Sums the split partials in z order and applies the offset correction and the epilogue
+// (kEpiStore with bias, or kEpiResidual with bf16 rounding).  One thread per 4 outputs.
+template <int EPI>
+__global__ void __launch_bounds__(256) gemm_splitk_reduce_kernel(GemmArgs a, int splits) {
+  const size_t quads = (size_t)a.tokens * (a.out_dim / 4);
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= quads) return;
+  const int tok = (int)(i / (a.out_dim / 4));
+  const int row0 = (int)(i % (a.out_dim / 4)) * 4;
+  float4 acc = make_float4(0, 0, 0, 0);
+  for (int z = 0; z < splits; ++z) {
+    const float4 p = *reinterpret_cast<const float4*>(a.part + ((size_t)z * a.tokens + tok) * a.out_dim + row0);
+    acc.x += p.x;
+    acc.y += p.y;
+    acc.z += p.z;
+    acc.w += p.w;
+  }
+  const double corr = -8.0 * (256.0 * (double)a.sums[2 * tok] + (double)a.sums[2 * tok + 1]) * (double)a.sx[tok];
+  float out[4] = {acc.x, acc.y, acc.z, acc.w};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float v = out[q] + (float)(corr * (double)a.sw[row0 + q]);
+    if (EPI == kEpiResidual) {
+      const float o = a.resid[(size_t)tok * a.resid_stride + row0 + q] + v;
+      out[q] = a.round_bf16 ? round_bf16(o) : o;
+    } else {
+      out[q] = v + (a.bias ? a.bias[row0 + q] : 0.0f);
+    }
+  }
+  *reinterpret_cast<float4*>(a.y + (size_t)tok * a.y_stride + row0) = make_float4(out[0], out[1], out[2], out[3]);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -908,6 +994,7 @@ __global__ void __launch_bounds__(256) attn_decode_combine_kernel(const float* _
                                                                   float* __restrict__ sx, int* __restrict__ sums) {
   __shared__ float row[QWEN_HIDDEN];
   __shared__ float wgt[QWEN_Q_HEADS][kMaxChunks];
+  __shared__ float lsum[QWEN_Q_HEADS][kMaxChunks];
   __shared__ float gm[QWEN_Q_HEADS], ginv[QWEN_Q_HEADS];
   __shared__ float red_f[4];
   __shared__ int red_i[4];
@@ -915,25 +1002,33 @@ __global__ void __launch_bounds__(256) attn_decode_combine_kernel(const float* _
   const int n = min(max(pos[b], 0) + 1, max_keys);
   const int nc = min((n + kAttnChunk - 1) / kAttnChunk, nchunk);
   const float2* pb = pml + (size_t)b * QWEN_Q_HEADS * nchunk;
+  for (int i = threadIdx.x; i < QWEN_Q_HEADS * nc; i += 256) {
+    const int h = i / nc, c = i % nc;
+    const float2 v = pb[h * nchunk + c];
+    wgt[h][c] = v.x;  // chunk maxima first, replaced by the merge weights below
+    lsum[h][c] = v.y;
+  }
+  __syncthreads();
   if (threadIdx.x < QWEN_Q_HEADS) {
-    const float2* pm = pb + threadIdx.x * nchunk;
+    const int h = threadIdx.x;
     float M = -INFINITY;
-    for (int c = 0; c < nc; ++c) M = fmaxf(M, pm[c].x);
+    for (int c = 0; c < nc; ++c) M = fmaxf(M, wgt[h][c]);
     float L = 0.0f;
-    for (int c = 0; c < nc; ++c) L += pm[c].y * __expf(pm[c].x - M);
-    gm[threadIdx.x] = M;
-    ginv[threadIdx.x] = L > 0.0f ? 1.0f / L : 0.0f;
+    for (int c = 0; c < nc; ++c) L += lsum[h][c] * __expf(wgt[h][c] - M);
+    gm[h] = M;
+    ginv[h] = L > 0.0f ? 1.0f / L : 0.0f;
   }
   __syncthreads();
   for (int i = threadIdx.x; i < QWEN_Q_HEADS * nc; i += 256) {
     const int h = i / nc, c = i % nc;
-    wgt[h][c] = __expf(pb[h * nchunk + c].x - gm[h]) * ginv[h];
+    wgt[h][c] = __expf(wgt[h][c] - gm[h]) * ginv[h];
   }
   __syncthreads();
   for (int i = threadIdx.x; i < QWEN_HIDDEN; i += 256) {
     const int h = i / QWEN_HEAD_DIM, d = i % QWEN_HEAD_DIM;
     const float* pa = part + ((size_t)b * QWEN_Q_HEADS + h) * nchunk * QWEN_HEAD_DIM + d;
     float acc = 0.0f;
+#pragma unroll 4
     for (int c = 0; c < nc; ++c) acc += pa[(size_t)c * QWEN_HEAD_DIM] * wgt[h][c];
     row[i] = acc;
     if (ctx) ctx[(size_t)b * QWEN_HIDDEN + i] = acc;
@@ -1042,6 +1137,141 @@ __global__ void __launch_bounds__(256) attn_prefill_kernel(const float* __restri
     *reinterpret_cast<float4*>(op + d) = make_float4(acc[d] * inv, acc[d + 1] * inv, acc[d + 2] * inv, acc[d + 3] * inv);
 }
 
+// ---------------------------------------------------------------------------------------------
+// Causal prefill attention on the fp32 matrix cores (qwen_prefill_attention_kernel.cpp:204-289
+// semantics: keys 0..i for query i, scale 0.08838834764831845f, approx_exp; online softmax).
+// Block (query tile qt of 16 queries, KV head kvh, sequence sq) = 6 waves, one per query head
+// of the group; each 16-key K/V tile is staged once in LDS (rows padded to 528 bytes, double
+// buffered) and consumed by all 6 waves.  Per wave and key tile (lane: col = l & 15, g = l >> 4):
+//   S = K . Q^T: A = K[key col][dim 4g+16j+e], B = Q[query col][same dim]  -> S[key 4g+r][query col]
+//   P = approx_exp(S - m) per query column (mask keys > query on the diagonal tile)
+//   O += P . V:  A = P[query col][key 4g+r] (own registers), B = V[key 4g+r][dim 4 col+e+64h]
+// O ends in lane l as O[query 4g+r'][dim 4col+e+64h]; rows are divided by l(query) at the end.
+// q rows: qkv + (sq*S + i)*qkv_stride + h*128; K/V rows: cache + sq*seq_stride + j*256 + kvh*128;
+// ctx: [sq*S + i][1536].  grid = (ceil(S/16), 2, nseq), block = 384.
+// ---------------------------------------------------------------------------------------------
+constexpr int kPfRow = QWEN_HEAD_DIM + 4;  // LDS floats per staged K/V row (16-byte pad)
+
+__global__ void __launch_bounds__(384) attn_prefill_mfma_kernel(const float* __restrict__ qkv, int qkv_stride,
+                                                                const float* __restrict__ k_cache,
+                                                                const float* __restrict__ v_cache, size_t seq_stride,
+                                                                int S, float* __restrict__ ctx) {
+  __shared__ __align__(16) float ks[2][16][kPfRow];
+  __shared__ __align__(16) float vs[2][16][kPfRow];
+  const int qt = blockIdx.x;
+  const int kvh = blockIdx.y;
+  const int sq = blockIdx.z;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;  // query head within the group
+  const int col = lane & 15;
+  const int g = lane >> 4;
+  const int h = kvh * QWEN_GROUPS + wave;
+  const int q0 = qt * 16;
+  const float scaling = 0.08838834764831845f;
+
+  // Q operand: query q0 + col, dims 4g + 16j + e
+  float qr[32];
+  {
+    const int qi = min(q0 + col, S - 1);
+    const float* qp = qkv + ((size_t)sq * S + qi) * qkv_stride + h * QWEN_HEAD_DIM + 4 * g;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float4 q4 = *reinterpret_cast<const float4*>(qp + 16 * j);
+      qr[4 * j + 0] = q4.x * scaling;
+      qr[4 * j + 1] = q4.y * scaling;
+      qr[4 * j + 2] = q4.z * scaling;
+      qr[4 * j + 3] = q4.w * scaling;
+    }
+  }
+  const float* kb = k_cache + (size_t)sq * seq_stride + kvh * QWEN_HEAD_DIM;
+  const float* vb = v_cache + (size_t)sq * seq_stride + kvh * QWEN_HEAD_DIM;
+  const int ntiles = qt + 1;  // key tiles 0..qt (causal)
+
+  // staging: 16 rows x 32 float4 for K and for V = 1024 float4 over 384 threads
+  auto stage = [&](int t, int buf) {
+    for (int e = threadIdx.x; e < 1024; e += 384) {
+      const int which = e >> 9, r = (e >> 5) & 15, c4 = e & 31;
+      const int key = min(t * 16 + r, S - 1);
+      const float* src = (which ? vb : kb) + (size_t)key * QWEN_KV_WIDTH + 4 * c4;
+      const float4 v = *reinterpret_cast<const float4*>(src);
+      float* dst = which ? &vs[buf][r][4 * c4] : &ks[buf][r][4 * c4];
+      *reinterpret_cast<float4*>(dst) = v;
+    }
+  };
+
+  float m = -INFINITY, lp = 0.0f;
+  v4f acc[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) acc[k] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  stage(0, 0);
+  __syncthreads();
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    if (t + 1 < ntiles) stage(t + 1, buf ^ 1);
+    v4f sc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    const float* kr = &ks[buf][col][4 * g];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float4 k4 = *reinterpret_cast<const float4*>(kr + 16 * j);
+      sc = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.x, qr[4 * j + 0], sc, 0, 0, 0);
+      sc = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.y, qr[4 * j + 1], sc, 0, 0, 0);
+      sc = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.z, qr[4 * j + 2], sc, 0, 0, 0);
+      sc = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.w, qr[4 * j + 3], sc, 0, 0, 0);
+    }
+    // causal mask on the diagonal tile: key (t*16 + 4g + r) > query (q0 + col)
+    float mt = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int key = t * 16 + 4 * g + r;
+      if (key > q0 + col || key >= S) sc[r] = -INFINITY;
+      mt = fmaxf(mt, sc[r]);
+    }
+    mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));  // finite: key t*16 <= q0 + col for every query of the tile
+    const float mn = fmaxf(m, mt);
+    const float corr = approx_exp_fast(m - mn);
+    float p[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) p[r] = sc[r] == -INFINITY ? 0.0f : approx_exp_fast(sc[r] - mn);
+    lp = lp * corr + ((p[0] + p[1]) + (p[2] + p[3]));
+    m = mn;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const float cr = __shfl(corr, 4 * g + rr, 64);  // lane 4g + rr holds query column 4g + rr
+#pragma unroll
+      for (int k = 0; k < 8; ++k) acc[k][rr] *= cr;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float* vr = &vs[buf][4 * g + r][4 * col];
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const float4 v4 = *reinterpret_cast<const float4*>(vr + 64 * hh);
+        acc[4 * hh + 0] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[r], v4.x, acc[4 * hh + 0], 0, 0, 0);
+        acc[4 * hh + 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[r], v4.y, acc[4 * hh + 1], 0, 0, 0);
+        acc[4 * hh + 2] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[r], v4.z, acc[4 * hh + 2], 0, 0, 0);
+        acc[4 * hh + 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[r], v4.w, acc[4 * hh + 3], 0, 0, 0);
+      }
+    }
+    __syncthreads();  // buffer `buf` is refilled at t+1; the next tile's stage has landed
+  }
+  lp += __shfl_xor(lp, 16, 64);
+  lp += __shfl_xor(lp, 32, 64);
+  const float inv = lp > 0.0f ? 1.0f / lp : 0.0f;  // per query column col
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) {
+    const int qi = q0 + 4 * g + rr;
+    const float ir = __shfl(inv, 4 * g + rr, 64);
+    if (qi < S) {
+      float* op = ctx + ((size_t)sq * S + qi) * QWEN_HIDDEN + h * QWEN_HEAD_DIM + 4 * col;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+        *reinterpret_cast<float4*>(op + 64 * hh) = make_float4(acc[4 * hh + 0][rr] * ir, acc[4 * hh + 1][rr] * ir,
+                                                                acc[4 * hh + 2][rr] * ir, acc[4 * hh + 3][rr] * ir);
+    }
+  }
+}
+
 // bf16 rounding of the driver between layers (verification/reference_wrapper_backend.py:40-46).
 __global__ void round_bf16_kernel(float* __restrict__ x, size_t n) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -1068,30 +1298,54 @@ static void launch_gemm_t(const GemmArgs& a, hipStream_t st) {
   hipLaunchKernelGGL((gemm_i8_kernel<NT, KSPLIT, EPI, DUAL>), grid, dim3(256), 0, st, a);
 }
 
-template <int NT, int RTW, int KSPLIT, int EPI, bool DUAL>
-static void launch_gemm_lds_t(const GemmArgs& a, hipStream_t st) {
-  constexpr int GROUPS = 4 / KSPLIT;
+template <int NT, int RTW, int NBUF, int EPI, bool DUAL>
+static void launch_gemm_pipe_t(const GemmArgs& a, int splits, hipStream_t st) {
   const int row_tiles = a.out_dim / 16;
-  const int rows_per_block = RTW * GROUPS;
-  const dim3 grid((a.tokens + 16 * NT - 1) / (16 * NT), (row_tiles + rows_per_block - 1) / rows_per_block);
-  hipLaunchKernelGGL((gemm_i8_lds_kernel<NT, RTW, KSPLIT, EPI, DUAL>), grid, dim3(256), 0, st, a);
+  const dim3 grid((a.tokens + 16 * NT - 1) / (16 * NT), (row_tiles + 4 * RTW - 1) / (4 * RTW), splits);
+  hipLaunchKernelGGL((gemm_i8_pipe_kernel<NT, RTW, NBUF, EPI, DUAL>), grid, dim3(256), 0, st, a);
+  if (splits > 1) {
+    const size_t quads = (size_t)a.tokens * (a.out_dim / 4);
+    hipLaunchKernelGGL((gemm_splitk_reduce_kernel<EPI>), dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, st, a,
+                       splits);
+  }
 }
 
-// Shape dispatch.  <= 16 tokens: direct-load kernel, 4-way K split per row tile (many small
-// blocks, weights streamed once).  17..64 tokens: LDS-staged activations for all tokens of the
-// block, 2 row groups x 2-way K split.  More tokens (prefill): 4 row tiles per wave.
+// Largest divisor of nkc that is <= want (K chunks split evenly over blocks).
+static int split_for(int nkc, int want) {
+  for (int s = want < kMaxSplits ? want : kMaxSplits; s > 1; --s)
+    if (nkc % s == 0) return s;
+  return 1;
+}
+
+// Shape dispatch (the split-K workspace a.part, when given, holds kMaxSplits x kSplitTokens x
+// out_dim floats).  <= 16 tokens: direct-load kernel, 4-way in-block K split per row tile (many
+// small blocks, weights streamed once).  More tokens: the pipelined LDS kernel; projections whose
+// row tiles alone give fewer than ~256 blocks are also split over K across blocks (needs a.part).
 template <int EPI, bool DUAL>
 static void launch_gemm_epi(const GemmArgs& a, hipStream_t st) {
   const int nkc = a.in_dim / kKChunk;
+  const int row_tiles = a.out_dim / 16;
   if (a.tokens <= 16) {
     launch_gemm_t<1, 4, EPI, DUAL>(a, st);
-  } else if (a.tokens <= 64 && nkc % 2 == 0) {
-    launch_gemm_lds_t<4, 1, 2, EPI, DUAL>(a, st);
-  } else {
-    if constexpr (DUAL)
-      launch_gemm_lds_t<4, 2, 1, EPI, DUAL>(a, st);
+    return;
+  }
+  if constexpr (DUAL) {
+    if (a.tokens <= 64)
+      launch_gemm_pipe_t<4, 1, 4, EPI, DUAL>(a, 1, st);
     else
-      launch_gemm_lds_t<4, 4, 1, EPI, DUAL>(a, st);
+      launch_gemm_pipe_t<4, 2, 4, EPI, DUAL>(a, 1, st);
+  } else {
+    if (a.tokens <= 64) {
+      const int blocks = (row_tiles + 3) / 4;
+      const int splits = a.part ? split_for(nkc, (256 + blocks - 1) / blocks) : 1;
+      launch_gemm_pipe_t<4, 1, 4, EPI, DUAL>(a, splits, st);  // a.part holds >= kSplitTokens rows
+    } else {
+      const int token_tiles = (a.tokens + 63) / 64;
+      const int blocks = token_tiles * ((row_tiles + 15) / 16);
+      const int splits =
+          (a.part && a.tokens <= kSplitTokens && blocks < 256) ? split_for(nkc, (256 + blocks - 1) / blocks) : 1;
+      launch_gemm_pipe_t<4, 4, 4, EPI, DUAL>(a, splits, st);
+    }
   }
 }
 
@@ -1130,7 +1384,7 @@ void launch_attn_decode_partial_only(const float* qkv, int qkv_stride, const flo
 
 void launch_attn_prefill(const float* qkv, int qkv_stride, const float* k_cache, const float* v_cache,
                          size_t seq_stride, int S, int nseq, float* ctx, hipStream_t st) {
-  hipLaunchKernelGGL(attn_prefill_kernel, dim3((S + 63) / 64, QWEN_Q_HEADS, nseq), dim3(256), 0, st, qkv,
+  hipLaunchKernelGGL(attn_prefill_mfma_kernel, dim3((S + 15) / 16, QWEN_KV_HEADS, nseq), dim3(384), 0, st, qkv,
                      qkv_stride, k_cache, v_cache, seq_stride, S, ctx);
 }
 

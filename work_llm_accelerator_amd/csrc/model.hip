@@ -79,6 +79,7 @@ struct qwen_hip_model {
     int* sums;
     float *qkv, *ctx, *att, *s, *tmp, *part;
     float2* pml;
+    float* splitk;  // K-split partials of the non-dual projections (out <= 2048)
   };
   Ws carve(size_t tokens, size_t batch, size_t nchunk) {
     size_t off = 0;
@@ -97,12 +98,14 @@ struct qwen_hip_model {
     const size_t o_tmp = take(tokens * QWEN_INTERMEDIATE * 4u);
     const size_t o_part = take(batch * QWEN_Q_HEADS * nchunk * QWEN_HEAD_DIM * 4u);
     const size_t o_pml = take(batch * QWEN_Q_HEADS * nchunk * 8u);
+    const size_t o_splitk = take(splitk_bytes(kQkvRows));
     char* b = static_cast<char*>(ws.get(off));
     return Ws{reinterpret_cast<int8_t*>(b + o_xq), reinterpret_cast<float*>(b + o_sx),
               reinterpret_cast<int*>(b + o_sums), reinterpret_cast<float*>(b + o_qkv),
               reinterpret_cast<float*>(b + o_ctx), reinterpret_cast<float*>(b + o_att),
               reinterpret_cast<float*>(b + o_s), reinterpret_cast<float*>(b + o_tmp),
-              reinterpret_cast<float*>(b + o_part), reinterpret_cast<float2*>(b + o_pml)};
+              reinterpret_cast<float*>(b + o_part), reinterpret_cast<float2*>(b + o_pml),
+              reinterpret_cast<float*>(b + o_splitk)};
   }
 
   DevLayer dev_layer(int l) const {
@@ -212,6 +215,7 @@ struct qwen_hip_model {
     g.y_raw = nullptr;
     g.round_bf16 = round;
     g.prefill_silu = prefill_silu;
+    g.part = wp2 ? nullptr : w.splitk;
     launch_gemm_i8(g, epi, stream);
   }
 
