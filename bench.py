@@ -157,10 +157,11 @@ def bench_decode(args, torch, batch: int, history: int, seed: int) -> dict:
                             "achieved_GBs": step_bytes / (ms_step * 1e-3) / 1e9,
                             "frac": step_bytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS}
     if mode == MODE_FAST:
-        # dominant kernel: decode attention over the KV cache (96% of the step's bytes at 64 x 4096)
+        # dominant kernel: decode attention over the KV cache (96% of the step's bytes at 64 x 4096),
+        # including its fused split merge and O-projection input quantization
         attn_ms = model.time_kernel(KERNEL_ATTN_DECODE, 0, 20)
         attn_bytes = kv_read + batch * 1536 * 4
-        res["roofline"] = {"bound": "hbm", "kernel": "attn_decode_partial_kernel", "achieved":
+        res["roofline"] = {"bound": "hbm", "kernel": "attn_decode_kernel", "achieved":
                            attn_bytes / (attn_ms * 1e-3) / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                            "frac": attn_bytes / (attn_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "traffic": None,
                            "avg_launch_us": attn_ms * 1e3, "algorithmic_bytes_per_launch": attn_bytes}

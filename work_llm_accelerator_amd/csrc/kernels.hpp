@@ -24,8 +24,7 @@ void launch_attention_ordered(const float* q, const float* k_cache, const float*
 constexpr int kKChunk = 128;        // K values per repacked weight chunk
 constexpr int kQuantMax = 32512;    // |X| bound of the two-limb activation code (127 * 256)
 constexpr int kMaxQuantRow = 8960;  // widest activation row that is quantized
-constexpr int kAttnChunk = 256;     // keys per decode-attention block
-constexpr int kMaxChunks = (32768 + kAttnChunk - 1) / kAttnChunk;  // chunks of the longest KV
+constexpr int kAttnMaxSplits = 64;  // most KV splits of one decode-attention sequence
 constexpr int kNormNone = 0, kNormDecode = 1, kNormPrefill = 2;
 constexpr int kEpiStore = 0, kEpiSiluMul = 1, kEpiResidual = 2;
 
@@ -64,12 +63,19 @@ void launch_norm_quant(const float* x, size_t x_stride, int rows, int n, const f
 void launch_gemm_i8(const GemmArgs& a, int epi, hipStream_t st);
 void launch_rope_qkv(float* qkv, int qkv_stride, const int* pos, int seq_len, int limit, int tokens,
                      const float* rope, float* k_cache, float* v_cache, size_t seq_stride, hipStream_t st);
+// Decode attention split: nsplit blocks of `chunk` keys (a multiple of 16) per sequence and KV
+// head, sized so that one launch fills the device once.  Workspace: part [batch][12][nsplit][128]
+// floats, pml [batch][12][nsplit] (m, l) pairs, arrivals [batch] counters that must be zero before
+// the first launch (every launch leaves them at zero).
+struct AttnDecodePlan {
+  int nsplit, chunk;
+};
+AttnDecodePlan plan_attn_decode(int batch, int max_keys);
+void launch_zero_u32(unsigned* p, int n, hipStream_t st);
 void launch_attn_decode(const float* qkv, int qkv_stride, const float* k_cache, const float* v_cache,
-                        size_t seq_stride, const int* pos, int batch, int max_keys, float* part, float2* pml,
-                        float* ctx, int8_t* xq, float* sx, int* sums, hipStream_t st);
-void launch_attn_decode_partial_only(const float* qkv, int qkv_stride, const float* k_cache, const float* v_cache,
-                                     size_t seq_stride, const int* pos, int batch, int max_keys, float* part,
-                                     float2* pml, hipStream_t st);
+                        size_t seq_stride, const int* pos, int batch, int max_keys, const AttnDecodePlan& plan,
+                        float* part, float2* pml, unsigned* arrivals, float* ctx, int8_t* xq, float* sx, int* sums,
+                        hipStream_t st);
 void launch_attn_prefill(const float* qkv, int qkv_stride, const float* k_cache, const float* v_cache,
                          size_t seq_stride, int S, int nseq, float* ctx, hipStream_t st);
 void launch_round_bf16(float* x, size_t n, hipStream_t st);

@@ -41,6 +41,14 @@ __device__ __forceinline__ float2 ld_stream(const float2* p) {
   return make_float2(v[0], v[1]);
 }
 
+// Device-coherent (agent-scope) store and load: visible across XCDs without an L2 write-back.
+__device__ __forceinline__ void store_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_agent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // ---------------------------------------------------------------------------------------------
 // Weight repack.  Reference layout: W[o][i] is the nibble at byte (o*in + i)/2, low nibble for
 // an even flat index, value q in [-8,7] stored as q & 15 (qwen_decode_attention_kernel.cpp:44-60).
@@ -737,126 +745,108 @@ __global__ void __launch_bounds__(64) rope_qkv_kernel(float* __restrict__ qkv, i
 }
 
 // ---------------------------------------------------------------------------------------------
-// Decode attention, split over the KV length.  Block (chunk c, KV head kvh, sequence b) handles
-// keys [c*256, min(n, c*256+256)) of sequence b (n = pos[b] + 1) for the 6 query heads of kvh:
-//   m_h = max_t s_ht, l_h = sum_t exp(s_ht - m_h), acc_h = sum_t exp(s_ht - m_h) v_t,
-// with s_ht = (q_h . k_t) * 0.08838834764831845f.  Partials go to part[b][h][c][128] and
-// pml[b][h][c] = (m, l); attn_decode_combine merges the chunks.  block = 256.
+// Decode attention on the fp32 matrix cores, split over the KV length, with the split merge and
+// the O-projection input quantization fused in (qwen_decode_attention_kernel.cpp:113-162 semantics:
+// s_t = (q . k_t) * 0.08838834764831845f over keys 0..pos, softmax, ctx = sum_t p_t v_t; here with
+// an online softmax, reordered sums and __expf).
+// grid = (nsplit, 2 KV heads, batch), block = 256 (4 waves).  Block (split c, KV head kvh, sequence
+// b) takes keys [c*chunk, min(n, c*chunk + chunk)) of sequence b, n = min(pos[b] + 1, max_keys);
+// wave w takes the 16-key tiles w, w+4, w+8, ... of that range.  Per tile (lane: col = lane & 15,
+// g = lane >> 4):
+//   S = K . Q^T:  A = K[key col][dim 4g+16j+e] (streamed from HBM, 64 contiguous bytes per key per
+//                 load), B = Q[head col][same dim] (LDS; heads >= 6 are zero rows), 32 MFMAs;
+//                 lane gets S[key 4g+r][head col], r = 0..3;
+//   online softmax per head col (max over the tile's keys: registers + xor-shuffles 16, 32);
+//   O += P . V:   MFMA (r, h, e): A = P[head col][key 4g+r] (the lane's own p[r]),
+//                 B = V[key 4g+r][dim 4col+e+64h]; lane holds O[head 4g+r'][dim 4col+e+64h].
+// The block merges its 4 waves in LDS and writes (m, l, acc[128]) per query head to
+// part[b][head][c][128] and pml[b][head][c] with device-coherent stores and counts itself in
+// arrivals[b]; the last of the sequence's 2*nsplit blocks to arrive merges the sequence's splits
+// into ctx[b] (optional), quantizes that row for the O projection (xq, sx, sums) and re-arms
+// arrivals[b] to 0 for the next launch.
 // ---------------------------------------------------------------------------------------------
-__global__ void __launch_bounds__(256) attn_decode_partial_kernel(const float* __restrict__ qkv, int qkv_stride,
-                                                                  const float* __restrict__ k_cache,
-                                                                  const float* __restrict__ v_cache,
-                                                                  size_t seq_stride, const int* __restrict__ pos,
-                                                                  float* __restrict__ part, float2* __restrict__ pml,
-                                                                  int nchunk, int max_keys) {
-  __shared__ __align__(16) float qs[QWEN_GROUPS][QWEN_HEAD_DIM];
-  __shared__ float ps[QWEN_GROUPS][kAttnChunk];
-  __shared__ float red[4][QWEN_GROUPS][QWEN_HEAD_DIM];
-  __shared__ float hm[QWEN_GROUPS], hl[QWEN_GROUPS];
-  const int c = blockIdx.x;
-  const int kvh = blockIdx.y;
-  const int b = blockIdx.z;
-  const int tid = threadIdx.x;
-  const int n = min(max(pos[b], 0) + 1, max_keys);
-  const int t0 = c * kAttnChunk;
-  if (t0 >= n) return;  // the combine step only reads chunks below ceil(n / 256)
-  const int cnt = min(kAttnChunk, n - t0);
-  const float scaling = 0.08838834764831845f;
-  for (int i = tid; i < QWEN_GROUPS * QWEN_HEAD_DIM; i += 256) {
-    const int h = i / QWEN_HEAD_DIM, d = i % QWEN_HEAD_DIM;
-    qs[h][d] = qkv[(size_t)b * qkv_stride + (kvh * QWEN_GROUPS + h) * QWEN_HEAD_DIM + d] * scaling;
-  }
-  __syncthreads();
-  const float* kbase = k_cache + (size_t)b * seq_stride + kvh * QWEN_HEAD_DIM;
-  const float* vbase = v_cache + (size_t)b * seq_stride + kvh * QWEN_HEAD_DIM;
+typedef float v4f __attribute__((ext_vector_type(4)));
+constexpr int kQRow = QWEN_HEAD_DIM + 4;  // LDS floats per query row (16-byte pad: no bank aliasing)
 
-  // scores: thread tid owns key t0 + tid
-  float s[QWEN_GROUPS];
+// One 16-key tile of attn_decode_kernel (keys tb..tb+15; MASK: keys >= t1 are masked out and not read).
+template <bool MASK>
+__device__ __forceinline__ void attn_decode_tile(const float* __restrict__ kb, const float* __restrict__ vb,
+                                                 const float* qrow, int tb, int t1, int col, int g, float& m,
+                                                 float& lp, v4f (&acc)[8]) {
+  float4 kr[8];
+  const int tk = tb + col;
+  const float* krow = kb + (size_t)tk * QWEN_KV_WIDTH + 4 * g;
 #pragma unroll
-  for (int h = 0; h < QWEN_GROUPS; ++h) s[h] = 0.0f;
-  if (tid < cnt) {
-    const float4* kr = reinterpret_cast<const float4*>(kbase + (size_t)(t0 + tid) * QWEN_KV_WIDTH);
-#pragma unroll 8
-    for (int d4 = 0; d4 < QWEN_HEAD_DIM / 4; ++d4) {
-      const float4 k4 = ld_stream(kr + d4);
+  for (int j = 0; j < 8; ++j)
+    kr[j] = (!MASK || tk < t1) ? ld_stream(reinterpret_cast<const float4*>(krow + 16 * j)) : make_float4(0, 0, 0, 0);
+  float4 vr[4][2];
+  const float* vrow = vb + (size_t)(tb + 4 * g) * QWEN_KV_WIDTH + 4 * col;
 #pragma unroll
-      for (int h = 0; h < QWEN_GROUPS; ++h) {
-        const float4 q4 = *reinterpret_cast<const float4*>(&qs[h][4 * d4]);
-        s[h] += q4.x * k4.x + q4.y * k4.y + q4.z * k4.z + q4.w * k4.w;
-      }
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      vr[r][h] = (!MASK || tb + 4 * g + r < t1)
+                     ? ld_stream(reinterpret_cast<const float4*>(vrow + r * QWEN_KV_WIDTH + 64 * h))
+                     : make_float4(0, 0, 0, 0);
+  // All 16 loads of the tile are issued before any math (16 KiB in flight per wave): without this
+  // fence the register-capped scheduler interleaves each load with its first use.
+  __builtin_amdgcn_sched_barrier(0);
+  v4f sc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float4 q4 = *reinterpret_cast<const float4*>(qrow + 16 * j);
+    sc = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[j].x, q4.x, sc, 0, 0, 0);
+    sc = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[j].y, q4.y, sc, 0, 0, 0);
+    sc = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[j].z, q4.z, sc, 0, 0, 0);
+    sc = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[j].w, q4.w, sc, 0, 0, 0);
+  }
+  float mt = -INFINITY;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    if (MASK && tb + 4 * g + r >= t1) sc[r] = -INFINITY;
+    mt = fmaxf(mt, sc[r]);
+  }
+  mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+  mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+  const float mn = fmaxf(m, mt);  // finite: key tb < t1 is in the tile
+  const float corr = __expf(m - mn);
+  float p[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) p[r] = __expf(sc[r] - mn);
+  lp = lp * corr + ((p[0] + p[1]) + (p[2] + p[3]));
+  m = mn;
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) {
+    const float cr = __shfl(corr, 4 * g + rr, 64);  // lane 4g + rr holds head 4g + rr
+#pragma unroll
+    for (int k = 0; k < 8; ++k) acc[k][rr] *= cr;
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      acc[4 * h + 0] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[r], vr[r][h].x, acc[4 * h + 0], 0, 0, 0);
+      acc[4 * h + 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[r], vr[r][h].y, acc[4 * h + 1], 0, 0, 0);
+      acc[4 * h + 2] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[r], vr[r][h].z, acc[4 * h + 2], 0, 0, 0);
+      acc[4 * h + 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[r], vr[r][h].w, acc[4 * h + 3], 0, 0, 0);
     }
-  }
-  float* redf = &red[0][0][0];
-#pragma unroll
-  for (int h = 0; h < QWEN_GROUPS; ++h) {
-    const float m = block_max4(tid < cnt ? s[h] : -INFINITY, redf + 4 * h);
-    const float p = tid < cnt ? __expf(s[h] - m) : 0.0f;
-    ps[h][tid] = p;
-    const float l = block_sum4(p, redf + 32 + 4 * h);
-    if (tid == 0) {
-      hm[h] = m;
-      hl[h] = l;
-    }
-  }
-  __syncthreads();
-
-  // P.V: thread = (key group tg = tid/64, dims 2*lane, 2*lane+1)
-  const int tg = tid >> 6;
-  const int ln = tid & 63;
-  float acc[QWEN_GROUPS][2];
-#pragma unroll
-  for (int h = 0; h < QWEN_GROUPS; ++h) acc[h][0] = acc[h][1] = 0.0f;
-#pragma unroll 4
-  for (int t = tg; t < cnt; t += 4) {
-    const float2 v2 = ld_stream(reinterpret_cast<const float2*>(vbase + (size_t)(t0 + t) * QWEN_KV_WIDTH) + ln);
-#pragma unroll
-    for (int h = 0; h < QWEN_GROUPS; ++h) {
-      const float p = ps[h][t];
-      acc[h][0] += p * v2.x;
-      acc[h][1] += p * v2.y;
-    }
-  }
-#pragma unroll
-  for (int h = 0; h < QWEN_GROUPS; ++h) {
-    red[tg][h][2 * ln] = acc[h][0];
-    red[tg][h][2 * ln + 1] = acc[h][1];
-  }
-  __syncthreads();
-  for (int i = tid; i < QWEN_GROUPS * QWEN_HEAD_DIM; i += 256) {
-    const int h = i / QWEN_HEAD_DIM, d = i % QWEN_HEAD_DIM;
-    const float v = (red[0][h][d] + red[1][h][d]) + (red[2][h][d] + red[3][h][d]);
-    const int qh = kvh * QWEN_GROUPS + h;
-    part[(((size_t)b * QWEN_Q_HEADS + qh) * nchunk + c) * QWEN_HEAD_DIM + d] = v;
-  }
-  if (tid < QWEN_GROUPS) {
-    const int qh = kvh * QWEN_GROUPS + tid;
-    pml[((size_t)b * QWEN_Q_HEADS + qh) * nchunk + c] = make_float2(hm[tid], hl[tid]);
   }
 }
 
-// ---------------------------------------------------------------------------------------------
-// Decode attention partials on the fp32 matrix cores (v_mfma_f32_16x16x4_f32): same partials as
-// attn_decode_partial_kernel, but the K/V rows are read straight into MFMA operand registers with
-// 64-byte-contiguous row segments, and the probabilities never leave registers.
-// Block (chunk c, KV head kvh, sequence b), 4 waves; wave w covers keys t0 + 64w + [0, 64) in
-// tiles of 16.  Per tile (lane l: col = l & 15, g = l >> 4):
-//   S = K_tile . Q^T:  A = K[token col][dims], B = Q[head col][dims] (heads >= 6 are zero),
-//                      32 MFMAs over the 128 dims (dim 4g + 16j + e for MFMA 4j + e);
-//                      lane gets S[token 4g + r][head col], r = 0..3.
-//   online softmax per head col (max over the 16 tokens: registers + xor-shuffles 16, 32);
-//   O += P . V:        MFMA (r, h, e): A = P[head col][token 4g + r] (the lane's own p[r]),
-//                      B = V[token 4g + r][dim 4 col + e + 64h]; lane holds O[head 4g + r'][dim].
-// The 4 waves are merged in LDS and one (m, l, acc[128]) partial per query head is written.
-// ---------------------------------------------------------------------------------------------
-typedef float v4f __attribute__((ext_vector_type(4)));
-
-__global__ void __launch_bounds__(256) attn_decode_mfma_kernel(const float* __restrict__ qkv, int qkv_stride,
-                                                               const float* __restrict__ k_cache,
-                                                               const float* __restrict__ v_cache, size_t seq_stride,
-                                                               const int* __restrict__ pos, float* __restrict__ part,
-                                                               float2* __restrict__ pml, int nchunk, int max_keys) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
+attn_decode_kernel(const float* __restrict__ qkv, int qkv_stride, const float* __restrict__ k_cache,
+                   const float* __restrict__ v_cache, size_t seq_stride, const int* __restrict__ pos, int chunk,
+                   int max_keys, float* __restrict__ part, float2* __restrict__ pml, unsigned* __restrict__ arrivals,
+                   float* __restrict__ ctx, int8_t* __restrict__ xq, float* __restrict__ sx, int* __restrict__ sums) {
+  __shared__ __align__(16) float qs[16][kQRow];
+  __shared__ __align__(16) float s_acc[4][QWEN_GROUPS][QWEN_HEAD_DIM];  // reused by the merge step
   __shared__ float s_m[4][QWEN_GROUPS], s_l[4][QWEN_GROUPS];
-  __shared__ float s_acc[4][QWEN_GROUPS][QWEN_HEAD_DIM];
+  __shared__ float red_f[4];
+  __shared__ int red_i[4];
+  __shared__ int s_last;
+  static_assert(2 * QWEN_Q_HEADS * kAttnMaxSplits <= 4 * QWEN_GROUPS * QWEN_HEAD_DIM && QWEN_HIDDEN <= 16 * kQRow,
+                "merge scratch");
+  const int nsplit = gridDim.x;
   const int c = blockIdx.x;
   const int kvh = blockIdx.y;
   const int b = blockIdx.z;
@@ -865,276 +855,144 @@ __global__ void __launch_bounds__(256) attn_decode_mfma_kernel(const float* __re
   const int col = lane & 15;
   const int g = lane >> 4;
   const int n = min(max(pos[b], 0) + 1, max_keys);
-  const int t0 = c * kAttnChunk;
-  if (t0 >= n) return;  // block-uniform; the combine step only reads chunks below ceil(n / 256)
+  const int t0 = c * chunk;
   const float scaling = 0.08838834764831845f;
 
-  float qr[32];
-  {
-    const bool hv = col < QWEN_GROUPS;
-    const float* qp = qkv + (size_t)b * qkv_stride + (kvh * QWEN_GROUPS + (hv ? col : 0)) * QWEN_HEAD_DIM + 4 * g;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float4 q4 = hv ? *reinterpret_cast<const float4*>(qp + 16 * j) : make_float4(0, 0, 0, 0);
-      qr[4 * j + 0] = q4.x * scaling;
-      qr[4 * j + 1] = q4.y * scaling;
-      qr[4 * j + 2] = q4.z * scaling;
-      qr[4 * j + 3] = q4.w * scaling;
+  if (t0 < n) {  // block-uniform; splits past the sequence only count themselves in below
+    const int t1 = min(n, t0 + chunk);
+    for (int i = threadIdx.x; i < 16 * QWEN_HEAD_DIM; i += 256) {
+      const int h = i >> 7, d = i & 127;
+      qs[h][d] = h < QWEN_GROUPS
+                     ? qkv[(size_t)b * qkv_stride + (kvh * QWEN_GROUPS + h) * QWEN_HEAD_DIM + d] * scaling
+                     : 0.0f;
     }
-  }
-  const float* kb = k_cache + (size_t)b * seq_stride + kvh * QWEN_HEAD_DIM;
-  const float* vb = v_cache + (size_t)b * seq_stride + kvh * QWEN_HEAD_DIM;
-  float m = -INFINITY;
-  float lp = 0.0f;
-  v4f acc[8];
+    __syncthreads();
+    const float* kb = k_cache + (size_t)b * seq_stride + kvh * QWEN_HEAD_DIM;
+    const float* vb = v_cache + (size_t)b * seq_stride + kvh * QWEN_HEAD_DIM;
+    const float* qrow = &qs[col][4 * g];
+    float m = -INFINITY;
+    float lp = 0.0f;
+    v4f acc[8];
 #pragma unroll
-  for (int k = 0; k < 8; ++k) acc[k] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int k = 0; k < 8; ++k) acc[k] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 
-  const int wbase = t0 + wave * 64;
+    int tb = t0 + 16 * wave;
 #pragma unroll 1
-  for (int tile = 0; tile < 4; ++tile) {
-    const int tb = wbase + tile * 16;
-    if (tb >= n) break;  // wave-uniform
-    float4 kr[8];
-    const int tk = tb + col;
-    const float* krow = kb + (size_t)tk * QWEN_KV_WIDTH + 4 * g;
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      kr[j] = tk < n ? ld_stream(reinterpret_cast<const float4*>(krow + 16 * j)) : make_float4(0, 0, 0, 0);
-    float4 vr[4][2];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int tv = tb + 4 * g + r;
-      const float* vrow = vb + (size_t)tv * QWEN_KV_WIDTH + 4 * col;
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-        vr[r][h] = tv < n ? ld_stream(reinterpret_cast<const float4*>(vrow + 64 * h)) : make_float4(0, 0, 0, 0);
+    for (; tb + 16 <= t1; tb += 64) attn_decode_tile<false>(kb, vb, qrow, tb, t1, col, g, m, lp, acc);
+    if (tb < t1) attn_decode_tile<true>(kb, vb, qrow, tb, t1, col, g, m, lp, acc);  // the range's last, partial tile
+    lp += __shfl_xor(lp, 16, 64);
+    lp += __shfl_xor(lp, 32, 64);
+    if (g == 0 && col < QWEN_GROUPS) {
+      s_m[wave][col] = m;
+      s_l[wave][col] = lp;
     }
-    v4f sc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      sc = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[j].x, qr[4 * j + 0], sc, 0, 0, 0);
-      sc = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[j].y, qr[4 * j + 1], sc, 0, 0, 0);
-      sc = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[j].z, qr[4 * j + 2], sc, 0, 0, 0);
-      sc = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[j].w, qr[4 * j + 3], sc, 0, 0, 0);
-    }
-    float mt = -INFINITY;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      if (tb + 4 * g + r >= n) sc[r] = -INFINITY;
-      mt = fmaxf(mt, sc[r]);
-    }
-    mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-    const float mn = fmaxf(m, mt);  // finite: token tb < n is in the tile
-    const float corr = __expf(m - mn);
-    float p[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) p[r] = __expf(sc[r] - mn);
-    lp = lp * corr + ((p[0] + p[1]) + (p[2] + p[3]));
-    m = mn;
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
-      const float cr = __shfl(corr, 4 * g + rr, 64);  // lane 4g + rr holds head 4g + rr
+      const int head = 4 * g + rr;
+      if (head < QWEN_GROUPS) {
 #pragma unroll
-      for (int k = 0; k < 8; ++k) acc[k][rr] *= cr;
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) s_acc[wave][head][4 * col + e + 64 * h] = acc[4 * h + e][rr];
+      }
     }
+    __syncthreads();
+    for (int i = threadIdx.x; i < QWEN_GROUPS * QWEN_HEAD_DIM; i += 256) {
+      const int head = i / QWEN_HEAD_DIM, d = i % QWEN_HEAD_DIM;
+      float M = s_m[0][head];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
+      for (int w = 1; w < 4; ++w) M = fmaxf(M, s_m[w][head]);
+      float L = 0.0f, A = 0.0f;
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        acc[4 * h + 0] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[r], vr[r][h].x, acc[4 * h + 0], 0, 0, 0);
-        acc[4 * h + 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[r], vr[r][h].y, acc[4 * h + 1], 0, 0, 0);
-        acc[4 * h + 2] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[r], vr[r][h].z, acc[4 * h + 2], 0, 0, 0);
-        acc[4 * h + 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[r], vr[r][h].w, acc[4 * h + 3], 0, 0, 0);
+      for (int w = 0; w < 4; ++w) {
+        const float f = s_m[w][head] == -INFINITY ? 0.0f : __expf(s_m[w][head] - M);  // waves without keys
+        L += s_l[w][head] * f;
+        A += s_acc[w][head][d] * f;
+      }
+      const int qh = kvh * QWEN_GROUPS + head;
+      store_agent(&part[(((size_t)b * QWEN_Q_HEADS + qh) * nsplit + c) * QWEN_HEAD_DIM + d], A);
+      if (d == 0) {
+        float* ml = reinterpret_cast<float*>(&pml[((size_t)b * QWEN_Q_HEADS + qh) * nsplit + c]);
+        store_agent(ml, M);
+        store_agent(ml + 1, L);
       }
     }
   }
-  lp += __shfl_xor(lp, 16, 64);
-  lp += __shfl_xor(lp, 32, 64);
-  if (g == 0 && col < QWEN_GROUPS) {
-    s_m[wave][col] = m;
-    s_l[wave][col] = lp;
-  }
-#pragma unroll
-  for (int rr = 0; rr < 4; ++rr) {
-    const int head = 4 * g + rr;
-    if (head < QWEN_GROUPS) {
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) s_acc[wave][head][4 * col + e + 64 * h] = acc[4 * h + e][rr];
-    }
-  }
-  __syncthreads();
-  for (int i = threadIdx.x; i < QWEN_GROUPS * QWEN_HEAD_DIM; i += 256) {
-    const int head = i / QWEN_HEAD_DIM, d = i % QWEN_HEAD_DIM;
-    float M = s_m[0][head];
-#pragma unroll
-    for (int w = 1; w < 4; ++w) M = fmaxf(M, s_m[w][head]);
-    float L = 0.0f, A = 0.0f;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const float f = s_m[w][head] == -INFINITY ? 0.0f : __expf(s_m[w][head] - M);
-      L += s_l[w][head] * f;
-      A += s_acc[w][head][d] * f;
-    }
-    const int qh = kvh * QWEN_GROUPS + head;
-    part[(((size_t)b * QWEN_Q_HEADS + qh) * nchunk + c) * QWEN_HEAD_DIM + d] = A;
-    if (d == 0) pml[((size_t)b * QWEN_Q_HEADS + qh) * nchunk + c] = make_float2(M, L);
-  }
-}
 
-// Merges the chunk partials of one sequence into ctx[b][1536] = acc / l and quantizes the row for
-// the O projection.  grid = batch, block = 256.
-__global__ void __launch_bounds__(256) attn_decode_combine_kernel(const float* __restrict__ part,
-                                                                  const float2* __restrict__ pml,
-                                                                  const int* __restrict__ pos, int nchunk, int max_keys,
-                                                                  float* __restrict__ ctx, int8_t* __restrict__ xq,
-                                                                  float* __restrict__ sx, int* __restrict__ sums) {
-  __shared__ float row[QWEN_HIDDEN];
-  __shared__ float wgt[QWEN_Q_HEADS][kMaxChunks];
-  __shared__ float lsum[QWEN_Q_HEADS][kMaxChunks];
-  __shared__ float gm[QWEN_Q_HEADS], ginv[QWEN_Q_HEADS];
-  __shared__ float red_f[4];
-  __shared__ int red_i[4];
-  const int b = blockIdx.x;
-  const int n = min(max(pos[b], 0) + 1, max_keys);
-  const int nc = min((n + kAttnChunk - 1) / kAttnChunk, nchunk);
-  const float2* pb = pml + (size_t)b * QWEN_Q_HEADS * nchunk;
+  // Arrival.  The partials were written with device-coherent (agent-scope) stores; once every wave
+  // has waited for its stores to complete, they are visible to every XCD, and one thread counts the
+  // block.  The last block reads them back with device-coherent loads, so no cache write-back or
+  // invalidation is needed on either side.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) s_last = atomicAdd(&arrivals[b], 1u) == 2u * (unsigned)nsplit - 1u;
+  __syncthreads();
+  if (!s_last) return;
+
+  // Merge of the sequence's splits (the last block only).  The (m, l) pairs and this thread's first
+  // 8 splits of partial values are loaded together, so sequences with at most 8 splits need one
+  // memory round trip.  Thread t owns dims d = t & 127 of heads (t >> 7) + 2k, k < 6.
+  const int nc = (n + chunk - 1) / chunk;  // splits that hold keys
+  float* ml = &s_acc[0][0][0];             // [12][kAttnMaxSplits][2] (m, l), then merge weights in place
+  float* row = &qs[0][0];                  // [1536] context row
+  const float* pb = reinterpret_cast<const float*>(pml + (size_t)b * QWEN_Q_HEADS * nsplit);
+  const int d = threadIdx.x & 127;
+  const int h0 = threadIdx.x >> 7;
+  const float* pa = part + (size_t)b * QWEN_Q_HEADS * nsplit * QWEN_HEAD_DIM + d;
+  float pv[6][8];
+  auto load_part = [&](int s0) {
+#pragma unroll
+    for (int k = 0; k < 6; ++k)
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        pv[k][j] = s0 + j < nc ? load_agent(pa + ((size_t)(h0 + 2 * k) * nsplit + s0 + j) * QWEN_HEAD_DIM) : 0.0f;
+  };
+  load_part(0);
   for (int i = threadIdx.x; i < QWEN_Q_HEADS * nc; i += 256) {
-    const int h = i / nc, c = i % nc;
-    const float2 v = pb[h * nchunk + c];
-    wgt[h][c] = v.x;  // chunk maxima first, replaced by the merge weights below
-    lsum[h][c] = v.y;
+    const int h = i / nc, sp = i % nc;
+    ml[(h * kAttnMaxSplits + sp) * 2] = load_agent(pb + 2 * (h * nsplit + sp));
+    ml[(h * kAttnMaxSplits + sp) * 2 + 1] = load_agent(pb + 2 * (h * nsplit + sp) + 1);
   }
   __syncthreads();
   if (threadIdx.x < QWEN_Q_HEADS) {
-    const int h = threadIdx.x;
+    float* mh = ml + threadIdx.x * kAttnMaxSplits * 2;
     float M = -INFINITY;
-    for (int c = 0; c < nc; ++c) M = fmaxf(M, wgt[h][c]);
+    for (int sp = 0; sp < nc; ++sp) M = fmaxf(M, mh[2 * sp]);
     float L = 0.0f;
-    for (int c = 0; c < nc; ++c) L += lsum[h][c] * __expf(wgt[h][c] - M);
-    gm[h] = M;
-    ginv[h] = L > 0.0f ? 1.0f / L : 0.0f;
+    for (int sp = 0; sp < nc; ++sp) {
+      const float f = __expf(mh[2 * sp] - M);
+      mh[2 * sp] = f;
+      L += mh[2 * sp + 1] * f;
+    }
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    for (int sp = 0; sp < nc; ++sp) mh[2 * sp] *= inv;  // merge weight of split sp
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < QWEN_Q_HEADS * nc; i += 256) {
-    const int h = i / nc, c = i % nc;
-    wgt[h][c] = __expf(wgt[h][c] - gm[h]) * ginv[h];
+  float out[6];
+#pragma unroll
+  for (int k = 0; k < 6; ++k) out[k] = 0.0f;
+  for (int s0 = 0; s0 < nc; s0 += 8) {
+    if (s0 > 0) load_part(s0);
+#pragma unroll
+    for (int k = 0; k < 6; ++k)
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (s0 + j < nc) out[k] += pv[k][j] * ml[((h0 + 2 * k) * kAttnMaxSplits + s0 + j) * 2];
   }
-  __syncthreads();
-  for (int i = threadIdx.x; i < QWEN_HIDDEN; i += 256) {
-    const int h = i / QWEN_HEAD_DIM, d = i % QWEN_HEAD_DIM;
-    const float* pa = part + ((size_t)b * QWEN_Q_HEADS + h) * nchunk * QWEN_HEAD_DIM + d;
-    float acc = 0.0f;
-#pragma unroll 4
-    for (int c = 0; c < nc; ++c) acc += pa[(size_t)c * QWEN_HEAD_DIM] * wgt[h][c];
-    row[i] = acc;
-    if (ctx) ctx[(size_t)b * QWEN_HIDDEN + i] = acc;
+#pragma unroll
+  for (int k = 0; k < 6; ++k) {
+    const int i = (h0 + 2 * k) * QWEN_HEAD_DIM + d;
+    row[i] = out[k];
+    if (ctx) ctx[(size_t)b * QWEN_HIDDEN + i] = out[k];
   }
   __syncthreads();
   quantize_row_lds(row, QWEN_HIDDEN, xq + (size_t)b * (2 * QWEN_HIDDEN), sx + b, sums + 2 * b, red_f, red_i);
+  if (threadIdx.x == 0) arrivals[b] = 0u;
 }
 
-// ---------------------------------------------------------------------------------------------
-// Causal prefill attention (qwen_prefill_attention_kernel.cpp:204-289 semantics, online softmax,
-// approx_exp).  Block (query tile qt of 64 queries, query head h, sequence sq): 4 threads per
-// query, each owning 32 of the 128 dims; K/V tiles of 64 keys are staged in LDS.
-// q rows: qkv + (sq*S + i)*qkv_stride + h*128; K/V rows: cache + sq*seq_stride + j*256 + kvh*128.
-// ctx: [sq*S + i][1536].  grid = (ceil(S/64), 12, nseq), block = 256.
-// ---------------------------------------------------------------------------------------------
-__global__ void __launch_bounds__(256) attn_prefill_kernel(const float* __restrict__ qkv, int qkv_stride,
-                                                           const float* __restrict__ k_cache,
-                                                           const float* __restrict__ v_cache, size_t seq_stride,
-                                                           int S, float* __restrict__ ctx) {
-  __shared__ __align__(16) float ks[64][QWEN_HEAD_DIM + 4];
-  __shared__ __align__(16) float vs[64][QWEN_HEAD_DIM + 4];
-  const int qt = blockIdx.x;
-  const int h = blockIdx.y;
-  const int sq = blockIdx.z;
-  const int kvh = h / QWEN_GROUPS;
-  const int tid = threadIdx.x;
-  const int qi = qt * 64 + (tid >> 2);  // query index within the sequence
-  const int part4 = tid & 3;            // dims [32*part4, 32*part4+32)
-  const bool q_ok = qi < S;
-  const float scaling = 0.08838834764831845f;
-  float q[32], acc[32];
-  {
-    const float* qp = qkv + ((size_t)sq * S + (q_ok ? qi : 0)) * qkv_stride + h * QWEN_HEAD_DIM + 32 * part4;
-#pragma unroll
-    for (int d = 0; d < 32; ++d) {
-      q[d] = q_ok ? qp[d] * scaling : 0.0f;
-      acc[d] = 0.0f;
-    }
-  }
-  float m = -INFINITY, l = 0.0f;
-  const int last_key = min(S, qt * 64 + 64);  // keys this tile can see
-  const float* kb = k_cache + (size_t)sq * seq_stride + kvh * QWEN_HEAD_DIM;
-  const float* vb = v_cache + (size_t)sq * seq_stride + kvh * QWEN_HEAD_DIM;
-  for (int j0 = 0; j0 < last_key; j0 += 64) {
-    __syncthreads();
-    for (int e = tid; e < 64 * 32; e += 256) {
-      const int r = e >> 5, c4 = e & 31;
-      const int j = j0 + r;
-      float4 kv = make_float4(0, 0, 0, 0), vv = kv;
-      if (j < S) {
-        kv = reinterpret_cast<const float4*>(kb + (size_t)j * QWEN_KV_WIDTH)[c4];
-        vv = reinterpret_cast<const float4*>(vb + (size_t)j * QWEN_KV_WIDTH)[c4];
-      }
-      *reinterpret_cast<float4*>(&ks[r][4 * c4]) = kv;
-      *reinterpret_cast<float4*>(&vs[r][4 * c4]) = vv;
-    }
-    __syncthreads();
-    const int jn = min(64, last_key - j0);
-    float s[64];
-    float tmax = -INFINITY;
-#pragma unroll
-    for (int jj = 0; jj < 64; ++jj) {
-      float d0 = 0.0f;
-      if (jj < jn) {
-        const float* kr = &ks[jj][32 * part4];
-#pragma unroll
-        for (int d = 0; d < 32; d += 4) {
-          const float4 k4 = *reinterpret_cast<const float4*>(kr + d);
-          d0 += q[d] * k4.x + q[d + 1] * k4.y + q[d + 2] * k4.z + q[d + 3] * k4.w;
-        }
-      }
-      d0 += __shfl_xor(d0, 1, 64);
-      d0 += __shfl_xor(d0, 2, 64);
-      const bool ok = jj < jn && (j0 + jj) <= qi;
-      s[jj] = ok ? d0 : -INFINITY;
-      tmax = fmaxf(tmax, s[jj]);
-    }
-    if (tmax == -INFINITY) continue;  // every key of this tile is masked for this query
-    const float mnew = fmaxf(m, tmax);
-    const float corr = approx_exp_fast(m - mnew);
-    l *= corr;
-#pragma unroll
-    for (int d = 0; d < 32; ++d) acc[d] *= corr;
-    m = mnew;
-#pragma unroll
-    for (int jj = 0; jj < 64; ++jj) {
-      if (s[jj] == -INFINITY) continue;
-      const float p = approx_exp_fast(s[jj] - m);
-      l += p;
-      const float* vr = &vs[jj][32 * part4];
-#pragma unroll
-      for (int d = 0; d < 32; d += 4) {
-        const float4 v4 = *reinterpret_cast<const float4*>(vr + d);
-        acc[d] += p * v4.x;
-        acc[d + 1] += p * v4.y;
-        acc[d + 2] += p * v4.z;
-        acc[d + 3] += p * v4.w;
-      }
-    }
-  }
-  if (!q_ok) return;
-  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-  float* op = ctx + ((size_t)sq * S + qi) * QWEN_HIDDEN + h * QWEN_HEAD_DIM + 32 * part4;
-#pragma unroll
-  for (int d = 0; d < 32; d += 4)
-    *reinterpret_cast<float4*>(op + d) = make_float4(acc[d] * inv, acc[d + 1] * inv, acc[d + 2] * inv, acc[d + 3] * inv);
+__global__ void zero_u32_kernel(unsigned* __restrict__ p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1364,22 +1222,34 @@ void launch_rope_qkv(float* qkv, int qkv_stride, const int* pos, int seq_len, in
                      k_cache, v_cache, seq_stride);
 }
 
-void launch_attn_decode(const float* qkv, int qkv_stride, const float* k_cache, const float* v_cache,
-                        size_t seq_stride, const int* pos, int batch, int max_keys, float* part, float2* pml,
-                        float* ctx, int8_t* xq, float* sx, int* sums, hipStream_t st) {
-  const int nchunk = (max_keys + kAttnChunk - 1) / kAttnChunk;
-  hipLaunchKernelGGL(attn_decode_mfma_kernel, dim3(nchunk, QWEN_KV_HEADS, batch), dim3(256), 0, st, qkv,
-                     qkv_stride, k_cache, v_cache, seq_stride, pos, part, pml, nchunk, max_keys);
-  hipLaunchKernelGGL(attn_decode_combine_kernel, dim3(batch), dim3(256), 0, st, part, pml, pos, nchunk, max_keys, ctx,
-                     xq, sx, sums);
+AttnDecodePlan plan_attn_decode(int batch, int max_keys) {
+  // co-resident blocks of attn_decode_kernel on the current device (CUs x blocks per CU)
+  static const int slots = [] {
+    int dev = 0, per_cu = 0;
+    hipDeviceProp_t prop;
+    if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess) return 1024;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, attn_decode_kernel, 256, 0) != hipSuccess || per_cu < 1)
+      per_cu = 1;
+    return prop.multiProcessorCount * per_cu;
+  }();
+  // 3 of every 4 co-resident slots: the KV stream runs faster at 12 than at 16 waves per CU.
+  int nsplit = (3 * slots / 4) / (QWEN_KV_HEADS * (batch > 0 ? batch : 1));
+  nsplit = nsplit < 1 ? 1 : (nsplit > kAttnMaxSplits ? kAttnMaxSplits : nsplit);
+  int chunk = (max_keys + nsplit - 1) / nsplit;
+  chunk = (chunk + 15) & ~15;  // whole 16-key tiles
+  return AttnDecodePlan{(max_keys + chunk - 1) / chunk, chunk};
 }
 
-void launch_attn_decode_partial_only(const float* qkv, int qkv_stride, const float* k_cache, const float* v_cache,
-                                     size_t seq_stride, const int* pos, int batch, int max_keys, float* part,
-                                     float2* pml, hipStream_t st) {
-  const int nchunk = (max_keys + kAttnChunk - 1) / kAttnChunk;
-  hipLaunchKernelGGL(attn_decode_mfma_kernel, dim3(nchunk, QWEN_KV_HEADS, batch), dim3(256), 0, st, qkv,
-                     qkv_stride, k_cache, v_cache, seq_stride, pos, part, pml, nchunk, max_keys);
+void launch_zero_u32(unsigned* p, int n, hipStream_t st) {
+  hipLaunchKernelGGL(zero_u32_kernel, dim3((n + 255) / 256), dim3(256), 0, st, p, n);
+}
+
+void launch_attn_decode(const float* qkv, int qkv_stride, const float* k_cache, const float* v_cache,
+                        size_t seq_stride, const int* pos, int batch, int max_keys, const AttnDecodePlan& plan,
+                        float* part, float2* pml, unsigned* arrivals, float* ctx, int8_t* xq, float* sx, int* sums,
+                        hipStream_t st) {
+  hipLaunchKernelGGL(attn_decode_kernel, dim3(plan.nsplit, QWEN_KV_HEADS, batch), dim3(256), 0, st, qkv, qkv_stride,
+                     k_cache, v_cache, seq_stride, pos, plan.chunk, max_keys, part, pml, arrivals, ctx, xq, sx, sums);
 }
 
 void launch_attn_prefill(const float* qkv, int qkv_stride, const float* k_cache, const float* v_cache,

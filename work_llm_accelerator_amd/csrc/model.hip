@@ -26,14 +26,18 @@ struct FastLayer {
 };
 
 constexpr size_t kQkvRows = QWEN_QKV_ROWS;  // 2048
+constexpr size_t kMaxArrivals = 4096;       // most sequences of one FAST decode call
 constexpr size_t kRepackedLayerBytes = QWEN_PACKED_WEIGHT_BYTES;
 
-// Device buffer that only grows (freed after a device synchronize).
+// Device buffer that only grows (freed after a device synchronize); `generation` counts the
+// allocations, so users can re-initialize state kept in the buffer after a move.
 struct DevBuf {
   void* p = nullptr;
   size_t cap = 0;
+  unsigned generation = 0;
   void* get(size_t bytes) {
     if (bytes <= cap) return p;
+    ++generation;
     if (p) {
       QWEN_HIP(hipDeviceSynchronize());
       QWEN_HIP(hipFree(p));
@@ -70,24 +74,29 @@ struct qwen_hip_model {
   uint16_t* embed = nullptr;      // synthetic models: [QWEN_VOCAB][1536] bf16
   Arena arena;                    // ORDERED per-layer intermediates
   DevBuf ws;                      // FAST workspace and ORDERED attention output
+  unsigned arrivals_ready = 0;    // ws generation whose arrival counters were zeroed
   LastCall last;
 
-  // FAST workspace carve-up for `tokens` rows (and `batch` x `nchunk` attention partials).
+  // FAST workspace carve-up for `tokens` rows and `batch` x `nsplit` decode-attention partials.
+  // The decode-attention arrival counters (one per sequence, batch <= kMaxArrivals) sit at offset 0
+  // of every carve-up and return to zero after each launch, so they are zeroed once per buffer.
   struct Ws {
     int8_t* xq;
     float* sx;
     int* sums;
     float *qkv, *ctx, *att, *s, *tmp, *part;
     float2* pml;
+    unsigned* arrivals;
     float* splitk;  // K-split partials of the non-dual projections (out <= 2048)
   };
-  Ws carve(size_t tokens, size_t batch, size_t nchunk) {
+  Ws carve(size_t tokens, size_t batch, size_t nsplit) {
     size_t off = 0;
     auto take = [&](size_t bytes) {
       const size_t o = off;
       off = (off + bytes + 255u) & ~size_t(255u);
       return o;
     };
+    const size_t o_arr = take(kMaxArrivals * 4u);  // fixed offset: never overlaps the parts below
     const size_t o_xq = take(xq_bytes(tokens, QWEN_INTERMEDIATE));
     const size_t o_sx = take(tokens * 4u);
     const size_t o_sums = take(tokens * 8u);
@@ -96,16 +105,27 @@ struct qwen_hip_model {
     const size_t o_att = take(tokens * QWEN_HIDDEN * 4u);
     const size_t o_s = take(tokens * QWEN_INTERMEDIATE * 4u);
     const size_t o_tmp = take(tokens * QWEN_INTERMEDIATE * 4u);
-    const size_t o_part = take(batch * QWEN_Q_HEADS * nchunk * QWEN_HEAD_DIM * 4u);
-    const size_t o_pml = take(batch * QWEN_Q_HEADS * nchunk * 8u);
+    const size_t o_part = take(batch * QWEN_Q_HEADS * nsplit * QWEN_HEAD_DIM * 4u);
+    const size_t o_pml = take(batch * QWEN_Q_HEADS * nsplit * 8u);
     const size_t o_splitk = take(splitk_bytes(kQkvRows));
     char* b = static_cast<char*>(ws.get(off));
+    unsigned* arr = reinterpret_cast<unsigned*>(b + o_arr);
+    if (ws.generation != arrivals_ready) {  // fresh buffer: arm the counters once
+      launch_zero_u32(arr, kMaxArrivals, stream);
+      arrivals_ready = ws.generation;
+    }
     return Ws{reinterpret_cast<int8_t*>(b + o_xq), reinterpret_cast<float*>(b + o_sx),
               reinterpret_cast<int*>(b + o_sums), reinterpret_cast<float*>(b + o_qkv),
               reinterpret_cast<float*>(b + o_ctx), reinterpret_cast<float*>(b + o_att),
               reinterpret_cast<float*>(b + o_s), reinterpret_cast<float*>(b + o_tmp),
-              reinterpret_cast<float*>(b + o_part), reinterpret_cast<float2*>(b + o_pml),
+              reinterpret_cast<float*>(b + o_part), reinterpret_cast<float2*>(b + o_pml), arr,
               reinterpret_cast<float*>(b + o_splitk)};
+  }
+
+  // Plain scratch of `bytes` in the workspace, past the arrival counters.
+  float* scratch(size_t bytes) {
+    const size_t off = (kMaxArrivals * 4u + 255u) & ~size_t(255u);
+    return reinterpret_cast<float*>(static_cast<char*>(ws.get(off + bytes)) + off);
   }
 
   DevLayer dev_layer(int l) const {
@@ -221,8 +241,8 @@ struct qwen_hip_model {
 
   void decode_fast(int B, float* hidden, const int* pos, int max_keys, float* kc0, float* vc0, uint64_t ss,
                    uint64_t ls, int round) {
-    const int nchunk = (max_keys + kAttnChunk - 1) / kAttnChunk;
-    const Ws w = carve(B, B, nchunk);
+    const AttnDecodePlan plan = plan_attn_decode(B, max_keys);
+    const Ws w = carve(B, B, plan.nsplit);
     for (int l = 0; l < layers; ++l) {
       const FastLayer& f = fast[l];
       float* kc = kc0 + (size_t)l * ls;
@@ -230,8 +250,8 @@ struct qwen_hip_model {
       launch_norm_quant(hidden, QWEN_HIDDEN, B, QWEN_HIDDEN, f.ln, kNormDecode, w.xq, w.sx, w.sums, nullptr, stream);
       gemm(w, B, QWEN_HIDDEN, (int)kQkvRows, f.qkv, f.sw_qkv, f.b_qkv, w.qkv, kQkvRows, kEpiStore);
       launch_rope_qkv(w.qkv, (int)kQkvRows, pos, 1, max_keys, B, rope_decode, kc, vc, ss, stream);
-      launch_attn_decode(w.qkv, (int)kQkvRows, kc, vc, ss, pos, B, max_keys, w.part, w.pml, w.ctx, w.xq, w.sx,
-                         w.sums, stream);
+      launch_attn_decode(w.qkv, (int)kQkvRows, kc, vc, ss, pos, B, max_keys, plan, w.part, w.pml, w.arrivals,
+                         nullptr, w.xq, w.sx, w.sums, stream);
       gemm(w, B, QWEN_HIDDEN, QWEN_HIDDEN, f.o, f.sw_o, nullptr, w.att, QWEN_HIDDEN, kEpiStore);
       launch_norm_quant(w.att, QWEN_HIDDEN, B, QWEN_HIDDEN, f.post_ln, kNormDecode, w.xq, w.sx, w.sums, nullptr,
                         stream);
@@ -273,7 +293,7 @@ struct qwen_hip_model {
 
   void decode_ordered(int B, float* hidden, const int* pos, int max_keys, float* kc0, float* vc0, uint64_t ss,
                       uint64_t ls, int round) {
-    float* att = static_cast<float*>(ws.get((size_t)B * QWEN_HIDDEN * 4u));
+    float* att = scratch((size_t)B * QWEN_HIDDEN * 4u);
     for (int l = 0; l < layers; ++l) {
       const DevLayer d = dev_layer(l);
       arena.reset();
@@ -288,7 +308,7 @@ struct qwen_hip_model {
   }
 
   void prefill_ordered(int B, int S, float* hidden, float* kc0, float* vc0, uint64_t ss, uint64_t ls, int round) {
-    float* att = static_cast<float*>(ws.get((size_t)S * QWEN_HIDDEN * 4u));
+    float* att = scratch((size_t)S * QWEN_HIDDEN * 4u);
     for (int l = 0; l < layers; ++l) {
       const DevLayer d = dev_layer(l);
       for (int b = 0; b < B; ++b) {
@@ -428,6 +448,7 @@ int qwen_hip_model_decode(qwen_hip_model* m, int mode, int batch, float* hidden,
   mode &= ~QWEN_FLAG_NO_BF16_ROUND;
   if (batch <= 0 || max_keys <= 0 || max_keys > QWEN_MAX_SEQ || (mode != QWEN_MODE_ORDERED && mode != QWEN_MODE_FAST))
     return invalid("invalid decode shape or mode");
+  if (mode == QWEN_MODE_FAST && (size_t)batch > kMaxArrivals) return invalid("FAST decode batch above 4096 sequences");
   if (seq_stride < (uint64_t)max_keys * QWEN_KV_WIDTH || (batch > 1 && layer_stride < (uint64_t)batch * seq_stride) ||
       (m->layers > 1 && layer_stride == 0))
     return invalid("KV strides too small for max_keys / batch");
@@ -484,16 +505,16 @@ int qwen_hip_model_time_kernel(qwen_hip_model* m, int kernel, int layer, int rep
     return invalid("kernel does not belong to the last call");
   return guarded_model([&]() -> int {
     const int T = c.batch * c.seq_len;
-    const int nchunk = (c.max_keys + kAttnChunk - 1) / kAttnChunk;
-    const qwen_hip_model::Ws w = m->carve(T, decode ? c.batch : 1, decode ? nchunk : 1);
+    const AttnDecodePlan plan = plan_attn_decode(decode ? c.batch : 1, c.max_keys);
+    const qwen_hip_model::Ws w = m->carve(T, decode ? c.batch : 1, decode ? plan.nsplit : 1);
     const FastLayer& f = m->fast[layer];
     float* kc = c.k_cache + (size_t)layer * c.layer_stride;
     float* vc = c.v_cache + (size_t)layer * c.layer_stride;
     auto once = [&]() {
       switch (kernel) {
         case QWEN_KERNEL_ATTN_DECODE:
-          launch_attn_decode_partial_only(w.qkv, (int)kQkvRows, kc, vc, c.seq_stride, c.positions, c.batch,
-                                          c.max_keys, w.part, w.pml, m->stream);
+          launch_attn_decode(w.qkv, (int)kQkvRows, kc, vc, c.seq_stride, c.positions, c.batch, c.max_keys, plan,
+                             w.part, w.pml, w.arrivals, nullptr, w.xq, w.sx, w.sums, m->stream);
           break;
         case QWEN_KERNEL_GEMM_GATE_UP:
           m->gemm(w, T, QWEN_HIDDEN, QWEN_INTERMEDIATE, f.gate, f.sw_gate, nullptr, w.tmp, QWEN_INTERMEDIATE,
