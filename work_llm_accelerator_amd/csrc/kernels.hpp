@@ -27,6 +27,11 @@ constexpr int kMaxQuantRow = 8960;  // widest activation row that is quantized
 constexpr int kAttnMaxSplits = 64;  // most KV splits of one decode-attention sequence
 constexpr int kNormNone = 0, kNormDecode = 1, kNormPrefill = 2;
 constexpr int kEpiStore = 0, kEpiSiluMul = 1, kEpiResidual = 2;
+// Epilogues fused into the split-K reduce kernel (GEMMs of at most kSplitTokens tokens):
+//   kFuseQkvRope:   [q|k|v] rows + bias, decode RoPE of q and k, K/V cache append (kEpiStore);
+//   kFuseNormQuant: the finished row (kEpiStore, or kEpiResidual after bf16 rounding) is RMS-normalized
+//                   with norm_w and quantized into xq_out / sx_out / sums_out for the next projection.
+constexpr int kFuseNone = 0, kFuseQkvRope = 1, kFuseNormQuant = 2;
 
 // Bytes of the two-limb code of `rows` activation rows of width n.
 inline size_t xq_bytes(size_t rows, size_t n) { return rows * n * 2u; }
@@ -49,6 +54,20 @@ struct GemmArgs {
   int round_bf16;       // kEpiResidual: round the output to bf16 (driver rounding)
   int prefill_silu;     // kEpiSiluMul: 1 = approx_exp SiLU (prefill), 0 = expf SiLU (decode)
   float* part;          // optional fp32 workspace for K splits across blocks: [splits][tokens][out]
+  int fuse;             // kFuse*: epilogue of the reduce kernel (needs part; tokens <= kSplitTokens)
+  // kFuseQkvRope (token t is sequence t at position pos[t]; positions outside [0, limit) are skipped)
+  const int* pos;
+  const float* rope;    // [position][cos 64 | sin 64]
+  float* k_cache;
+  float* v_cache;
+  size_t seq_stride;
+  int limit;
+  // kFuseNormQuant
+  const float* norm_w;
+  int norm;             // kNormDecode or kNormPrefill
+  int8_t* xq_out;
+  float* sx_out;
+  int* sums_out;
 };
 
 // K splits across blocks: at most kMaxSplits splits, only for GEMMs of at most kSplitTokens tokens;

@@ -181,40 +181,32 @@ __device__ void quantize_row_lds(const float* __restrict__ v, int n, int8_t* __r
 }
 
 // ---------------------------------------------------------------------------------------------
-// RMSNorm (optional) + quantization, one block per token row.
-//   NORM_DECODE: decode rmsnorm (double mean square, qwen_decode_attention_kernel.cpp:13-27)
-//   NORM_PREFILL: prefill rmsnorm (float, approx_sqrt, qwen_prefill_attention_kernel.cpp:112-126)
-//   NORM_NONE: quantize x as is.
-// Optionally writes the normalized fp32 row to xn.
+// RMSNorm (optional) + quantization of one token row held by a 256-thread block as float4 v[j] at
+// float4 index threadIdx.x + 256*j (n % 128 == 0, n <= 1024*NV):
+//   kNormDecode: decode rmsnorm (double mean square, qwen_decode_attention_kernel.cpp:13-27)
+//   kNormPrefill: prefill rmsnorm (float, approx_sqrt, qwen_prefill_attention_kernel.cpp:112-126)
+//   kNormNone: quantize the row as is.
+// Writes the two-limb code ([K chunk][limb][128 bytes]), the token scale and the limb sums, and
+// optionally the normalized fp32 row (xn_row).
 // ---------------------------------------------------------------------------------------------
-constexpr int kQuantVecs = (kMaxQuantRow / 4 + 255) / 256;  // float4 per thread for the widest row
-
-__global__ void __launch_bounds__(256) norm_quant_kernel(const float* __restrict__ x, size_t x_stride, int n,
-                                                         const float* __restrict__ w, int norm,
-                                                         int8_t* __restrict__ xq, float* __restrict__ sx,
-                                                         int* __restrict__ sums, float* __restrict__ xn) {
+template <int NV>
+__device__ __forceinline__ void norm_quant_row(float4 (&v)[NV], int n, const float* __restrict__ w, int norm,
+                                               int8_t* __restrict__ row, float* __restrict__ sx_out,
+                                               int* __restrict__ sums_out, float* __restrict__ xn_row) {
   __shared__ float red_f[4];
   __shared__ double red_d[4];
   __shared__ int red_i[4];
-  const int t = blockIdx.x;
   const int n4 = n >> 2;
-  const float4* xr = reinterpret_cast<const float4*>(x + (size_t)t * x_stride);
-  float4 v[kQuantVecs];
-#pragma unroll
-  for (int j = 0; j < kQuantVecs; ++j) {
-    const int k = threadIdx.x + 256 * j;
-    v[j] = k < n4 ? xr[k] : make_float4(0, 0, 0, 0);
-  }
   if (norm == kNormDecode) {
     double ss = 0.0;
 #pragma unroll
-    for (int j = 0; j < kQuantVecs; ++j)
+    for (int j = 0; j < NV; ++j)
       ss += (double)v[j].x * v[j].x + (double)v[j].y * v[j].y + (double)v[j].z * v[j].z + (double)v[j].w * v[j].w;
     ss = block_sum4_d(ss, red_d);
     const double inv = 1.0 / sqrt(ss / (double)n + (double)QWEN_RMS_EPS);
     const float4* w4 = reinterpret_cast<const float4*>(w);
 #pragma unroll
-    for (int j = 0; j < kQuantVecs; ++j) {
+    for (int j = 0; j < NV; ++j) {
       const int k = threadIdx.x + 256 * j;
       if (k < n4) {
         const float4 ww = w4[k];
@@ -225,12 +217,12 @@ __global__ void __launch_bounds__(256) norm_quant_kernel(const float* __restrict
   } else if (norm == kNormPrefill) {
     float ss = 0.0f;
 #pragma unroll
-    for (int j = 0; j < kQuantVecs; ++j) ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
+    for (int j = 0; j < NV; ++j) ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
     ss = block_sum4(ss, red_f);
     const float inv = 1.0f / approx_sqrt(ss / (float)n + QWEN_RMS_EPS);
     const float4* w4 = reinterpret_cast<const float4*>(w);
 #pragma unroll
-    for (int j = 0; j < kQuantVecs; ++j) {
+    for (int j = 0; j < NV; ++j) {
       const int k = threadIdx.x + 256 * j;
       if (k < n4) {
         const float4 ww = w4[k];
@@ -238,24 +230,23 @@ __global__ void __launch_bounds__(256) norm_quant_kernel(const float* __restrict
       }
     }
   }
-  if (xn) {
-    float4* xo = reinterpret_cast<float4*>(xn + (size_t)t * n);
+  if (xn_row) {
+    float4* xo = reinterpret_cast<float4*>(xn_row);
 #pragma unroll
-    for (int j = 0; j < kQuantVecs; ++j) {
+    for (int j = 0; j < NV; ++j) {
       const int k = threadIdx.x + 256 * j;
       if (k < n4) xo[k] = v[j];
     }
   }
   float amax = 0.0f;
 #pragma unroll
-  for (int j = 0; j < kQuantVecs; ++j)
+  for (int j = 0; j < NV; ++j)
     amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
   amax = block_max4(amax, red_f);
   const float inv = amax > 0.0f ? (float)kQuantMax / amax : 0.0f;
-  int8_t* row = xq + (size_t)t * (size_t)(2 * n);
   int sh = 0, sl = 0;
 #pragma unroll
-  for (int j = 0; j < kQuantVecs; ++j) {
+  for (int j = 0; j < NV; ++j) {
     const int k = threadIdx.x + 256 * j;
     if (k < n4) {
       const float e[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
@@ -279,10 +270,31 @@ __global__ void __launch_bounds__(256) norm_quant_kernel(const float* __restrict
   sh = block_sum4_i(sh, red_i);
   sl = block_sum4_i(sl, red_i);
   if (threadIdx.x == 0) {
-    sx[t] = amax > 0.0f ? amax / (float)kQuantMax : 1.0f;
-    sums[2 * t] = sh;
-    sums[2 * t + 1] = sl;
+    *sx_out = amax > 0.0f ? amax / (float)kQuantMax : 1.0f;
+    sums_out[0] = sh;
+    sums_out[1] = sl;
   }
+}
+
+// One block per token row: loads x[t] and runs norm_quant_row.  grid = rows, block = 256.
+constexpr int kQuantVecs = (kMaxQuantRow / 4 + 255) / 256;  // float4 per thread for the widest row
+
+template <int NV>
+__global__ void __launch_bounds__(256) norm_quant_kernel(const float* __restrict__ x, size_t x_stride, int n,
+                                                         const float* __restrict__ w, int norm,
+                                                         int8_t* __restrict__ xq, float* __restrict__ sx,
+                                                         int* __restrict__ sums, float* __restrict__ xn) {
+  const int t = blockIdx.x;
+  const int n4 = n >> 2;
+  const float4* xr = reinterpret_cast<const float4*>(x + (size_t)t * x_stride);
+  float4 v[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int k = threadIdx.x + 256 * j;
+    v[j] = k < n4 ? xr[k] : make_float4(0, 0, 0, 0);
+  }
+  norm_quant_row<NV>(v, n, w, norm, xq + (size_t)t * (size_t)(2 * n), sx + t, sums + 2 * t,
+                     xn ? xn + (size_t)t * n : nullptr);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -437,6 +449,21 @@ __global__ void __launch_bounds__(256) gemm_i8_kernel(GemmArgs a) {
 
   // Epilogue: lane holds rows row0..row0+3 of token column `col` of each column tile.
   const int row0 = rt * 16 + 4 * g;
+  if (!DUAL && a.fuse != kFuseNone) {
+    // fused reduce follows: fp32 partials sw*sx*(256*sumH + sumL) into split 0 of a.part
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+      const int tok = tok0 + n * 16 + col;
+      if (tok >= a.tokens) continue;
+      const double sx = (double)a.sx[tok];
+      float out[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        out[r] = (float)(((double)accH[n][r] * 256.0 + (double)accL[n][r]) * sx) * a.sw[row0 + r];
+      *reinterpret_cast<float4*>(a.part + (size_t)tok * a.out_dim + row0) = make_float4(out[0], out[1], out[2], out[3]);
+    }
+    return;
+  }
   float sw[4], sw2[4], bias[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
@@ -502,6 +529,24 @@ __device__ __forceinline__ void wait_vmcnt() {
   // gfx9 s_waitcnt: vmcnt[3:0] | expcnt[6:4] (7 = no wait) | lgkmcnt[11:8] (15 = no wait) | vmcnt[5:4] << 14
   __builtin_amdgcn_s_waitcnt((VMCNT & 0xF) | (0x7 << 4) | (0xF << 8) | ((VMCNT >> 4) << 14));
 }
+
+// LDS byte address of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+// 16-byte LDS read issued as is: the result may only be used after an lgkm_wait_tie covering it.
+__device__ __forceinline__ v4i lds_read_b128(uint32_t addr) {
+  v4i r;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(addr) : "memory");
+  return r;
+}
+// Waits until at most N LDS reads are outstanding; the tied registers are the ones this makes valid.
+template <int N>
+__device__ __forceinline__ void lgkm_wait_tie(v4i& a, v4i& b, v4i& c, v4i& d) {
+  asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "i"(N) : "memory");
+}
+// Orders later uses of r after the preceding waits (no instruction).
+__device__ __forceinline__ void reg_tie(v4i& r) { asm volatile("" : "+v"(r)); }
 
 template <int NT, int RTW, int NBUF, int EPI, bool DUAL>
 __global__ void __launch_bounds__(256) gemm_i8_pipe_kernel(GemmArgs a) {
@@ -587,30 +632,52 @@ __global__ void __launch_bounds__(256) gemm_i8_pipe_kernel(GemmArgs a) {
         wait_vmcnt<(NBUF - 2) * OPS>();
         __builtin_amdgcn_s_barrier();
         issue(i + NBUF - 1, XS[(sidx + NBUF - 1) % NBUF], WS[(sidx + NBUF - 1) % NBUF]);
-        const uint8_t* xst = XS[sidx];
-        const uint8_t* wst = WS[sidx];
-        v4i a1[D][RTW], a2[D][RTW];
+        // LDS reads of the stage: the weight tiles and token tile 0 first, then tile n+1 while the
+        // matrix cores work on tile n.  They are issued as ds_read_b128 with explicit lgkmcnt waits:
+        // the compiler cannot tell which stage an in-flight direct load writes, and would otherwise
+        // drain every outstanding load (s_waitcnt vmcnt(0)) before each read, i.e. the whole pipeline.
+        const uint32_t wa = lds_addr(WS[sidx]) + (uint32_t)(wave * D * RTW * 1024 + lane * 16);
+        const uint32_t xb = lds_addr(XS[sidx]) + (uint32_t)(col * 256);
+        const uint32_t xo[4] = {xb + (uint32_t)(((2 * g) ^ col) << 4), xb + (uint32_t)(((2 * g + 1) ^ col) << 4),
+                                xb + (uint32_t)(((8 + 2 * g) ^ col) << 4), xb + (uint32_t)(((9 + 2 * g) ^ col) << 4)};
+        v4i wr[D][RTW];
 #pragma unroll
         for (int d = 0; d < D; ++d)
 #pragma unroll
-          for (int r = 0; r < RTW; ++r)
-            unpack16(*reinterpret_cast<const uint4*>(wst + ((wave * D + d) * RTW + r) * 1024 + lane * 16), a1[d][r],
-                     a2[d][r]);
+          for (int r = 0; r < RTW; ++r) wr[d][r] = lds_read_b128(wa + (uint32_t)((d * RTW + r) * 1024));
+        v4i bx[2][4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) bx[0][q] = lds_read_b128(xo[q]);
+        v4i a1[D][RTW], a2[D][RTW];
 #pragma unroll
         for (int n = 0; n < NT; ++n) {
-          const uint8_t* xr = xst + (n * 16 + col) * 256;
-          const v4i bh1 = *reinterpret_cast<const v4i*>(xr + (((2 * g) ^ col) << 4));
-          const v4i bh2 = *reinterpret_cast<const v4i*>(xr + (((2 * g + 1) ^ col) << 4));
-          const v4i bl1 = *reinterpret_cast<const v4i*>(xr + (((8 + 2 * g) ^ col) << 4));
-          const v4i bl2 = *reinterpret_cast<const v4i*>(xr + (((9 + 2 * g) ^ col) << 4));
+          v4i* cur = bx[n & 1];
+          if (n + 1 < NT) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) bx[(n + 1) & 1][q] = lds_read_b128(xo[q] + (uint32_t)((n + 1) * 16 * 256));
+            lgkm_wait_tie<4>(cur[0], cur[1], cur[2], cur[3]);
+          } else {
+            lgkm_wait_tie<0>(cur[0], cur[1], cur[2], cur[3]);
+          }
+          if (n == 0) {
+#pragma unroll
+            for (int d = 0; d < D; ++d)
+#pragma unroll
+              for (int r = 0; r < RTW; ++r) {
+                reg_tie(wr[d][r]);  // landed before token tile 0 (LDS reads complete in order)
+                unpack16(make_uint4((uint32_t)wr[d][r][0], (uint32_t)wr[d][r][1], (uint32_t)wr[d][r][2],
+                                    (uint32_t)wr[d][r][3]),
+                         a1[d][r], a2[d][r]);
+              }
+          }
 #pragma unroll
           for (int d = 0; d < D; ++d)
 #pragma unroll
             for (int r = 0; r < RTW; ++r) {
-              accH[d][r][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[d][r], bh1, accH[d][r][n], 0, 0, 0);
-              accH[d][r][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2[d][r], bh2, accH[d][r][n], 0, 0, 0);
-              accL[d][r][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[d][r], bl1, accL[d][r][n], 0, 0, 0);
-              accL[d][r][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2[d][r], bl2, accL[d][r][n], 0, 0, 0);
+              accH[d][r][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[d][r], cur[0], accH[d][r][n], 0, 0, 0);
+              accH[d][r][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2[d][r], cur[1], accH[d][r][n], 0, 0, 0);
+              accL[d][r][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[d][r], cur[2], accL[d][r][n], 0, 0, 0);
+              accL[d][r][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2[d][r], cur[3], accL[d][r][n], 0, 0, 0);
             }
         }
       }
@@ -618,7 +685,7 @@ __global__ void __launch_bounds__(256) gemm_i8_pipe_kernel(GemmArgs a) {
   }
   wait_vmcnt<0>();  // the trailing reloads land before the wave moves on
 
-  const bool partial = gridDim.z > 1;
+  const bool partial = gridDim.z > 1 || (!DUAL && a.fuse != kFuseNone);  // a reduce kernel finishes
 #pragma unroll
   for (int r = 0; r < RTW; ++r) {
     if (!rt_ok[r]) continue;
@@ -671,6 +738,213 @@ __global__ void __launch_bounds__(256) gemm_i8_pipe_kernel(GemmArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Skinny GEMM for decode batches (the same y = W x products as the kernels above, for few tokens).
+// A block owns 16 tokens (token tile tt), 4*RTW row tiles (row group rg: wave w holds row tiles
+// rg*4*RTW + w + 4r, r < RTW) and NKC K chunks (split z).  Every load of the block is issued at
+// once: its activation slice goes to LDS by direct loads ([chunk][token][256 B], 16-byte segments
+// XOR-swizzled by token), its weight tiles go straight to registers (RTW*D*NKC x 16 B per lane);
+// after one wait the matrix cores run from registers and LDS.  Blocks that share weights (the
+// token tiles of one (rg, z)) are given block ids on the same XCD (ids are dealt to the 8 XCDs
+// round robin), so the weights come from HBM once and from that XCD's L2 after.
+// Epilogues: EPI as in gemm_i8_kernel, or fp32 partials to a.part[z] (K splits, or a fused reduce
+// step), or with ROPE the decode RoPE + K/V cache append of the fused [q | k | v] projection (RTW=2:
+// wave w holds rows p and p + 64 of head rg, p = 16w + 4g + q).
+// grid = 8 * tt_count * ceil(groups / 8) blocks of 256, groups = row groups x splits.
+// ---------------------------------------------------------------------------------------------
+template <int RTW, bool DUAL, int EPI, int NKC, bool ROPE>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
+gemm_skinny_kernel(GemmArgs a, int tt_count, int rg_count, int splits) {
+  constexpr int D = DUAL ? 2 : 1;
+  __shared__ __align__(16) uint8_t xs[NKC * 16 * 256];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int g = lane >> 4;
+  const int col = lane & 15;
+  const int xcd = blockIdx.x & 7;
+  const int j = blockIdx.x >> 3;
+  const int tt = j % tt_count;
+  const int grp = (j / tt_count) * 8 + xcd;
+  if (grp >= rg_count * splits) return;  // block-uniform: ids past the last group
+  const int rg = grp % rg_count;
+  const int z = grp / rg_count;
+  const int nkc_all = a.in_dim / kKChunk;
+  const int kc0 = z * NKC;
+  const int tok0 = tt * 16;
+  const int row_tiles = a.out_dim / 16;
+  const size_t row_stride_x = (size_t)a.in_dim * 2u;
+
+  // activation slice -> LDS: chunk c, rows 4q..4q+3 per load (1 KiB), wave w takes chunks w, w+4, ..
+  for (int c = wave; c < NKC; c += 4) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int row = 4 * q + (lane >> 4);
+      const int tok = min(tok0 + row, a.tokens - 1);  // rows past the last token reload a valid row
+      const int seg = (lane & 15) ^ row;
+      const uint8_t* src = reinterpret_cast<const uint8_t*>(a.xq) + (size_t)tok * row_stride_x +
+                           (size_t)(kc0 + c) * 256u + seg * 16;
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src),
+                                       (__attribute__((address_space(3))) void*)(xs + (c * 16 + 4 * q) * 256), 16, 0,
+                                       0);
+    }
+  }
+  // weight tiles -> registers
+  uint4 wv[RTW][D][NKC];
+  bool ok[RTW];
+#pragma unroll
+  for (int r = 0; r < RTW; ++r) {
+    const int rt = rg * 4 * RTW + wave + 4 * r;
+    ok[r] = rt < row_tiles;
+    const size_t base = ((size_t)(ok[r] ? rt : 0) * nkc_all + kc0) * 64u + lane;
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const uint4* wp = reinterpret_cast<const uint4*>(d ? a.wp2 : a.wp) + base;
+#pragma unroll
+      for (int c = 0; c < NKC; ++c) wv[r][d][c] = wp[(size_t)c * 64u];  // cached: reused by the XCD's other token tiles
+    }
+  }
+  wait_vmcnt<0>();
+  __syncthreads();
+
+  v4i accH[RTW][D], accL[RTW][D];
+#pragma unroll
+  for (int r = 0; r < RTW; ++r)
+#pragma unroll
+    for (int d = 0; d < D; ++d) accH[r][d] = accL[r][d] = v4i{0, 0, 0, 0};
+#pragma unroll
+  for (int c = 0; c < NKC; ++c) {
+    const uint8_t* xr = xs + (c * 16 + col) * 256;
+    const v4i bh1 = *reinterpret_cast<const v4i*>(xr + (((2 * g) ^ col) << 4));
+    const v4i bh2 = *reinterpret_cast<const v4i*>(xr + (((2 * g + 1) ^ col) << 4));
+    const v4i bl1 = *reinterpret_cast<const v4i*>(xr + (((8 + 2 * g) ^ col) << 4));
+    const v4i bl2 = *reinterpret_cast<const v4i*>(xr + (((9 + 2 * g) ^ col) << 4));
+#pragma unroll
+    for (int r = 0; r < RTW; ++r)
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+        v4i a1, a2;
+        unpack16(wv[r][d][c], a1, a2);
+        accH[r][d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bh1, accH[r][d], 0, 0, 0);
+        accH[r][d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2, bh2, accH[r][d], 0, 0, 0);
+        accL[r][d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bl1, accL[r][d], 0, 0, 0);
+        accL[r][d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2, bl2, accL[r][d], 0, 0, 0);
+      }
+  }
+
+  // epilogue: lane holds rows 16*rt + 4g + q (q < 4) of token tok0 + col
+  const int tok = tok0 + col;
+  if (tok >= a.tokens) return;
+  const double sx = (double)a.sx[tok];
+  const bool partial = splits > 1 || (!DUAL && !ROPE && a.fuse != kFuseNone);
+  if (partial) {
+#pragma unroll
+    for (int r = 0; r < RTW; ++r) {
+      if (!ok[r]) continue;
+      const int row0 = (rg * 4 * RTW + wave + 4 * r) * 16 + 4 * g;
+      float out[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        out[q] = (float)(((double)accH[r][0][q] * 256.0 + (double)accL[r][0][q]) * sx) * a.sw[row0 + q];
+      *reinterpret_cast<float4*>(a.part + ((size_t)z * a.tokens + tok) * a.out_dim + row0) =
+          make_float4(out[0], out[1], out[2], out[3]);
+    }
+    return;
+  }
+  const int sh8 = 8 * a.sums[2 * tok];
+  const int sl8 = 8 * a.sums[2 * tok + 1];
+  float y[RTW][4];
+#pragma unroll
+  for (int r = 0; r < RTW; ++r) {
+    const int row0 = (rg * 4 * RTW + wave + 4 * r) * 16 + 4 * g;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (!ok[r]) {
+        y[r][q] = 0.0f;
+        continue;
+      }
+      const double tot = (double)(accH[r][0][q] - sh8) * 256.0 + (double)(accL[r][0][q] - sl8);
+      const float v = (float)(tot * sx) * a.sw[row0 + q];
+      if (EPI == kEpiSiluMul) {
+        const double tot2 = (double)(accH[r][D - 1][q] - sh8) * 256.0 + (double)(accL[r][D - 1][q] - sl8);
+        const float u = (float)(tot2 * sx) * a.sw2[row0 + q];
+        const float sg = a.prefill_silu ? silu_prefill(v) : silu_decode(v);
+        y[r][q] = sg * u;
+      } else if (EPI == kEpiResidual) {
+        y[r][q] = a.resid[(size_t)tok * a.resid_stride + row0 + q] + v;
+      } else {
+        y[r][q] = v + (a.bias ? a.bias[row0 + q] : 0.0f);
+      }
+    }
+  }
+  if constexpr (ROPE) {
+    // rows p (tile r=0) and p + 64 (tile r=1) of head rg: 12 q heads, then 2 k heads, then 2 v heads
+    const int P = a.pos[tok];
+    const bool in = P >= 0 && P < a.limit;
+    const int head = rg;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int p = 16 * wave + 4 * g + q;
+      float c = 1.0f, sn = 0.0f;
+      if (in) {
+        c = a.rope[(size_t)P * 128 + p];
+        sn = a.rope[(size_t)P * 128 + 64 + p];
+      }
+      const float e = y[0][q], od = y[1][q];
+      if (head < QWEN_Q_HEADS) {
+        float* yq = a.y + (size_t)tok * a.y_stride + head * QWEN_HEAD_DIM + p;
+        yq[0] = in ? e * c - od * sn : e;
+        yq[64] = in ? od * c + e * sn : od;
+      } else if (in) {
+        const size_t cache_row = (size_t)tok * a.seq_stride + (size_t)P * QWEN_KV_WIDTH;
+        if (head < QWEN_Q_HEADS + QWEN_KV_HEADS) {
+          float* kc = a.k_cache + cache_row + (head - QWEN_Q_HEADS) * QWEN_HEAD_DIM + p;
+          kc[0] = e * c - od * sn;
+          kc[64] = od * c + e * sn;
+        } else {
+          float* vc = a.v_cache + cache_row + (head - QWEN_Q_HEADS - QWEN_KV_HEADS) * QWEN_HEAD_DIM + p;
+          vc[0] = e;
+          vc[64] = od;
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < RTW; ++r) {
+      if (!ok[r]) continue;
+      const int row0 = (rg * 4 * RTW + wave + 4 * r) * 16 + 4 * g;
+      float o[4] = {y[r][0], y[r][1], y[r][2], y[r][3]};
+      if (EPI == kEpiResidual && a.y_raw)
+        *reinterpret_cast<float4*>(a.y_raw + (size_t)tok * a.y_stride + row0) = make_float4(o[0], o[1], o[2], o[3]);
+      if (EPI == kEpiResidual && a.round_bf16)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) o[q] = round_bf16(o[q]);
+      *reinterpret_cast<float4*>(a.y + (size_t)tok * a.y_stride + row0) = make_float4(o[0], o[1], o[2], o[3]);
+    }
+  }
+}
+
+// Sum over z < splits of part[z * zstride + off .. + 3] in z order.  The loads of 8 splits are all
+// issued before the first add, so a reduce costs one memory round trip per 8 splits.
+__device__ __forceinline__ float4 sum_splits4(const float* __restrict__ part, size_t zstride, size_t off, int splits) {
+  float4 acc = make_float4(0, 0, 0, 0);
+  for (int z0 = 0; z0 < splits; z0 += 8) {
+    float4 pz[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      pz[u] = z0 + u < splits ? *reinterpret_cast<const float4*>(part + (size_t)(z0 + u) * zstride + off)
+                              : make_float4(0, 0, 0, 0);
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (z0 + u < splits) {
+        acc.x += pz[u].x;
+        acc.y += pz[u].y;
+        acc.z += pz[u].z;
+        acc.w += pz[u].w;
+      }
+  }
+  return acc;
+}
+
 // Sums the split partials in z order and applies the offset correction and the epilogue
 // (kEpiStore with bias, or kEpiResidual with bf16 rounding).  One thread per 4 outputs.
 template <int EPI>
@@ -680,14 +954,7 @@ __global__ void __launch_bounds__(256) gemm_splitk_reduce_kernel(GemmArgs a, int
   if (i >= quads) return;
   const int tok = (int)(i / (a.out_dim / 4));
   const int row0 = (int)(i % (a.out_dim / 4)) * 4;
-  float4 acc = make_float4(0, 0, 0, 0);
-  for (int z = 0; z < splits; ++z) {
-    const float4 p = *reinterpret_cast<const float4*>(a.part + ((size_t)z * a.tokens + tok) * a.out_dim + row0);
-    acc.x += p.x;
-    acc.y += p.y;
-    acc.z += p.z;
-    acc.w += p.w;
-  }
+  const float4 acc = sum_splits4(a.part, (size_t)a.tokens * a.out_dim, (size_t)tok * a.out_dim + row0, splits);
   const double corr = -8.0 * (256.0 * (double)a.sums[2 * tok] + (double)a.sums[2 * tok + 1]) * (double)a.sx[tok];
   float out[4] = {acc.x, acc.y, acc.z, acc.w};
 #pragma unroll
@@ -701,6 +968,119 @@ __global__ void __launch_bounds__(256) gemm_splitk_reduce_kernel(GemmArgs a, int
     }
   }
   *reinterpret_cast<float4*>(a.y + (size_t)tok * a.y_stride + row0) = make_float4(out[0], out[1], out[2], out[3]);
+}
+
+// Finishes output (tok, row) from its split sum: offset correction and bias, the same arithmetic as
+// gemm_splitk_reduce_kernel.
+__device__ __forceinline__ float finish_one(const GemmArgs& a, float acc, int row, double corr) {
+  return acc + (float)(corr * (double)a.sw[row]) + (a.bias ? a.bias[row] : 0.0f);
+}
+
+// kFuseQkvRope: reduce of the fused [q | k | v] projection (2048 rows) for decode token t, bias, RoPE
+// of the 12 q heads (in place in a.y) and the 2 k heads, and the K/V cache append at position
+// pos[t] of sequence t (qwen_decode_attention_kernel.cpp:29-42,100-111 semantics; positions outside
+// [0, limit) leave q unrotated and the cache untouched).  Thread t of the block owns rotation pair
+// p = t & 63 of heads (t >> 6) + 4k, k < 4 (heads 0-11 q, 12-13 k, 14-15 v).  grid = tokens, block = 256.
+__global__ void __launch_bounds__(256) reduce_qkv_rope_kernel(GemmArgs a, int splits) {
+  const int tok = blockIdx.x;
+  const int p = threadIdx.x & 63;
+  const double corr = -8.0 * (256.0 * (double)a.sums[2 * tok] + (double)a.sums[2 * tok + 1]) * (double)a.sx[tok];
+  const int P = a.pos[tok];
+  const bool in = P >= 0 && P < a.limit;
+  float c = 1.0f, sn = 0.0f;
+  if (in) {
+    c = a.rope[(size_t)P * 128 + p];
+    sn = a.rope[(size_t)P * 128 + 64 + p];
+  }
+  float* yq = a.y + (size_t)tok * a.y_stride;
+  float* kc = a.k_cache + (size_t)tok * a.seq_stride + (size_t)(in ? P : 0) * QWEN_KV_WIDTH;
+  float* vc = a.v_cache + (size_t)tok * a.seq_stride + (size_t)(in ? P : 0) * QWEN_KV_WIDTH;
+  // split sums of the thread's 8 rows (4 pairs), 4 splits per batch of loads, in z order
+  const size_t zstride = (size_t)a.tokens * a.out_dim;
+  const float* pt = a.part + (size_t)tok * a.out_dim + p;
+  float sum[4][2];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) sum[k][0] = sum[k][1] = 0.0f;
+  for (int z0 = 0; z0 < splits; z0 += 4) {
+    float pz[4][4][2];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+          pz[u][k][hh] = z0 + u < splits
+                             ? pt[(size_t)(z0 + u) * zstride + ((threadIdx.x >> 6) + 4 * k) * QWEN_HEAD_DIM + 64 * hh]
+                             : 0.0f;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (z0 + u < splits)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          sum[k][0] += pz[u][k][0];
+          sum[k][1] += pz[u][k][1];
+        }
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int head = (threadIdx.x >> 6) + 4 * k;
+    const int r0 = head * QWEN_HEAD_DIM + p;
+    const float e = finish_one(a, sum[k][0], r0, corr);
+    const float od = finish_one(a, sum[k][1], r0 + 64, corr);
+    if (head < QWEN_Q_HEADS) {
+      yq[r0] = in ? e * c - od * sn : e;
+      yq[r0 + 64] = in ? od * c + e * sn : od;
+    } else if (!in) {
+      continue;
+    } else if (head < QWEN_Q_HEADS + QWEN_KV_HEADS) {
+      const int base = (head - QWEN_Q_HEADS) * QWEN_HEAD_DIM + p;
+      kc[base] = e * c - od * sn;
+      kc[base + 64] = od * c + e * sn;
+    } else {
+      const int base = (head - QWEN_Q_HEADS - QWEN_KV_HEADS) * QWEN_HEAD_DIM + p;
+      vc[base] = e;
+      vc[base + 64] = od;
+    }
+  }
+}
+
+// kFuseNormQuant: reduce of a 1536-row projection for token t with the EPI epilogue (kEpiStore: bias;
+// kEpiResidual: residual, optional raw copy, optional bf16 rounding), the finished row written to
+// a.y, then RMSNorm(norm_w) + two-limb quantization of that row into xq_out / sx_out / sums_out.
+// Thread t owns float4 columns t and t + 256.  grid = tokens, block = 256.
+template <int EPI>
+__global__ void __launch_bounds__(256) reduce_norm_quant_kernel(GemmArgs a, int splits) {
+  const int tok = blockIdx.x;
+  const int n4 = a.out_dim >> 2;
+  const double corr = -8.0 * (256.0 * (double)a.sums[2 * tok] + (double)a.sums[2 * tok + 1]) * (double)a.sx[tok];
+  float4 v[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int k = threadIdx.x + 256 * j;
+    v[j] = make_float4(0, 0, 0, 0);
+    if (k >= n4) continue;
+    const int row0 = 4 * k;
+    const float4 acc = sum_splits4(a.part, (size_t)a.tokens * a.out_dim, (size_t)tok * a.out_dim + row0, splits);
+    float out[4] = {acc.x, acc.y, acc.z, acc.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float val = out[q] + (float)(corr * (double)a.sw[row0 + q]);
+      if (EPI == kEpiResidual) {
+        out[q] = a.resid[(size_t)tok * a.resid_stride + row0 + q] + val;
+      } else {
+        out[q] = val + (a.bias ? a.bias[row0 + q] : 0.0f);
+      }
+    }
+    if (EPI == kEpiResidual && a.y_raw)
+      *reinterpret_cast<float4*>(a.y_raw + (size_t)tok * a.y_stride + row0) = make_float4(out[0], out[1], out[2], out[3]);
+    if (EPI == kEpiResidual && a.round_bf16)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) out[q] = round_bf16(out[q]);
+    v[j] = make_float4(out[0], out[1], out[2], out[3]);
+    *reinterpret_cast<float4*>(a.y + (size_t)tok * a.y_stride + row0) = v[j];
+  }
+  norm_quant_row<2>(v, a.out_dim, a.norm_w, a.norm, a.xq_out + (size_t)tok * (size_t)(2 * a.out_dim), a.sx_out + tok,
+                    a.sums_out + 2 * tok, nullptr);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1145,7 +1525,11 @@ void launch_repack_int4(const uint8_t* W, int out_dim, int in_dim, uint8_t* WP, 
 
 void launch_norm_quant(const float* x, size_t x_stride, int rows, int n, const float* w, int norm, int8_t* xq,
                        float* sx, int* sums, float* xn, hipStream_t st) {
-  hipLaunchKernelGGL(norm_quant_kernel, dim3(rows), dim3(256), 0, st, x, x_stride, n, w, norm, xq, sx, sums, xn);
+  if (n <= 2048)
+    hipLaunchKernelGGL(norm_quant_kernel<2>, dim3(rows), dim3(256), 0, st, x, x_stride, n, w, norm, xq, sx, sums, xn);
+  else
+    hipLaunchKernelGGL(norm_quant_kernel<kQuantVecs>, dim3(rows), dim3(256), 0, st, x, x_stride, n, w, norm, xq, sx,
+                       sums, xn);
 }
 
 template <int NT, int KSPLIT, int EPI, bool DUAL>
@@ -1156,16 +1540,64 @@ static void launch_gemm_t(const GemmArgs& a, hipStream_t st) {
   hipLaunchKernelGGL((gemm_i8_kernel<NT, KSPLIT, EPI, DUAL>), grid, dim3(256), 0, st, a);
 }
 
+// The reduce step after a GEMM that wrote fp32 partials: plain (bias / residual epilogue) or fused.
+template <int EPI>
+static void launch_reduce(const GemmArgs& a, int splits, hipStream_t st) {
+  if (a.fuse == kFuseQkvRope) {
+    hipLaunchKernelGGL(reduce_qkv_rope_kernel, dim3(a.tokens), dim3(256), 0, st, a, splits);
+  } else if (a.fuse == kFuseNormQuant) {
+    hipLaunchKernelGGL((reduce_norm_quant_kernel<EPI>), dim3(a.tokens), dim3(256), 0, st, a, splits);
+  } else {
+    const size_t quads = (size_t)a.tokens * (a.out_dim / 4);
+    hipLaunchKernelGGL((gemm_splitk_reduce_kernel<EPI>), dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, st, a,
+                       splits);
+  }
+}
+
 template <int NT, int RTW, int NBUF, int EPI, bool DUAL>
 static void launch_gemm_pipe_t(const GemmArgs& a, int splits, hipStream_t st) {
   const int row_tiles = a.out_dim / 16;
   const dim3 grid((a.tokens + 16 * NT - 1) / (16 * NT), (row_tiles + 4 * RTW - 1) / (4 * RTW), splits);
   hipLaunchKernelGGL((gemm_i8_pipe_kernel<NT, RTW, NBUF, EPI, DUAL>), grid, dim3(256), 0, st, a);
-  if (splits > 1) {
-    const size_t quads = (size_t)a.tokens * (a.out_dim / 4);
-    hipLaunchKernelGGL((gemm_splitk_reduce_kernel<EPI>), dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, st, a,
-                       splits);
+  if (!DUAL && (splits > 1 || a.fuse != kFuseNone)) launch_reduce<EPI>(a, splits, st);
+}
+
+// Skinny GEMMs for at most kSkinnyTokens tokens with in_dim 1536 (12 K chunks in one block) or 8960
+// (5 splits of 14 chunks, finished by the reduce step).  Returns false for other shapes.
+constexpr int kSkinnyTokens = 64;
+
+template <int RTW, bool DUAL, int EPI, int NKC, bool ROPE>
+static void launch_skinny_t(const GemmArgs& a, int rg_count, int splits, hipStream_t st) {
+  const int tt = (a.tokens + 15) / 16;
+  const int groups = rg_count * splits;
+  const int blocks = 8 * tt * ((groups + 7) / 8);
+  hipLaunchKernelGGL((gemm_skinny_kernel<RTW, DUAL, EPI, NKC, ROPE>), dim3(blocks), dim3(256), 0, st, a, tt, rg_count,
+                     splits);
+}
+
+template <int EPI, bool DUAL>
+static bool launch_skinny(const GemmArgs& a, hipStream_t st) {
+  if (a.tokens > kSkinnyTokens || a.out_dim % 64 != 0) return false;
+  const int row_tiles = a.out_dim / 16;
+  if (a.in_dim == QWEN_HIDDEN) {
+    if (!DUAL && EPI == kEpiStore && a.fuse == kFuseQkvRope) {
+      if (a.out_dim != QWEN_QKV_ROWS) return false;
+      launch_skinny_t<2, false, kEpiStore, 12, true>(a, row_tiles / 8, 1, st);
+      return true;
+    }
+    if (!DUAL && a.fuse != kFuseNone && !a.part) return false;
+    launch_skinny_t<1, DUAL, EPI, 12, false>(a, row_tiles / 4, 1, st);
+    if (!DUAL && a.fuse != kFuseNone) launch_reduce<EPI>(a, 1, st);
+    return true;
   }
+  if constexpr (!DUAL) {
+    if (a.in_dim == QWEN_INTERMEDIATE && a.part && a.fuse != kFuseQkvRope) {
+      launch_skinny_t<1, false, EPI, 14, false>(a, row_tiles / 4, 5, st);
+      launch_reduce<EPI>(a, 5, st);
+      return true;
+    }
+  }
+  return false;
 }
 
 // Largest divisor of nkc that is <= want (K chunks split evenly over blocks).
@@ -1183,8 +1615,10 @@ template <int EPI, bool DUAL>
 static void launch_gemm_epi(const GemmArgs& a, hipStream_t st) {
   const int nkc = a.in_dim / kKChunk;
   const int row_tiles = a.out_dim / 16;
+  if (launch_skinny<EPI, DUAL>(a, st)) return;
   if (a.tokens <= 16) {
     launch_gemm_t<1, 4, EPI, DUAL>(a, st);
+    if (!DUAL && a.fuse != kFuseNone) launch_reduce<EPI>(a, 1, st);
     return;
   }
   if constexpr (DUAL) {

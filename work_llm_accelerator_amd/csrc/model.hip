@@ -213,10 +213,12 @@ struct qwen_hip_model {
   }
 
   // ---- one step -------------------------------------------------------------------------
+  // A FAST projection of the activations quantized in w (xq, sx, sums).  `fuse` (optional) selects an
+  // epilogue fused into the split-K reduce step and carries its extra arguments.
   void gemm(const Ws& w, int tokens, int in, int out, const uint8_t* wpm, const float* sw, const float* bias,
             float* y, size_t ys, int epi, const uint8_t* wp2 = nullptr, const float* sw2 = nullptr,
-            const float* resid = nullptr, int round = 0, int prefill_silu = 0) {
-    GemmArgs g{};
+            const float* resid = nullptr, int round = 0, int prefill_silu = 0, const GemmArgs* fuse = nullptr) {
+    GemmArgs g = fuse ? *fuse : GemmArgs{};
     g.wp = wpm;
     g.wp2 = wp2;
     g.sw = sw;
@@ -243,24 +245,56 @@ struct qwen_hip_model {
                    uint64_t ls, int round) {
     const AttnDecodePlan plan = plan_attn_decode(B, max_keys);
     const Ws w = carve(B, B, plan.nsplit);
+    const bool fused = B <= kSplitTokens;
     for (int l = 0; l < layers; ++l) {
       const FastLayer& f = fast[l];
       float* kc = kc0 + (size_t)l * ls;
       float* vc = vc0 + (size_t)l * ls;
-      launch_norm_quant(hidden, QWEN_HIDDEN, B, QWEN_HIDDEN, f.ln, kNormDecode, w.xq, w.sx, w.sums, nullptr, stream);
-      gemm(w, B, QWEN_HIDDEN, (int)kQkvRows, f.qkv, f.sw_qkv, f.b_qkv, w.qkv, kQkvRows, kEpiStore);
-      launch_rope_qkv(w.qkv, (int)kQkvRows, pos, 1, max_keys, B, rope_decode, kc, vc, ss, stream);
+      // With at most kSplitTokens sequences, RoPE + KV append and the two RMSNorm + quantize steps
+      // run inside the split-K reduce kernels of the QKV, O and down projections.
+      if (l == 0 || !fused)
+        launch_norm_quant(hidden, QWEN_HIDDEN, B, QWEN_HIDDEN, f.ln, kNormDecode, w.xq, w.sx, w.sums, nullptr,
+                          stream);
+      if (fused) {
+        GemmArgs fq{};
+        fq.fuse = kFuseQkvRope;
+        fq.pos = pos;
+        fq.rope = rope_decode;
+        fq.k_cache = kc;
+        fq.v_cache = vc;
+        fq.seq_stride = ss;
+        fq.limit = max_keys;
+        gemm(w, B, QWEN_HIDDEN, (int)kQkvRows, f.qkv, f.sw_qkv, f.b_qkv, w.qkv, kQkvRows, kEpiStore, nullptr, nullptr,
+             nullptr, 0, 0, &fq);
+      } else {
+        gemm(w, B, QWEN_HIDDEN, (int)kQkvRows, f.qkv, f.sw_qkv, f.b_qkv, w.qkv, kQkvRows, kEpiStore);
+        launch_rope_qkv(w.qkv, (int)kQkvRows, pos, 1, max_keys, B, rope_decode, kc, vc, ss, stream);
+      }
       launch_attn_decode(w.qkv, (int)kQkvRows, kc, vc, ss, pos, B, max_keys, plan, w.part, w.pml, w.arrivals,
                          nullptr, w.xq, w.sx, w.sums, stream);
-      gemm(w, B, QWEN_HIDDEN, QWEN_HIDDEN, f.o, f.sw_o, nullptr, w.att, QWEN_HIDDEN, kEpiStore);
-      launch_norm_quant(w.att, QWEN_HIDDEN, B, QWEN_HIDDEN, f.post_ln, kNormDecode, w.xq, w.sx, w.sums, nullptr,
-                        stream);
+      GemmArgs fn{};
+      fn.fuse = kFuseNormQuant;
+      fn.norm = kNormDecode;
+      fn.xq_out = w.xq;
+      fn.sx_out = w.sx;
+      fn.sums_out = w.sums;
+      if (fused) {
+        fn.norm_w = f.post_ln;
+        gemm(w, B, QWEN_HIDDEN, QWEN_HIDDEN, f.o, f.sw_o, nullptr, w.att, QWEN_HIDDEN, kEpiStore, nullptr, nullptr,
+             nullptr, 0, 0, &fn);
+      } else {
+        gemm(w, B, QWEN_HIDDEN, QWEN_HIDDEN, f.o, f.sw_o, nullptr, w.att, QWEN_HIDDEN, kEpiStore);
+        launch_norm_quant(w.att, QWEN_HIDDEN, B, QWEN_HIDDEN, f.post_ln, kNormDecode, w.xq, w.sx, w.sums, nullptr,
+                          stream);
+      }
       gemm(w, B, QWEN_HIDDEN, QWEN_INTERMEDIATE, f.gate, f.sw_gate, nullptr, w.s, QWEN_INTERMEDIATE, kEpiSiluMul,
            f.up, f.sw_up, nullptr, 0, 0);
       launch_norm_quant(w.s, QWEN_INTERMEDIATE, B, QWEN_INTERMEDIATE, nullptr, kNormNone, w.xq, w.sx, w.sums,
                         nullptr, stream);
+      const bool fuse_next = fused && l + 1 < layers;  // the next layer's input RMSNorm + quantize
+      fn.norm_w = fuse_next ? fast[l + 1].ln : nullptr;
       gemm(w, B, QWEN_INTERMEDIATE, QWEN_HIDDEN, f.down, f.sw_down, nullptr, hidden, QWEN_HIDDEN, kEpiResidual,
-           nullptr, nullptr, w.att, round, 0);
+           nullptr, nullptr, w.att, round, 0, fuse_next ? &fn : nullptr);
     }
     QWEN_HIP(hipGetLastError());
   }
