@@ -108,6 +108,25 @@ def cpu_model() -> str:
 
 
 # ---------------------------------------------------------------------------------------------
+def copy_bandwidth(torch, nbytes: int = 1 << 30, reps: int = 5) -> dict:
+    """Device-to-device copy of `nbytes` (torch's copy kernel): the measured stream bandwidth of this
+    GPU, and the kernel of known size whose HBM counters (FETCH_SIZE, WRITE_SIZE) scale the traffic."""
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    del src, dst
+    torch.cuda.empty_cache()
+    return {"GBs": 2 * nbytes / (ms * 1e-3) / 1e9, "bytes_read": nbytes, "bytes_written": nbytes, "avg_us": ms * 1e3}
+
+
 def bench_decode(args, torch, batch: int, history: int, seed: int) -> dict:
     from work_llm_accelerator_amd.model import (KERNEL_ATTN_DECODE, KERNEL_GEMM_DOWN, KERNEL_GEMM_GATE_UP,
                                                 MODE_FAST, MODE_ORDERED, DeviceModel, KvCache, fill_kv_synthetic)
@@ -265,6 +284,7 @@ def main():
     for k in ("roofline", "step_roofline", "kernels"):
         if k in r:
             line[k] = r[k]
+    line["copy_bandwidth"] = copy_bandwidth(torch)
     if not args.no_cpu and cpu_past is not None:
         line["cpu_baseline"] = cpu_baseline_decode(cpu_past, args.cpu_seconds)
     print(json.dumps(line), flush=True)

@@ -752,13 +752,17 @@ __global__ void __launch_bounds__(256) gemm_i8_pipe_kernel(GemmArgs a) {
 // wave w holds rows p and p + 64 of head rg, p = 16w + 4g + q).
 // grid = 8 * tt_count * ceil(groups / 8) blocks of 256, groups = row groups x splits.
 // ---------------------------------------------------------------------------------------------
-template <int RTW, bool DUAL, int EPI, int NKC, bool ROPE>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
+template <int RTW, bool DUAL, int EPI, int NKC, bool ROPE, int KSW>
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(3)))
 gemm_skinny_kernel(GemmArgs a, int tt_count, int rg_count, int splits) {
   constexpr int D = DUAL ? 2 : 1;
+  constexpr int KC = NKC / KSW;  // K chunks per wave group
+  static_assert(NKC % KSW == 0, "K chunks split evenly over the wave groups");
+  static_assert(RTW * D * 8 * 1024 <= NKC * 16 * 256 || KSW == 1, "K-group reduction fits the slice buffer");
   __shared__ __align__(16) uint8_t xs[NKC * 16 * 256];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = (threadIdx.x >> 6) & 3;  // row position of the wave
+  const int kg = threadIdx.x >> 8;                                  // K group of the wave
   const int g = lane >> 4;
   const int col = lane & 15;
   const int xcd = blockIdx.x & 7;
@@ -774,8 +778,8 @@ gemm_skinny_kernel(GemmArgs a, int tt_count, int rg_count, int splits) {
   const int row_tiles = a.out_dim / 16;
   const size_t row_stride_x = (size_t)a.in_dim * 2u;
 
-  // activation slice -> LDS: chunk c, rows 4q..4q+3 per load (1 KiB), wave w takes chunks w, w+4, ..
-  for (int c = wave; c < NKC; c += 4) {
+  // activation slice -> LDS: chunk c, rows 4q..4q+3 per load (1 KiB), wave w takes chunks w, w+4KSW, ..
+  for (int c = threadIdx.x >> 6; c < NKC; c += 4 * KSW) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int row = 4 * q + (lane >> 4);
@@ -788,32 +792,43 @@ gemm_skinny_kernel(GemmArgs a, int tt_count, int rg_count, int splits) {
                                        0);
     }
   }
+  // decode position of this lane's token (RoPE epilogue), loaded with the weights
+  const int P = ROPE ? a.pos[min(tok0 + col, a.tokens - 1)] : 0;
   // weight tiles -> registers
-  uint4 wv[RTW][D][NKC];
+  uint4 wv[RTW][D][KC];
   bool ok[RTW];
 #pragma unroll
   for (int r = 0; r < RTW; ++r) {
     const int rt = rg * 4 * RTW + wave + 4 * r;
     ok[r] = rt < row_tiles;
-    const size_t base = ((size_t)(ok[r] ? rt : 0) * nkc_all + kc0) * 64u + lane;
+    const size_t base = ((size_t)(ok[r] ? rt : 0) * nkc_all + kc0 + kg * KC) * 64u + lane;
 #pragma unroll
     for (int d = 0; d < D; ++d) {
       const uint4* wp = reinterpret_cast<const uint4*>(d ? a.wp2 : a.wp) + base;
 #pragma unroll
-      for (int c = 0; c < NKC; ++c) wv[r][d][c] = wp[(size_t)c * 64u];  // cached: reused by the XCD's other token tiles
+      for (int c = 0; c < KC; ++c) wv[r][d][c] = wp[(size_t)c * 64u];  // cached: reused by the XCD's other token tiles
     }
   }
+  __builtin_amdgcn_sched_barrier(0);  // every load above is in flight before any use (one round trip)
   wait_vmcnt<0>();
   __syncthreads();
 
+  // RoPE cos/sin of pairs p = 16*wave + 4g + q, q < 4, at position P: in flight during the MFMAs
+  const bool rope_in = ROPE && P >= 0 && P < a.limit;
+  float4 rc = make_float4(1.0f, 1.0f, 1.0f, 1.0f), rs = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (rope_in && kg == 0) {
+    const float* rr = a.rope + (size_t)P * 128 + 16 * wave + 4 * g;
+    rc = *reinterpret_cast<const float4*>(rr);
+    rs = *reinterpret_cast<const float4*>(rr + 64);
+  }
   v4i accH[RTW][D], accL[RTW][D];
 #pragma unroll
   for (int r = 0; r < RTW; ++r)
 #pragma unroll
     for (int d = 0; d < D; ++d) accH[r][d] = accL[r][d] = v4i{0, 0, 0, 0};
 #pragma unroll
-  for (int c = 0; c < NKC; ++c) {
-    const uint8_t* xr = xs + (c * 16 + col) * 256;
+  for (int c = 0; c < KC; ++c) {
+    const uint8_t* xr = xs + ((kg * KC + c) * 16 + col) * 256;
     const v4i bh1 = *reinterpret_cast<const v4i*>(xr + (((2 * g) ^ col) << 4));
     const v4i bh2 = *reinterpret_cast<const v4i*>(xr + (((2 * g + 1) ^ col) << 4));
     const v4i bl1 = *reinterpret_cast<const v4i*>(xr + (((8 + 2 * g) ^ col) << 4));
@@ -829,6 +844,34 @@ gemm_skinny_kernel(GemmArgs a, int tt_count, int rg_count, int splits) {
         accL[r][d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bl1, accL[r][d], 0, 0, 0);
         accL[r][d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2, bl2, accL[r][d], 0, 0, 0);
       }
+  }
+
+  if constexpr (KSW > 1) {
+    // K group 1 hands its exact int32 sums to K group 0 through LDS (the slice buffer, now read).
+    __syncthreads();
+    int* red = reinterpret_cast<int*>(xs) + (wave * RTW * D * 8) * 64 + lane;
+    if (kg == 1) {
+#pragma unroll
+      for (int r = 0; r < RTW; ++r)
+#pragma unroll
+        for (int d = 0; d < D; ++d)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            red[((r * D + d) * 8 + q) * 64] = accH[r][d][q];
+            red[((r * D + d) * 8 + 4 + q) * 64] = accL[r][d][q];
+          }
+    }
+    __syncthreads();
+    if (kg == 1) return;
+#pragma unroll
+    for (int r = 0; r < RTW; ++r)
+#pragma unroll
+      for (int d = 0; d < D; ++d)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          accH[r][d][q] += red[((r * D + d) * 8 + q) * 64];
+          accL[r][d][q] += red[((r * D + d) * 8 + 4 + q) * 64];
+        }
   }
 
   // epilogue: lane holds rows 16*rt + 4g + q (q < 4) of token tok0 + col
@@ -877,35 +920,31 @@ gemm_skinny_kernel(GemmArgs a, int tt_count, int rg_count, int splits) {
     }
   }
   if constexpr (ROPE) {
-    // rows p (tile r=0) and p + 64 (tile r=1) of head rg: 12 q heads, then 2 k heads, then 2 v heads
-    const int P = a.pos[tok];
-    const bool in = P >= 0 && P < a.limit;
+    // rows p (tile r=0) and p + 64 (tile r=1) of head rg, p = 16*wave + 4g + q: 12 q heads, then 2 k
+    // heads, then 2 v heads; each lane writes 4 consecutive p as one float4 per half.
     const int head = rg;
+    const float c4[4] = {rc.x, rc.y, rc.z, rc.w}, s4[4] = {rs.x, rs.y, rs.z, rs.w};
+    float lo[4], hi[4];
+    const bool rotate = head < QWEN_Q_HEADS + QWEN_KV_HEADS && rope_in;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int p = 16 * wave + 4 * g + q;
-      float c = 1.0f, sn = 0.0f;
-      if (in) {
-        c = a.rope[(size_t)P * 128 + p];
-        sn = a.rope[(size_t)P * 128 + 64 + p];
-      }
       const float e = y[0][q], od = y[1][q];
-      if (head < QWEN_Q_HEADS) {
-        float* yq = a.y + (size_t)tok * a.y_stride + head * QWEN_HEAD_DIM + p;
-        yq[0] = in ? e * c - od * sn : e;
-        yq[64] = in ? od * c + e * sn : od;
-      } else if (in) {
-        const size_t cache_row = (size_t)tok * a.seq_stride + (size_t)P * QWEN_KV_WIDTH;
-        if (head < QWEN_Q_HEADS + QWEN_KV_HEADS) {
-          float* kc = a.k_cache + cache_row + (head - QWEN_Q_HEADS) * QWEN_HEAD_DIM + p;
-          kc[0] = e * c - od * sn;
-          kc[64] = od * c + e * sn;
-        } else {
-          float* vc = a.v_cache + cache_row + (head - QWEN_Q_HEADS - QWEN_KV_HEADS) * QWEN_HEAD_DIM + p;
-          vc[0] = e;
-          vc[64] = od;
-        }
-      }
+      lo[q] = rotate ? e * c4[q] - od * s4[q] : e;
+      hi[q] = rotate ? od * c4[q] + e * s4[q] : od;
+    }
+    const int p0 = 16 * wave + 4 * g;
+    float* dst = nullptr;
+    if (head < QWEN_Q_HEADS) {
+      dst = a.y + (size_t)tok * a.y_stride + head * QWEN_HEAD_DIM + p0;
+    } else if (rope_in) {
+      const size_t cache_row = (size_t)tok * a.seq_stride + (size_t)P * QWEN_KV_WIDTH;
+      dst = head < QWEN_Q_HEADS + QWEN_KV_HEADS
+                ? a.k_cache + cache_row + (head - QWEN_Q_HEADS) * QWEN_HEAD_DIM + p0
+                : a.v_cache + cache_row + (head - QWEN_Q_HEADS - QWEN_KV_HEADS) * QWEN_HEAD_DIM + p0;
+    }
+    if (dst) {
+      *reinterpret_cast<float4*>(dst) = make_float4(lo[0], lo[1], lo[2], lo[3]);
+      *reinterpret_cast<float4*>(dst + 64) = make_float4(hi[0], hi[1], hi[2], hi[3]);
     }
   } else {
 #pragma unroll
@@ -1566,13 +1605,13 @@ static void launch_gemm_pipe_t(const GemmArgs& a, int splits, hipStream_t st) {
 // (5 splits of 14 chunks, finished by the reduce step).  Returns false for other shapes.
 constexpr int kSkinnyTokens = 64;
 
-template <int RTW, bool DUAL, int EPI, int NKC, bool ROPE>
+template <int RTW, bool DUAL, int EPI, int NKC, bool ROPE, int KSW = 1>
 static void launch_skinny_t(const GemmArgs& a, int rg_count, int splits, hipStream_t st) {
   const int tt = (a.tokens + 15) / 16;
   const int groups = rg_count * splits;
   const int blocks = 8 * tt * ((groups + 7) / 8);
-  hipLaunchKernelGGL((gemm_skinny_kernel<RTW, DUAL, EPI, NKC, ROPE>), dim3(blocks), dim3(256), 0, st, a, tt, rg_count,
-                     splits);
+  hipLaunchKernelGGL((gemm_skinny_kernel<RTW, DUAL, EPI, NKC, ROPE, KSW>), dim3(blocks), dim3(256 * KSW), 0, st, a, tt,
+                     rg_count, splits);
 }
 
 template <int EPI, bool DUAL>
@@ -1582,7 +1621,7 @@ static bool launch_skinny(const GemmArgs& a, hipStream_t st) {
   if (a.in_dim == QWEN_HIDDEN) {
     if (!DUAL && EPI == kEpiStore && a.fuse == kFuseQkvRope) {
       if (a.out_dim != QWEN_QKV_ROWS) return false;
-      launch_skinny_t<2, false, kEpiStore, 12, true>(a, row_tiles / 8, 1, st);
+      launch_skinny_t<2, false, kEpiStore, 12, true, 1>(a, row_tiles / 8, 1, st);
       return true;
     }
     if (!DUAL && a.fuse != kFuseNone && !a.part) return false;
