@@ -548,6 +548,8 @@ __device__ __forceinline__ void lgkm_wait_tie(v4i& a, v4i& b, v4i& c, v4i& d) {
 // Orders later uses of r after the preceding waits (no instruction).
 __device__ __forceinline__ void reg_tie(v4i& r) { asm volatile("" : "+v"(r)); }
 
+constexpr int kRasterGroup = 8;  // token tiles per raster group of the pipelined GEMM
+
 template <int NT, int RTW, int NBUF, int EPI, bool DUAL>
 __global__ void __launch_bounds__(256) gemm_i8_pipe_kernel(GemmArgs a) {
   constexpr int D = DUAL ? 2 : 1;
@@ -568,11 +570,26 @@ __global__ void __launch_bounds__(256) gemm_i8_pipe_kernel(GemmArgs a) {
   const int g = lane >> 4;
   const int col = lane & 15;
   const int row_tiles = a.out_dim / 16;
-  const int rt0 = (blockIdx.y * 4 + wave) * RTW;
+  // Block order: block ids are dealt to the 8 XCDs round robin, so XCD x gets the contiguous run
+  // [x*per_xcd, (x+1)*per_xcd) of the grid order below; that order walks groups of kRasterGroup
+  // token tiles with the token tile fastest, so the blocks an XCD runs together share a few
+  // activation tiles and a few weight row groups in its L2.
+  const int tiles_t = (a.tokens + TOK - 1) / TOK;
+  const int tiles_r = (row_tiles + 4 * RTW - 1) / (4 * RTW);
+  const int nblk = tiles_t * tiles_r;
+  const int per_xcd = (nblk + 7) / 8;
+  const int lin = (int)(blockIdx.x & 7) * per_xcd + (int)(blockIdx.x >> 3);
+  if (lin >= nblk) return;  // block-uniform: padding ids of the last XCD run
+  const int G = min(kRasterGroup, tiles_t);
+  const int group = lin / (G * tiles_r);
+  const int first_t = group * G;
+  const int gsize = min(tiles_t - first_t, G);
+  const int within = lin - group * G * tiles_r;
+  const int rt0 = ((within / gsize) * 4 + wave) * RTW;
   const int nkc_all = a.in_dim / kKChunk;
   const int nch = nkc_all / gridDim.z;
   const int kc0 = blockIdx.z * nch;
-  const int tok0 = blockIdx.x * TOK;
+  const int tok0 = (first_t + within % gsize) * TOK;
   const size_t row_stride_x = (size_t)a.in_dim * 2u;
 
   // per-lane global sources (chunk offsets are added per issue)
@@ -1549,6 +1566,226 @@ __global__ void __launch_bounds__(384) attn_prefill_mfma_kernel(const float* __r
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Causal prefill attention on the bf16 matrix cores (v_mfma_f32_16x16x32_bf16) with hi/lo
+// splitting: every fp32 operand x is carried as hi = bf16(x) and lo = bf16(x - hi), and each
+// product is hi*hi + lo*hi + hi*lo (the lo*lo term is below fp32 rounding of the sum), accumulated
+// in fp32.  Semantics of qwen_prefill_attention_kernel.cpp:204-289: keys 0..i for query i, scale
+// 0.08838834764831845f, online softmax (exp evaluated with __expf, inside the FAST tolerance).
+// Block (query tile of 32, KV head kvh, sequence sq): 6 waves, wave h = query head kvh*6 + h with
+// its 32 queries as two 16-query tiles.  Each 32-key K/V tile is converted once into LDS (K as
+// [key][dim], V transposed as [dim][key], hi and lo planes, double buffered; the next tile's fp32
+// rows are loaded into registers while the current one is used).  Per tile and wave:
+//   S^T = K . Q^T: A = K[key][32m + 8g..+7], B = Q[query][same dims] -> S[key 4g+r][query col];
+//   online softmax per query column; P to bf16 hi/lo, keys ordered kt*16 + 4g + r;
+//   O += P . V:    A = P[query col][those keys], B = V^T[dim 16n + col][the same keys].
+// q rows: qkv + (sq*S + i)*qkv_stride + h*128; K/V rows: cache + sq*seq_stride + j*256 + kvh*128;
+// ctx: [sq*S + i][1536].  grid = (ceil(S/32), 2, nseq) with query tiles in reverse order (the
+// longest causal rows start first), block = 384.
+// ---------------------------------------------------------------------------------------------
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+constexpr int kPfQ = 32;                     // queries per block
+constexpr int kPfKeys = 32;                  // keys per staged tile
+constexpr int kPfKRow = QWEN_HEAD_DIM + 8;   // bf16 per staged K row (16-byte pad)
+constexpr int kPfVRow = kPfKeys + 8;         // bf16 per staged V^T row (16-byte pad)
+
+struct __align__(16) PfTile {
+  __bf16 khi[kPfKeys][kPfKRow];
+  __bf16 klo[kPfKeys][kPfKRow];
+  __bf16 vhi[QWEN_HEAD_DIM][kPfVRow];
+  __bf16 vlo[QWEN_HEAD_DIM][kPfVRow];
+};
+
+__device__ __forceinline__ bf16x4 bf16_hi4(float4 x) {
+  return bf16x4{(__bf16)x.x, (__bf16)x.y, (__bf16)x.z, (__bf16)x.w};
+}
+__device__ __forceinline__ bf16x4 bf16_lo4(float4 x, bf16x4 h) {
+  return bf16x4{(__bf16)(x.x - (float)h[0]), (__bf16)(x.y - (float)h[1]), (__bf16)(x.z - (float)h[2]),
+                (__bf16)(x.w - (float)h[3])};
+}
+
+__global__ void __launch_bounds__(384) attn_prefill_bf16x3_kernel(const float* __restrict__ qkv, int qkv_stride,
+                                                                  const float* __restrict__ k_cache,
+                                                                  const float* __restrict__ v_cache,
+                                                                  size_t seq_stride, int S, float* __restrict__ ctx) {
+  __shared__ PfTile tiles[2];
+  const int nqt = gridDim.x;
+  const int qt = nqt - 1 - blockIdx.x;  // longest rows first
+  const int kvh = blockIdx.y;
+  const int sq = blockIdx.z;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int col = lane & 15;
+  const int g = lane >> 4;
+  const int h = kvh * QWEN_GROUPS + wave;
+  const int q0 = qt * kPfQ;
+  const int qlast = min(q0 + kPfQ, S) - 1;
+  const int ntiles = qlast / kPfKeys + 1;  // key tiles 0 .. qlast/32 (causal)
+  const float scaling = 0.08838834764831845f;
+  const float* kb = k_cache + (size_t)sq * seq_stride + kvh * QWEN_HEAD_DIM;
+  const float* vb = v_cache + (size_t)sq * seq_stride + kvh * QWEN_HEAD_DIM;
+
+  // staging: item e < 1024 of K is (key e >> 5, float4 e & 31); item e < 1024 of V is (key group
+  // e >> 7 of 4 keys, dim e & 127).  Thread t takes items t, t + 384, t + 768 (< 1024).
+  float4 kreg[3], vreg[3];
+  auto load_tile = [&](int t) {
+#pragma unroll
+    for (int u = 0; u < 3; ++u) {
+      const int e = threadIdx.x + 384 * u;
+      if (e < 1024) {
+        const int key = min(t * kPfKeys + (e >> 5), S - 1);
+        kreg[u] = *reinterpret_cast<const float4*>(kb + (size_t)key * QWEN_KV_WIDTH + 4 * (e & 31));
+        const int kq = e >> 7, d = e & 127;
+        const float* vp = vb + d;
+        const int k0 = t * kPfKeys + 4 * kq;
+        vreg[u] = make_float4(vp[(size_t)min(k0, S - 1) * QWEN_KV_WIDTH], vp[(size_t)min(k0 + 1, S - 1) * QWEN_KV_WIDTH],
+                              vp[(size_t)min(k0 + 2, S - 1) * QWEN_KV_WIDTH],
+                              vp[(size_t)min(k0 + 3, S - 1) * QWEN_KV_WIDTH]);
+      }
+    }
+  };
+  auto store_tile = [&](PfTile& T) {
+#pragma unroll
+    for (int u = 0; u < 3; ++u) {
+      const int e = threadIdx.x + 384 * u;
+      if (e < 1024) {
+        const bf16x4 kh = bf16_hi4(kreg[u]);
+        *reinterpret_cast<bf16x4*>(&T.khi[e >> 5][4 * (e & 31)]) = kh;
+        *reinterpret_cast<bf16x4*>(&T.klo[e >> 5][4 * (e & 31)]) = bf16_lo4(kreg[u], kh);
+        const bf16x4 vh = bf16_hi4(vreg[u]);
+        *reinterpret_cast<bf16x4*>(&T.vhi[e & 127][4 * (e >> 7)]) = vh;
+        *reinterpret_cast<bf16x4*>(&T.vlo[e & 127][4 * (e >> 7)]) = bf16_lo4(vreg[u], vh);
+      }
+    }
+  };
+
+  // Q operand, scaled: query q0 + 16qs + col, dims 32m + 8g .. +7, as hi and lo planes
+  bf16x8 qh[2][4], ql[2][4];
+#pragma unroll
+  for (int qs = 0; qs < 2; ++qs) {
+    const int qi = min(q0 + 16 * qs + col, S - 1);
+    const float* qp = qkv + ((size_t)sq * S + qi) * qkv_stride + h * QWEN_HEAD_DIM + 8 * g;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const float4 x0 = *reinterpret_cast<const float4*>(qp + 32 * m);
+      const float4 x1 = *reinterpret_cast<const float4*>(qp + 32 * m + 4);
+      const float4 s0 = make_float4(x0.x * scaling, x0.y * scaling, x0.z * scaling, x0.w * scaling);
+      const float4 s1 = make_float4(x1.x * scaling, x1.y * scaling, x1.z * scaling, x1.w * scaling);
+      const bf16x4 h0 = bf16_hi4(s0), h1 = bf16_hi4(s1);
+      const bf16x4 l0 = bf16_lo4(s0, h0), l1 = bf16_lo4(s1, h1);
+      qh[qs][m] = bf16x8{h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
+      ql[qs][m] = bf16x8{l0[0], l0[1], l0[2], l0[3], l1[0], l1[1], l1[2], l1[3]};
+    }
+  }
+
+  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.0f, 0.0f};
+  v4f acc[2][8];
+#pragma unroll
+  for (int qs = 0; qs < 2; ++qs)
+#pragma unroll
+    for (int n = 0; n < 8; ++n) acc[qs][n] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+  load_tile(0);
+  store_tile(tiles[0]);
+  __syncthreads();
+  for (int t = 0; t < ntiles; ++t) {
+    const PfTile& T = tiles[t & 1];
+    if (t + 1 < ntiles) load_tile(t + 1);
+    // S^T for keys t*32 + kt*16 + 4g + r
+    v4f sc[2][2];
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs) sc[qs][0] = sc[qs][1] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const bf16x8 ah = *reinterpret_cast<const bf16x8*>(&T.khi[kt * 16 + col][32 * m + 8 * g]);
+        const bf16x8 al = *reinterpret_cast<const bf16x8*>(&T.klo[kt * 16 + col][32 * m + 8 * g]);
+#pragma unroll
+        for (int qs = 0; qs < 2; ++qs) {
+          sc[qs][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, qh[qs][m], sc[qs][kt], 0, 0, 0);
+          sc[qs][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, qh[qs][m], sc[qs][kt], 0, 0, 0);
+          sc[qs][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, ql[qs][m], sc[qs][kt], 0, 0, 0);
+        }
+      }
+    // online softmax per query column, P to hi/lo
+    bf16x8 ph[2], pl[2];
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs) {
+      const int qi = q0 + 16 * qs + col;
+      float mt = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = t * kPfKeys + kt * 16 + 4 * g + r;
+          if (key > qi || key >= S) sc[qs][kt][r] = -INFINITY;
+          mt = fmaxf(mt, sc[qs][kt][r]);
+        }
+      mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+      mt = fmaxf(mt, __shfl_xor(mt, 32, 64));  // finite: key t*32 <= q0 <= qi
+      const float mn = fmaxf(m_run[qs], mt);
+      const float corr = __expf(m_run[qs] - mn);
+      float p[8];
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) p[kt * 4 + r] = __expf(sc[qs][kt][r] - mn);
+      l_run[qs] = l_run[qs] * corr + (((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7])));
+      m_run[qs] = mn;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        ph[qs][e] = (__bf16)p[e];
+        pl[qs][e] = (__bf16)(p[e] - (float)ph[qs][e]);
+      }
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const float cr = __shfl(corr, 4 * g + rr, 64);  // lane 4g + rr holds query column 4g + rr
+#pragma unroll
+        for (int n = 0; n < 8; ++n) acc[qs][n][rr] *= cr;
+      }
+    }
+    // O += P . V
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+      const __bf16* vhr = &T.vhi[16 * n + col][0];
+      const __bf16* vlr = &T.vlo[16 * n + col][0];
+      const bf16x4 vh0 = *reinterpret_cast<const bf16x4*>(vhr + 4 * g);
+      const bf16x4 vh1 = *reinterpret_cast<const bf16x4*>(vhr + 16 + 4 * g);
+      const bf16x4 vl0 = *reinterpret_cast<const bf16x4*>(vlr + 4 * g);
+      const bf16x4 vl1 = *reinterpret_cast<const bf16x4*>(vlr + 16 + 4 * g);
+      const bf16x8 vh = bf16x8{vh0[0], vh0[1], vh0[2], vh0[3], vh1[0], vh1[1], vh1[2], vh1[3]};
+      const bf16x8 vl = bf16x8{vl0[0], vl0[1], vl0[2], vl0[3], vl1[0], vl1[1], vl1[2], vl1[3]};
+#pragma unroll
+      for (int qs = 0; qs < 2; ++qs) {
+        acc[qs][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph[qs], vh, acc[qs][n], 0, 0, 0);
+        acc[qs][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pl[qs], vh, acc[qs][n], 0, 0, 0);
+        acc[qs][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph[qs], vl, acc[qs][n], 0, 0, 0);
+      }
+    }
+    if (t + 1 < ntiles) store_tile(tiles[(t + 1) & 1]);
+    __syncthreads();  // the next tile is staged; this one is free for tile t + 2
+  }
+#pragma unroll
+  for (int qs = 0; qs < 2; ++qs) {
+    float lp = l_run[qs];
+    lp += __shfl_xor(lp, 16, 64);
+    lp += __shfl_xor(lp, 32, 64);
+    const float inv = lp > 0.0f ? 1.0f / lp : 0.0f;  // of query column col
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int qi = q0 + 16 * qs + 4 * g + rr;
+      const float ir = __shfl(inv, 4 * g + rr, 64);
+      if (qi < S) {
+        float* op = ctx + ((size_t)sq * S + qi) * QWEN_HIDDEN + h * QWEN_HEAD_DIM + col;
+#pragma unroll
+        for (int n = 0; n < 8; ++n) op[16 * n] = acc[qs][n][rr] * ir;
+      }
+    }
+  }
+}
+
 // bf16 rounding of the driver between layers (verification/reference_wrapper_backend.py:40-46).
 __global__ void round_bf16_kernel(float* __restrict__ x, size_t n) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -1596,7 +1833,8 @@ static void launch_reduce(const GemmArgs& a, int splits, hipStream_t st) {
 template <int NT, int RTW, int NBUF, int EPI, bool DUAL>
 static void launch_gemm_pipe_t(const GemmArgs& a, int splits, hipStream_t st) {
   const int row_tiles = a.out_dim / 16;
-  const dim3 grid((a.tokens + 16 * NT - 1) / (16 * NT), (row_tiles + 4 * RTW - 1) / (4 * RTW), splits);
+  const int nblk = ((a.tokens + 16 * NT - 1) / (16 * NT)) * ((row_tiles + 4 * RTW - 1) / (4 * RTW));
+  const dim3 grid(8 * ((nblk + 7) / 8), 1, splits);
   hipLaunchKernelGGL((gemm_i8_pipe_kernel<NT, RTW, NBUF, EPI, DUAL>), grid, dim3(256), 0, st, a);
   if (!DUAL && (splits > 1 || a.fuse != kFuseNone)) launch_reduce<EPI>(a, splits, st);
 }
@@ -1727,8 +1965,8 @@ void launch_attn_decode(const float* qkv, int qkv_stride, const float* k_cache, 
 
 void launch_attn_prefill(const float* qkv, int qkv_stride, const float* k_cache, const float* v_cache,
                          size_t seq_stride, int S, int nseq, float* ctx, hipStream_t st) {
-  hipLaunchKernelGGL(attn_prefill_mfma_kernel, dim3((S + 15) / 16, QWEN_KV_HEADS, nseq), dim3(384), 0, st, qkv,
-                     qkv_stride, k_cache, v_cache, seq_stride, S, ctx);
+  hipLaunchKernelGGL(attn_prefill_bf16x3_kernel, dim3((S + kPfQ - 1) / kPfQ, QWEN_KV_HEADS, nseq), dim3(384), 0, st,
+                     qkv, qkv_stride, k_cache, v_cache, seq_stride, S, ctx);
 }
 
 void launch_round_bf16(float* x, size_t n, hipStream_t st) {
