@@ -108,6 +108,18 @@ def cpu_model() -> str:
 
 
 # ---------------------------------------------------------------------------------------------
+TRAFFIC_PROFILE = ROOT / "profiles" / "attn_decode_b64_kv4096_hbm_traffic.json"
+
+
+def measured_traffic(batch: int, history: int):
+    """HBM bytes per launch of the decode attention kernel at 64 sequences x KV 4096, from the
+    committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes (each scaled by the same counter's reading
+    for a 1 GiB copy); None for other shapes or when the summary is absent."""
+    if (batch, history) != (64, 4096) or not TRAFFIC_PROFILE.exists():
+        return None
+    return json.loads(TRAFFIC_PROFILE.read_text())["traffic_bytes_per_launch"]
+
+
 def copy_bandwidth(torch, nbytes: int = 1 << 30, reps: int = 5) -> dict:
     """Device-to-device copy of `nbytes` (torch's copy kernel): the measured stream bandwidth of this
     GPU, and the kernel of known size whose HBM counters (FETCH_SIZE, WRITE_SIZE) scale the traffic."""
@@ -182,7 +194,8 @@ def bench_decode(args, torch, batch: int, history: int, seed: int) -> dict:
         attn_bytes = kv_read + batch * 1536 * 4
         res["roofline"] = {"bound": "hbm", "kernel": "attn_decode_kernel", "achieved":
                            attn_bytes / (attn_ms * 1e-3) / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                           "frac": attn_bytes / (attn_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "traffic": None,
+                           "frac": attn_bytes / (attn_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                           "traffic": measured_traffic(batch, history),
                            "avg_launch_us": attn_ms * 1e3, "algorithmic_bytes_per_launch": attn_bytes}
         gu_ms = model.time_kernel(KERNEL_GEMM_GATE_UP, 0, 20)
         dn_ms = model.time_kernel(KERNEL_GEMM_DOWN, 0, 20)

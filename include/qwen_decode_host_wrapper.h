@@ -9,9 +9,9 @@
  * Return value: 0 on success, otherwise the reference's error code (1, 10, 11), or 90 when the
  * HIP runtime fails (no counterpart in the reference).
  *
- * Numerics mode: bit-exact with the reference (serial fp32 order) by default; the environment
- * variable QWEN_HIP_MODE=fast selects the reordered, roofline-oriented kernels, whose fp32
- * outputs agree with the reference to a relative tolerance of 1e-3 of each tensor's max.
+ * Numerics: bit-exact with the reference (every fp32/f64 operation in the reference's serial
+ * order).  The reordered, roofline-oriented kernels are reached through the device-resident model
+ * API (qwen_hip_model.h, QWEN_MODE_FAST).
  */
 #ifndef QWEN_DECODE_HOST_WRAPPER_H
 #define QWEN_DECODE_HOST_WRAPPER_H

@@ -11,8 +11,8 @@
  * Return value: 0 on success, the reference's error code (1, 2, 20, 21, 22), or 90 when the HIP
  * runtime fails (no counterpart in the reference).
  *
- * Numerics mode: bit-exact with the reference by default; QWEN_HIP_MODE=fast selects the MFMA
- * kernels, whose fp32 outputs agree with the reference to 1e-3 of each tensor's max.
+ * Numerics: bit-exact with the reference.  The matrix-core kernels are reached through the
+ * device-resident model API (qwen_hip_model.h, QWEN_MODE_FAST).
  */
 #ifndef QWEN_PREFILL_HOST_WRAPPER_H
 #define QWEN_PREFILL_HOST_WRAPPER_H

@@ -6,8 +6,6 @@ every untouched cache row.  Status codes must equal the reference's for every er
 
 from __future__ import annotations
 
-import os
-
 import numpy as np
 import pytest
 
@@ -22,7 +20,6 @@ pytestmark = pytest.mark.gpu
 
 @pytest.fixture(scope="module")
 def lib():
-    os.environ.pop("QWEN_HIP_MODE", None)
     return abi.load(abi.DECODE_STUB_PATH)
 
 

@@ -6,8 +6,6 @@ wrapper's attention scratch); status codes must equal the reference's on every e
 
 from __future__ import annotations
 
-import os
-
 import numpy as np
 import pytest
 
@@ -25,7 +23,6 @@ TILES = valid_prefill_tile_config()
 
 @pytest.fixture(scope="module")
 def lib():
-    os.environ.pop("QWEN_HIP_MODE", None)
     return abi.load(abi.PREFILL_STUB_PATH)
 
 

@@ -92,7 +92,6 @@ int decode_layer_host(const HostLayer& h, const float* x, int past, float* k_cac
     CallScope cs(decode_call_bytes(past));
     Arena& A = cs.A();
     const hipStream_t st = cs.st();
-    const Mode m = mode_from_env();
     const DevLayer d = stage_layer(A, h, st);
     const float* x_d = stage_in(A, x, QWEN_HIDDEN, st);
     const int* pos_d = stage_in(A, &past, 1, st);
@@ -104,7 +103,7 @@ int decode_layer_host(const HostLayer& h, const float* x, int past, float* k_cac
     float* vc_d = stage_in(A, v_cache, kv_n, st);
     float* att_d = A.alloc_n<float>(QWEN_HIDDEN);
     DecodeBatch b{1, pos_d, rope_d, true, kc_d, vc_d, 0, past + 1};
-    run_decode_attention(d, x_d, b, att_d, A, m, st);
+    run_decode_attention(d, x_d, b, att_d, A, st);
     const size_t row = (size_t)past * QWEN_KV_WIDTH;
     copy_out(k_cache + row, kc_d + row, QWEN_KV_WIDTH, st);
     copy_out(v_cache + row, vc_d + row, QWEN_KV_WIDTH, st);
@@ -114,7 +113,7 @@ int decode_layer_host(const HostLayer& h, const float* x, int past, float* k_cac
       return run_mlp ? QWEN_ERR_KERNEL : QWEN_OK;
     }
     float* out_d = A.alloc_n<float>(QWEN_HIDDEN);
-    run_decode_mlp(d, att_d, 1, out_d, A, m, st);
+    run_decode_mlp(d, att_d, 1, out_d, A, st);
     copy_out(out, out_d, QWEN_HIDDEN, st);
     cs.sync();
     return QWEN_OK;
@@ -152,7 +151,7 @@ int qwen_decode_mlp_smoke_forward(const float* a, const float* post_ln, const ui
     const DevLayer d = stage_layer(cs.A(), h, cs.st());
     const float* a_d = stage_in(cs.A(), a, QWEN_HIDDEN, cs.st());
     float* out_d = cs.A().alloc_n<float>(QWEN_HIDDEN);
-    run_decode_mlp(d, a_d, 1, out_d, cs.A(), mode_from_env(), cs.st());
+    run_decode_mlp(d, a_d, 1, out_d, cs.A(), cs.st());
     copy_out(out, out_d, QWEN_HIDDEN, cs.st());
     cs.sync();
     return QWEN_OK;
@@ -269,14 +268,13 @@ int prefill_layer_host(const HostLayer& h, const float* x, int S, float* k_cache
     CallScope cs(prefill_call_bytes(S));
     Arena& A = cs.A();
     const hipStream_t st = cs.st();
-    const Mode m = mode_from_env();
     const float* rope = cs.rt.prefill_rope(S);
     const DevLayer d = stage_layer(A, h, st);
     const float* x_d = stage_in(A, x, (size_t)S * QWEN_HIDDEN, st);
     float* kc_d = A.alloc_n<float>((size_t)S * QWEN_KV_WIDTH);
     float* vc_d = A.alloc_n<float>((size_t)S * QWEN_KV_WIDTH);
     float* att_d = A.alloc_n<float>((size_t)S * QWEN_HIDDEN);
-    run_prefill_attention(d, x_d, S, rope, kc_d, vc_d, att_d, A, m, st);
+    run_prefill_attention(d, x_d, S, rope, kc_d, vc_d, att_d, A, st);
     copy_out(k_cache, kc_d, (size_t)S * QWEN_KV_WIDTH, st);
     copy_out(v_cache, vc_d, (size_t)S * QWEN_KV_WIDTH, st);
     if (att_host) copy_out(att_host, att_d, (size_t)S * QWEN_HIDDEN, st);
@@ -285,7 +283,7 @@ int prefill_layer_host(const HostLayer& h, const float* x, int S, float* k_cache
       return run_mlp ? mlp_status : QWEN_OK;
     }
     float* out_d = A.alloc_n<float>((size_t)S * QWEN_HIDDEN);
-    run_prefill_mlp(d, att_d, S, out_d, A, m, st);
+    run_prefill_mlp(d, att_d, S, out_d, A, st);
     copy_out(out, out_d, (size_t)S * QWEN_HIDDEN, st);
     cs.sync();
     return QWEN_OK;
@@ -372,7 +370,7 @@ int qwen_prefill_mlp_smoke_forward(const float* a, int S, int m_seq, int m_hidde
     const DevLayer d = stage_layer(cs.A(), h, cs.st());
     const float* a_d = stage_in(cs.A(), a, (size_t)S * QWEN_HIDDEN, cs.st());
     float* out_d = cs.A().alloc_n<float>((size_t)S * QWEN_HIDDEN);
-    run_prefill_mlp(d, a_d, S, out_d, cs.A(), mode_from_env(), cs.st());
+    run_prefill_mlp(d, a_d, S, out_d, cs.A(), cs.st());
     copy_out(out, out_d, (size_t)S * QWEN_HIDDEN, cs.st());
     cs.sync();
     return QWEN_OK;

@@ -333,8 +333,8 @@ struct qwen_hip_model {
       arena.reset();
       arena.reserve(decode_workspace_bytes(B));
       DecodeBatch b{B, pos, rope_decode, false, kc0 + (size_t)l * ls, vc0 + (size_t)l * ls, (size_t)ss, max_keys};
-      run_decode_attention(d, hidden, b, att, arena, Mode::Ordered, stream);
-      run_decode_mlp(d, att, B, hidden, arena, Mode::Ordered, stream);
+      run_decode_attention(d, hidden, b, att, arena, stream);
+      run_decode_mlp(d, att, B, hidden, arena, stream);
       if (round) launch_round_bf16(hidden, (size_t)B * QWEN_HIDDEN, stream);
     }
     arena.reset();
@@ -350,8 +350,8 @@ struct qwen_hip_model {
         arena.reset();
         arena.reserve(prefill_workspace_bytes(S));
         run_prefill_attention(d, x, S, rope_prefill, kc0 + (size_t)l * ls + (size_t)b * ss,
-                              vc0 + (size_t)l * ls + (size_t)b * ss, att, arena, Mode::Ordered, stream);
-        run_prefill_mlp(d, att, S, x, arena, Mode::Ordered, stream);
+                              vc0 + (size_t)l * ls + (size_t)b * ss, att, arena, stream);
+        run_prefill_mlp(d, att, S, x, arena, stream);
       }
       if (round) launch_round_bf16(hidden, (size_t)B * S * QWEN_HIDDEN, stream);
     }

@@ -11,12 +11,6 @@
 
 namespace qwen {
 
-Mode mode_from_env() {
-  const char* m = std::getenv("QWEN_HIP_MODE");
-  if (m && (std::strcmp(m, "fast") == 0 || std::strcmp(m, "FAST") == 0)) return Mode::Fast;
-  return Mode::Ordered;
-}
-
 namespace {
 thread_local std::string g_last_error;
 }
@@ -167,9 +161,8 @@ size_t decode_workspace_bytes(int tokens) {
 }
 size_t prefill_workspace_bytes(int tokens) { return decode_workspace_bytes(tokens); }
 
-void run_decode_attention(const DevLayer& L, const float* x, const DecodeBatch& b, float* att, Arena& a, Mode m,
+void run_decode_attention(const DevLayer& L, const float* x, const DecodeBatch& b, float* att, Arena& a,
                           hipStream_t st) {
-  (void)m;
   const int T = b.tokens;
   float* xn = a.alloc_n<float>((size_t)T * QWEN_HIDDEN);
   float* q = a.alloc_n<float>((size_t)T * QWEN_HIDDEN);
@@ -187,8 +180,7 @@ void run_decode_attention(const DevLayer& L, const float* x, const DecodeBatch& 
   QWEN_HIP(hipGetLastError());
 }
 
-void run_decode_mlp(const DevLayer& L, const float* att, int T, float* out, Arena& a, Mode m, hipStream_t st) {
-  (void)m;
+void run_decode_mlp(const DevLayer& L, const float* att, int T, float* out, Arena& a, hipStream_t st) {
   float* pn = a.alloc_n<float>((size_t)T * QWEN_HIDDEN);
   float* g = a.alloc_n<float>((size_t)T * QWEN_INTERMEDIATE);
   float* u = a.alloc_n<float>((size_t)T * QWEN_INTERMEDIATE);
@@ -202,8 +194,7 @@ void run_decode_mlp(const DevLayer& L, const float* att, int T, float* out, Aren
 }
 
 void run_prefill_attention(const DevLayer& L, const float* x, int T, const float* rope, float* k_rows, float* v_rows,
-                           float* att, Arena& a, Mode m, hipStream_t st) {
-  (void)m;
+                           float* att, Arena& a, hipStream_t st) {
   float* xn = a.alloc_n<float>((size_t)T * QWEN_HIDDEN);
   float* q = a.alloc_n<float>((size_t)T * QWEN_HIDDEN);
   float* ctx = a.alloc_n<float>((size_t)T * QWEN_HIDDEN);
@@ -217,8 +208,7 @@ void run_prefill_attention(const DevLayer& L, const float* x, int T, const float
   QWEN_HIP(hipGetLastError());
 }
 
-void run_prefill_mlp(const DevLayer& L, const float* att, int T, float* out, Arena& a, Mode m, hipStream_t st) {
-  (void)m;
+void run_prefill_mlp(const DevLayer& L, const float* att, int T, float* out, Arena& a, hipStream_t st) {
   float* pn = a.alloc_n<float>((size_t)T * QWEN_HIDDEN);
   float* g = a.alloc_n<float>((size_t)T * QWEN_INTERMEDIATE);
   float* u = a.alloc_n<float>((size_t)T * QWEN_INTERMEDIATE);

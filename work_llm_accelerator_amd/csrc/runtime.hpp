@@ -13,10 +13,6 @@
 
 namespace qwen {
 
-enum class Mode { Ordered = 0, Fast = 1 };
-
-// QWEN_HIP_MODE=fast|ordered (default ordered) for the drop-in entry points.
-Mode mode_from_env();
 
 struct HipError {
   hipError_t code;
@@ -125,11 +121,11 @@ struct DecodeBatch {
 size_t decode_workspace_bytes(int tokens);
 size_t prefill_workspace_bytes(int tokens);
 
-void run_decode_attention(const DevLayer& L, const float* x, const DecodeBatch& b, float* att, Arena& a, Mode m,
+void run_decode_attention(const DevLayer& L, const float* x, const DecodeBatch& b, float* att, Arena& a,
                           hipStream_t st);
-void run_decode_mlp(const DevLayer& L, const float* att, int tokens, float* out, Arena& a, Mode m, hipStream_t st);
+void run_decode_mlp(const DevLayer& L, const float* att, int tokens, float* out, Arena& a, hipStream_t st);
 void run_prefill_attention(const DevLayer& L, const float* x, int tokens, const float* rope, float* k_rows,
-                           float* v_rows, float* att, Arena& a, Mode m, hipStream_t st);
-void run_prefill_mlp(const DevLayer& L, const float* att, int tokens, float* out, Arena& a, Mode m, hipStream_t st);
+                           float* v_rows, float* att, Arena& a, hipStream_t st);
+void run_prefill_mlp(const DevLayer& L, const float* att, int tokens, float* out, Arena& a, hipStream_t st);
 
 }  // namespace qwen
