@@ -292,10 +292,11 @@ def test_model_decode_fast_batched(torch, layers2, batch):
         m1.close()
 
 
-@pytest.mark.parametrize("S", [40, 150])
+@pytest.mark.parametrize("S", [40, 150, 300])
 def test_model_prefill_fast_mid(torch, layers2, S):
-    """40 tokens: the 17..64-token GEMM path on prefill shapes; 150 tokens: the many-token GEMM
-    path and ten causal key tiles of the prefill attention (partial last tile)."""
+    """40 tokens: the 17..64-token GEMM path on prefill shapes; 150 tokens: the 65..256-token GEMM
+    path and five causal 32-key tiles of the prefill attention (partial last tile); 300 tokens: the
+    8-wave many-token GEMM (two full 128-token tiles and a partial one) and ten key tiles."""
     from work_llm_accelerator_amd.model import FLAG_NO_BF16_ROUND, MODE_FAST, DeviceModel, KvCache
 
     print(f"model prefill fast S={S}", flush=True)

@@ -550,23 +550,30 @@ __device__ __forceinline__ void reg_tie(v4i& r) { asm volatile("" : "+v"(r)); }
 
 constexpr int kRasterGroup = 8;  // token tiles per raster group of the pipelined GEMM
 
-template <int NT, int RTW, int NBUF, int EPI, bool DUAL>
-__global__ void __launch_bounds__(256) gemm_i8_pipe_kernel(GemmArgs a) {
+template <int NT, int RTW, int NBUF, int EPI, bool DUAL, int TW>
+__global__ void __launch_bounds__(256 * TW) gemm_i8_pipe_kernel(GemmArgs a) {
   constexpr int D = DUAL ? 2 : 1;
-  constexpr int TOK = 16 * NT;
+  constexpr int TOK = 16 * NT * TW;        // tokens per block (TW token groups of 16*NT)
   constexpr int XB = TOK * 256;                 // activation bytes per stage
   constexpr int WB = 4 * RTW * D * 1024;        // weight bytes per stage (4 waves)
-  constexpr int OPS = NT + RTW * D;             // direct loads per chunk per wave
-  static_assert(NBUF == 4, "the stage arrays below are written out for 4 stages");
+  constexpr int OPS = NT + RTW * D / TW;        // direct loads per chunk per wave
+  static_assert(NBUF >= 3, "at least two chunks in flight");
+  static_assert((RTW * D) % TW == 0, "weight tiles split evenly over the token groups");
   static_assert((NBUF - 2) * OPS < 64, "pipeline depth");
   // One LDS object per stage and operand: the compiler tracks direct-load writes per object, so
   // reads of one stage do not wait for loads still landing in the others.
-  __shared__ __align__(16) uint8_t xs0[XB], xs1[XB], xs2[XB], xs3[XB];
-  __shared__ __align__(16) uint8_t ws0[WB], ws1[WB], ws2[WB], ws3[WB];
-  uint8_t* const XS[4] = {xs0, xs1, xs2, xs3};
-  uint8_t* const WS[4] = {ws0, ws1, ws2, ws3};
+  __shared__ __align__(16) uint8_t smem[NBUF * (XB + WB)];  // stage s: [XB activations][WB weights]
+  uint8_t* XS[NBUF];
+  uint8_t* WS[NBUF];
+#pragma unroll
+  for (int st = 0; st < NBUF; ++st) {
+    XS[st] = smem + st * (XB + WB);
+    WS[st] = XS[st] + XB;
+  }
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wv = threadIdx.x >> 6;  // wave of the block
+  const int wave = wv & 3;           // row position of the wave
+  const int tw = wv >> 2;            // token group of the wave
   const int g = lane >> 4;
   const int col = lane & 15;
   const int row_tiles = a.out_dim / 16;
@@ -596,7 +603,7 @@ __global__ void __launch_bounds__(256) gemm_i8_pipe_kernel(GemmArgs a) {
   const uint8_t* xsrc[NT];
 #pragma unroll
   for (int j = 0; j < NT; ++j) {
-    const int r = (wave * NT + j) * 4 + (lane >> 4);  // activation row (token) this lane loads
+    const int r = (wv * NT + j) * 4 + (lane >> 4);    // activation row (token) this lane loads
     const int seg = (lane & 15) ^ (r & 15);
     const int tok = min(tok0 + r, a.tokens - 1);      // rows past the last token reload a valid row
     xsrc[j] = reinterpret_cast<const uint8_t*>(a.xq) + (size_t)tok * row_stride_x + seg * 16;
@@ -617,15 +624,16 @@ __global__ void __launch_bounds__(256) gemm_i8_pipe_kernel(GemmArgs a) {
 #pragma unroll
     for (int j = 0; j < NT; ++j)
       __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(xsrc[j] + (size_t)kc * 256u),
-                                       (__attribute__((address_space(3))) void*)(xst + (wave * NT + j) * 1024), 16, 0,
+                                       (__attribute__((address_space(3))) void*)(xst + (wv * NT + j) * 1024), 16, 0,
                                        0);
 #pragma unroll
     for (int d = 0; d < D; ++d)
 #pragma unroll
       for (int r = 0; r < RTW; ++r)
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(wsrc[d][r] + (size_t)kc * 1024u),
-                                         (__attribute__((address_space(3))) void*)(wst + ((wave * D + d) * RTW + r) * 1024),
-                                         16, 0, 0);
+        if ((d * RTW + r) % TW == tw)  // the token groups share the row position's weight tiles
+          __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(wsrc[d][r] + (size_t)kc * 1024u),
+                                           (__attribute__((address_space(3))) void*)(wst + ((wave * D + d) * RTW + r) * 1024),
+                                           16, 0, 0);
   };
 
   v4i accH[D][RTW][NT], accL[D][RTW][NT];
@@ -654,7 +662,7 @@ __global__ void __launch_bounds__(256) gemm_i8_pipe_kernel(GemmArgs a) {
         // the compiler cannot tell which stage an in-flight direct load writes, and would otherwise
         // drain every outstanding load (s_waitcnt vmcnt(0)) before each read, i.e. the whole pipeline.
         const uint32_t wa = lds_addr(WS[sidx]) + (uint32_t)(wave * D * RTW * 1024 + lane * 16);
-        const uint32_t xb = lds_addr(XS[sidx]) + (uint32_t)(col * 256);
+        const uint32_t xb = lds_addr(XS[sidx]) + (uint32_t)((tw * 16 * NT + col) * 256);
         const uint32_t xo[4] = {xb + (uint32_t)(((2 * g) ^ col) << 4), xb + (uint32_t)(((2 * g + 1) ^ col) << 4),
                                 xb + (uint32_t)(((8 + 2 * g) ^ col) << 4), xb + (uint32_t)(((9 + 2 * g) ^ col) << 4)};
         v4i wr[D][RTW];
@@ -716,7 +724,7 @@ __global__ void __launch_bounds__(256) gemm_i8_pipe_kernel(GemmArgs a) {
     }
 #pragma unroll
     for (int n = 0; n < NT; ++n) {
-      const int tok = tok0 + n * 16 + col;
+      const int tok = tok0 + tw * 16 * NT + n * 16 + col;
       if (tok >= a.tokens) continue;
       const double sx = (double)a.sx[tok];
       float out[4];
@@ -1830,12 +1838,12 @@ static void launch_reduce(const GemmArgs& a, int splits, hipStream_t st) {
   }
 }
 
-template <int NT, int RTW, int NBUF, int EPI, bool DUAL>
+template <int NT, int RTW, int NBUF, int EPI, bool DUAL, int TW = 1>
 static void launch_gemm_pipe_t(const GemmArgs& a, int splits, hipStream_t st) {
   const int row_tiles = a.out_dim / 16;
-  const int nblk = ((a.tokens + 16 * NT - 1) / (16 * NT)) * ((row_tiles + 4 * RTW - 1) / (4 * RTW));
+  const int nblk = ((a.tokens + 16 * NT * TW - 1) / (16 * NT * TW)) * ((row_tiles + 4 * RTW - 1) / (4 * RTW));
   const dim3 grid(8 * ((nblk + 7) / 8), 1, splits);
-  hipLaunchKernelGGL((gemm_i8_pipe_kernel<NT, RTW, NBUF, EPI, DUAL>), grid, dim3(256), 0, st, a);
+  hipLaunchKernelGGL((gemm_i8_pipe_kernel<NT, RTW, NBUF, EPI, DUAL, TW>), grid, dim3(256 * TW), 0, st, a);
   if (!DUAL && (splits > 1 || a.fuse != kFuseNone)) launch_reduce<EPI>(a, splits, st);
 }
 
@@ -1896,6 +1904,14 @@ static void launch_gemm_epi(const GemmArgs& a, hipStream_t st) {
   if (a.tokens <= 16) {
     launch_gemm_t<1, 4, EPI, DUAL>(a, st);
     if (!DUAL && a.fuse != kFuseNone) launch_reduce<EPI>(a, 1, st);
+    return;
+  }
+  // Many tokens (prefill): 8-wave blocks of 128 tokens, two waves per SIMD, three LDS stages.
+  if (a.tokens > kSplitTokens && a.fuse == kFuseNone) {
+    if constexpr (DUAL)
+      launch_gemm_pipe_t<4, 2, 3, EPI, DUAL, 2>(a, 1, st);
+    else
+      launch_gemm_pipe_t<4, 4, 3, EPI, DUAL, 2>(a, 1, st);
     return;
   }
   if constexpr (DUAL) {
