@@ -95,8 +95,11 @@ void launch_attn_decode(const float* qkv, int qkv_stride, const float* k_cache, 
                         size_t seq_stride, const int* pos, int batch, int max_keys, const AttnDecodePlan& plan,
                         float* part, float2* pml, unsigned* arrivals, float* ctx, int8_t* xq, float* sx, int* sums,
                         hipStream_t st);
+// Prefill attention: K/V converted once into bf16 hi/lo tiles (workspace of
+// attn_prefill_workspace_bytes), then the causal attention over them.
+size_t attn_prefill_workspace_bytes(int S, int nseq);
 void launch_attn_prefill(const float* qkv, int qkv_stride, const float* k_cache, const float* v_cache,
-                         size_t seq_stride, int S, int nseq, float* ctx, hipStream_t st);
+                         size_t seq_stride, int S, int nseq, uint8_t* kv_tiles, float* ctx, hipStream_t st);
 void launch_round_bf16(float* x, size_t n, hipStream_t st);
 
 }  // namespace qwen

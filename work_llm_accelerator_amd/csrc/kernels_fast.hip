@@ -1794,6 +1794,240 @@ __global__ void __launch_bounds__(384) attn_prefill_bf16x3_kernel(const float* _
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// K/V of one prefill layer in bf16 hi/lo tiles for attn_prefill_tiles_kernel.  Tile (sequence sq,
+// KV head kvh, keys 32t..32t+31) is 32 KiB at kvt + ((sq*2 + kvh)*ntile + t) * 32 KiB:
+//   [0, 8K)   K hi: row r (key 32t + r) of 256 bytes; 16-byte segment s (dims 8s..8s+7) stored at
+//             position s ^ (r & 15)
+//   [8K, 16K) K lo, same layout
+//   [16K,24K) V^T hi: row d (dim) of 64 bytes; segment s (keys 8s..8s+7) at position s ^ ((d>>2)&3)
+//   [24K,32K) V^T lo, same layout
+// Keys past S repeat key S-1 (masked by the attention).  The swizzles make the attention's LDS
+// reads of 16 rows at one column fall on distinct bank groups.  grid = (ntile, 2, nseq), block = 256.
+// ---------------------------------------------------------------------------------------------
+constexpr int kPfTileBytes = 32768;
+
+__global__ void __launch_bounds__(256) kv_bf16_tiles_kernel(const float* __restrict__ k_cache,
+                                                            const float* __restrict__ v_cache, size_t seq_stride,
+                                                            int S, uint8_t* __restrict__ kvt) {
+  const int t = blockIdx.x, kvh = blockIdx.y, sq = blockIdx.z;
+  const int ntile = gridDim.x;
+  uint8_t* tile = kvt + ((size_t)(sq * 2 + kvh) * ntile + t) * kPfTileBytes;
+  const float* kb = k_cache + (size_t)sq * seq_stride + kvh * QWEN_HEAD_DIM;
+  const float* vb = v_cache + (size_t)sq * seq_stride + kvh * QWEN_HEAD_DIM;
+  {  // K: thread = (row r, segment pair sp)
+    const int r = threadIdx.x >> 3, sp = threadIdx.x & 7;
+    const int key = min(t * kPfKeys + r, S - 1);
+    const float4* src = reinterpret_cast<const float4*>(kb + (size_t)key * QWEN_KV_WIDTH + 16 * sp);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float4 x0 = src[2 * h], x1 = src[2 * h + 1];
+      const bf16x4 h0 = bf16_hi4(x0), h1 = bf16_hi4(x1);
+      const bf16x4 l0 = bf16_lo4(x0, h0), l1 = bf16_lo4(x1, h1);
+      const int pos = ((2 * sp + h) ^ (r & 15)) * 16;
+      *reinterpret_cast<bf16x8*>(tile + r * 256 + pos) = bf16x8{h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
+      *reinterpret_cast<bf16x8*>(tile + 8192 + r * 256 + pos) =
+          bf16x8{l0[0], l0[1], l0[2], l0[3], l1[0], l1[1], l1[2], l1[3]};
+    }
+  }
+  {  // V^T: thread = (dim d, key half h)
+    const int d = threadIdx.x >> 1, h = threadIdx.x & 1;
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) x[i] = vb[(size_t)min(t * kPfKeys + 16 * h + i, S - 1) * QWEN_KV_WIDTH + d];
+#pragma unroll
+    for (int sgi = 0; sgi < 2; ++sgi) {
+      bf16x8 vh, vl;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        vh[e] = (__bf16)x[8 * sgi + e];
+        vl[e] = (__bf16)(x[8 * sgi + e] - (float)vh[e]);
+      }
+      const int pos = ((2 * h + sgi) ^ ((d >> 2) & 3)) * 16;
+      *reinterpret_cast<bf16x8*>(tile + 16384 + d * 64 + pos) = vh;
+      *reinterpret_cast<bf16x8*>(tile + 24576 + d * 64 + pos) = vl;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Causal prefill attention over the bf16 hi/lo tiles of kv_bf16_tiles_kernel, warp-specialized:
+// waves 0-5 compute (wave h = query head kvh*6 + h, 32 queries as two 16-query tiles, the same
+// arithmetic as attn_prefill_bf16x3_kernel), waves 6-7 only stream tiles into a 3-stage LDS ring
+// with direct global->LDS loads (16 KiB each per tile).  The compute waves never have a load in
+// flight, so nothing drains their work; one barrier per tile hands a landed tile to them and frees
+// the stage of the tile they finished.  grid = (ceil(S/32), 2, nseq) with query tiles longest
+// first, block = 512.
+// ---------------------------------------------------------------------------------------------
+constexpr int kPfStages = 3;
+
+__global__ void __launch_bounds__(512) attn_prefill_tiles_kernel(const float* __restrict__ qkv, int qkv_stride,
+                                                                 const uint8_t* __restrict__ kvt, int S,
+                                                                 float* __restrict__ ctx) {
+  __shared__ __align__(16) uint8_t stages[kPfStages][kPfTileBytes];
+  const int nqt = gridDim.x;
+  const int qt = nqt - 1 - blockIdx.x;  // longest rows first
+  const int kvh = blockIdx.y;
+  const int sq = blockIdx.z;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int q0 = qt * kPfQ;
+  const int qlast = min(q0 + kPfQ, S) - 1;
+  const int ntiles = qlast / kPfKeys + 1;  // key tiles 0 .. qlast/32 (causal)
+  const int ntile_all = (S + kPfKeys - 1) / kPfKeys;
+  const uint8_t* tiles = kvt + (size_t)(sq * 2 + kvh) * ntile_all * kPfTileBytes;
+
+  if (wave >= QWEN_GROUPS) {
+    // producer: wave pw streams bytes [16K*pw, 16K*pw + 16K) of each tile, 16 loads of 1 KiB
+    const int pw = wave - QWEN_GROUPS;
+    auto issue = [&](int t) {
+      const int tt = min(t, ntiles - 1);  // past the last tile: reload it into a stage nobody reads
+      const uint8_t* src = tiles + (size_t)tt * kPfTileBytes + pw * 16384 + lane * 16;
+      uint8_t* dst = stages[t % kPfStages] + pw * 16384;
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src + i * 1024),
+                                         (__attribute__((address_space(3))) void*)(dst + i * 1024), 16, 0, 0);
+    };
+    issue(0);
+    issue(1);
+    wait_vmcnt<16>();  // tile 0 landed
+    __syncthreads();
+    for (int t = 0; t < ntiles; ++t) {
+      issue(t + 2);      // into the stage of tile t-1, freed by the barrier that ended iteration t-1
+      wait_vmcnt<16>();  // tile t+1 landed (t+2 may be in flight)
+      __syncthreads();
+    }
+    wait_vmcnt<0>();
+    return;
+  }
+
+  const int col = lane & 15;
+  const int g = lane >> 4;
+  const int h = kvh * QWEN_GROUPS + wave;
+  const float scaling = 0.08838834764831845f;
+  bf16x8 qh[2][4], ql[2][4];
+#pragma unroll
+  for (int qs = 0; qs < 2; ++qs) {
+    const int qi = min(q0 + 16 * qs + col, S - 1);
+    const float* qp = qkv + ((size_t)sq * S + qi) * qkv_stride + h * QWEN_HEAD_DIM + 8 * g;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const float4 x0 = *reinterpret_cast<const float4*>(qp + 32 * m);
+      const float4 x1 = *reinterpret_cast<const float4*>(qp + 32 * m + 4);
+      const float4 s0 = make_float4(x0.x * scaling, x0.y * scaling, x0.z * scaling, x0.w * scaling);
+      const float4 s1 = make_float4(x1.x * scaling, x1.y * scaling, x1.z * scaling, x1.w * scaling);
+      const bf16x4 h0 = bf16_hi4(s0), h1 = bf16_hi4(s1);
+      const bf16x4 l0 = bf16_lo4(s0, h0), l1 = bf16_lo4(s1, h1);
+      qh[qs][m] = bf16x8{h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
+      ql[qs][m] = bf16x8{l0[0], l0[1], l0[2], l0[3], l1[0], l1[1], l1[2], l1[3]};
+    }
+  }
+  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.0f, 0.0f};
+  v4f acc[2][8];
+#pragma unroll
+  for (int qs = 0; qs < 2; ++qs)
+#pragma unroll
+    for (int n = 0; n < 8; ++n) acc[qs][n] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+  __syncthreads();  // tile 0 landed
+  for (int t = 0; t < ntiles; ++t) {
+    const uint8_t* T = stages[t % kPfStages];
+    v4f sc[2][2];
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs) sc[qs][0] = sc[qs][1] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      const int r = kt * 16 + col;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const int pos = r * 256 + (((4 * m + g) ^ (r & 15)) << 4);
+        const bf16x8 ah = *reinterpret_cast<const bf16x8*>(T + pos);
+        const bf16x8 al = *reinterpret_cast<const bf16x8*>(T + 8192 + pos);
+#pragma unroll
+        for (int qs = 0; qs < 2; ++qs) {
+          sc[qs][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, qh[qs][m], sc[qs][kt], 0, 0, 0);
+          sc[qs][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, qh[qs][m], sc[qs][kt], 0, 0, 0);
+          sc[qs][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, ql[qs][m], sc[qs][kt], 0, 0, 0);
+        }
+      }
+    }
+    bf16x8 ph[2], pl[2];
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs) {
+      const int qi = q0 + 16 * qs + col;
+      float mt = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = t * kPfKeys + kt * 16 + 4 * g + r;
+          if (key > qi || key >= S) sc[qs][kt][r] = -INFINITY;
+          mt = fmaxf(mt, sc[qs][kt][r]);
+        }
+      mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+      mt = fmaxf(mt, __shfl_xor(mt, 32, 64));  // finite: key t*32 <= q0 <= qi
+      const float mn = fmaxf(m_run[qs], mt);
+      const float corr = __expf(m_run[qs] - mn);
+      float p[8];
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) p[kt * 4 + r] = __expf(sc[qs][kt][r] - mn);
+      l_run[qs] = l_run[qs] * corr + (((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7])));
+      m_run[qs] = mn;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        ph[qs][e] = (__bf16)p[e];
+        pl[qs][e] = (__bf16)(p[e] - (float)ph[qs][e]);
+      }
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const float cr = __shfl(corr, 4 * g + rr, 64);  // lane 4g + rr holds query column 4g + rr
+#pragma unroll
+        for (int n = 0; n < 8; ++n) acc[qs][n][rr] *= cr;
+      }
+    }
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+      const int d = 16 * n + col;
+      const int sw = (d >> 2) & 3;
+      const int p0 = 16384 + d * 64 + (((g >> 1) ^ sw) << 4) + 8 * (g & 1);        // keys 4g..4g+3
+      const int p1 = 16384 + d * 64 + (((2 + (g >> 1)) ^ sw) << 4) + 8 * (g & 1);  // keys 16+4g..16+4g+3
+      const bf16x4 vh0 = *reinterpret_cast<const bf16x4*>(T + p0);
+      const bf16x4 vh1 = *reinterpret_cast<const bf16x4*>(T + p1);
+      const bf16x4 vl0 = *reinterpret_cast<const bf16x4*>(T + 8192 + p0);
+      const bf16x4 vl1 = *reinterpret_cast<const bf16x4*>(T + 8192 + p1);
+      const bf16x8 vh = bf16x8{vh0[0], vh0[1], vh0[2], vh0[3], vh1[0], vh1[1], vh1[2], vh1[3]};
+      const bf16x8 vl = bf16x8{vl0[0], vl0[1], vl0[2], vl0[3], vl1[0], vl1[1], vl1[2], vl1[3]};
+#pragma unroll
+      for (int qs = 0; qs < 2; ++qs) {
+        acc[qs][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph[qs], vh, acc[qs][n], 0, 0, 0);
+        acc[qs][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pl[qs], vh, acc[qs][n], 0, 0, 0);
+        acc[qs][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph[qs], vl, acc[qs][n], 0, 0, 0);
+      }
+    }
+    __syncthreads();  // done with tile t; tile t+1 has landed
+  }
+#pragma unroll
+  for (int qs = 0; qs < 2; ++qs) {
+    float lp = l_run[qs];
+    lp += __shfl_xor(lp, 16, 64);
+    lp += __shfl_xor(lp, 32, 64);
+    const float inv = lp > 0.0f ? 1.0f / lp : 0.0f;  // of query column col
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int qi = q0 + 16 * qs + 4 * g + rr;
+      const float ir = __shfl(inv, 4 * g + rr, 64);
+      if (qi < S) {
+        float* op = ctx + ((size_t)sq * S + qi) * QWEN_HIDDEN + h * QWEN_HEAD_DIM + col;
+#pragma unroll
+        for (int n = 0; n < 8; ++n) op[16 * n] = acc[qs][n][rr] * ir;
+      }
+    }
+  }
+}
+
 // bf16 rounding of the driver between layers (verification/reference_wrapper_backend.py:40-46).
 __global__ void round_bf16_kernel(float* __restrict__ x, size_t n) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -1979,10 +2213,17 @@ void launch_attn_decode(const float* qkv, int qkv_stride, const float* k_cache, 
                      k_cache, v_cache, seq_stride, pos, plan.chunk, max_keys, part, pml, arrivals, ctx, xq, sx, sums);
 }
 
+size_t attn_prefill_workspace_bytes(int S, int nseq) {
+  return (size_t)nseq * QWEN_KV_HEADS * ((S + kPfKeys - 1) / kPfKeys) * kPfTileBytes;
+}
+
 void launch_attn_prefill(const float* qkv, int qkv_stride, const float* k_cache, const float* v_cache,
-                         size_t seq_stride, int S, int nseq, float* ctx, hipStream_t st) {
-  hipLaunchKernelGGL(attn_prefill_bf16x3_kernel, dim3((S + kPfQ - 1) / kPfQ, QWEN_KV_HEADS, nseq), dim3(384), 0, st,
-                     qkv, qkv_stride, k_cache, v_cache, seq_stride, S, ctx);
+                         size_t seq_stride, int S, int nseq, uint8_t* kv_tiles, float* ctx, hipStream_t st) {
+  const int ntile = (S + kPfKeys - 1) / kPfKeys;
+  hipLaunchKernelGGL(kv_bf16_tiles_kernel, dim3(ntile, QWEN_KV_HEADS, nseq), dim3(256), 0, st, k_cache, v_cache,
+                     seq_stride, S, kv_tiles);
+  hipLaunchKernelGGL(attn_prefill_tiles_kernel, dim3((S + kPfQ - 1) / kPfQ, QWEN_KV_HEADS, nseq), dim3(512), 0, st,
+                     qkv, qkv_stride, kv_tiles, S, ctx);
 }
 
 void launch_round_bf16(float* x, size_t n, hipStream_t st) {

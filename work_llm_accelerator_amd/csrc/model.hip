@@ -88,8 +88,9 @@ struct qwen_hip_model {
     float2* pml;
     unsigned* arrivals;
     float* splitk;  // K-split partials of the non-dual projections (out <= 2048)
+    uint8_t* kvt;   // prefill attention: bf16 hi/lo K/V tiles of one layer
   };
-  Ws carve(size_t tokens, size_t batch, size_t nsplit) {
+  Ws carve(size_t tokens, size_t batch, size_t nsplit, size_t kvt_bytes = 0) {
     size_t off = 0;
     auto take = [&](size_t bytes) {
       const size_t o = off;
@@ -108,6 +109,7 @@ struct qwen_hip_model {
     const size_t o_part = take(batch * QWEN_Q_HEADS * nsplit * QWEN_HEAD_DIM * 4u);
     const size_t o_pml = take(batch * QWEN_Q_HEADS * nsplit * 8u);
     const size_t o_splitk = take(splitk_bytes(kQkvRows));
+    const size_t o_kvt = take(kvt_bytes);
     char* b = static_cast<char*>(ws.get(off));
     unsigned* arr = reinterpret_cast<unsigned*>(b + o_arr);
     if (ws.generation != arrivals_ready) {  // fresh buffer: arm the counters once
@@ -119,7 +121,7 @@ struct qwen_hip_model {
               reinterpret_cast<float*>(b + o_ctx), reinterpret_cast<float*>(b + o_att),
               reinterpret_cast<float*>(b + o_s), reinterpret_cast<float*>(b + o_tmp),
               reinterpret_cast<float*>(b + o_part), reinterpret_cast<float2*>(b + o_pml), arr,
-              reinterpret_cast<float*>(b + o_splitk)};
+              reinterpret_cast<float*>(b + o_splitk), reinterpret_cast<uint8_t*>(b + o_kvt)};
   }
 
   // Plain scratch of `bytes` in the workspace, past the arrival counters.
@@ -301,7 +303,7 @@ struct qwen_hip_model {
 
   void prefill_fast(int B, int S, float* hidden, float* kc0, float* vc0, uint64_t ss, uint64_t ls, int round) {
     const int T = B * S;
-    const Ws w = carve(T, 1, 1);
+    const Ws w = carve(T, 1, 1, attn_prefill_workspace_bytes(S, B));
     for (int l = 0; l < layers; ++l) {
       const FastLayer& f = fast[l];
       float* kc = kc0 + (size_t)l * ls;
@@ -310,7 +312,7 @@ struct qwen_hip_model {
                         stream);
       gemm(w, T, QWEN_HIDDEN, (int)kQkvRows, f.qkv, f.sw_qkv, f.b_qkv, w.qkv, kQkvRows, kEpiStore);
       launch_rope_qkv(w.qkv, (int)kQkvRows, nullptr, S, S, T, rope_prefill, kc, vc, ss, stream);
-      launch_attn_prefill(w.qkv, (int)kQkvRows, kc, vc, ss, S, B, w.ctx, stream);
+      launch_attn_prefill(w.qkv, (int)kQkvRows, kc, vc, ss, S, B, w.kvt, w.ctx, stream);
       launch_norm_quant(w.ctx, QWEN_HIDDEN, T, QWEN_HIDDEN, nullptr, kNormNone, w.xq, w.sx, w.sums, nullptr, stream);
       gemm(w, T, QWEN_HIDDEN, QWEN_HIDDEN, f.o, f.sw_o, nullptr, w.att, QWEN_HIDDEN, kEpiStore);
       launch_norm_quant(w.att, QWEN_HIDDEN, T, QWEN_HIDDEN, f.post_ln, kNormPrefill, w.xq, w.sx, w.sums, nullptr,
@@ -540,7 +542,8 @@ int qwen_hip_model_time_kernel(qwen_hip_model* m, int kernel, int layer, int rep
   return guarded_model([&]() -> int {
     const int T = c.batch * c.seq_len;
     const AttnDecodePlan plan = plan_attn_decode(decode ? c.batch : 1, c.max_keys);
-    const qwen_hip_model::Ws w = m->carve(T, decode ? c.batch : 1, decode ? plan.nsplit : 1);
+    const qwen_hip_model::Ws w = m->carve(T, decode ? c.batch : 1, decode ? plan.nsplit : 1,
+                                          decode ? 0 : attn_prefill_workspace_bytes(c.seq_len, c.batch));
     const FastLayer& f = m->fast[layer];
     float* kc = c.k_cache + (size_t)layer * c.layer_stride;
     float* vc = c.v_cache + (size_t)layer * c.layer_stride;
@@ -565,7 +568,8 @@ int qwen_hip_model_time_kernel(qwen_hip_model* m, int kernel, int layer, int rep
           m->gemm(w, T, QWEN_HIDDEN, QWEN_HIDDEN, f.o, f.sw_o, nullptr, w.tmp, QWEN_HIDDEN, kEpiStore);
           break;
         case QWEN_KERNEL_ATTN_PREFILL:
-          launch_attn_prefill(w.qkv, (int)kQkvRows, kc, vc, c.seq_stride, c.seq_len, c.batch, w.ctx, m->stream);
+          launch_attn_prefill(w.qkv, (int)kQkvRows, kc, vc, c.seq_stride, c.seq_len, c.batch, w.kvt, w.ctx,
+                              m->stream);
           break;
         default:
           throw std::runtime_error("unknown kernel id");
