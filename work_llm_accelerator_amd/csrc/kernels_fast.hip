@@ -49,6 +49,11 @@ __device__ __forceinline__ float load_agent(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Prefill SiLU for the FAST GEMM epilogue: v / (1 + approx_exp(-v)) with approx_exp in its
+// division-free Horner form and a fast reciprocal division (a few ulp from silu_prefill, whose
+// reference form spends seven IEEE divisions per element).
+__device__ __forceinline__ float silu_prefill_fast(float v) { return __fdividef(v, 1.0f + approx_exp_fast(-v)); }
+
 // ---------------------------------------------------------------------------------------------
 // Weight repack.  Reference layout: W[o][i] is the nibble at byte (o*in + i)/2, low nibble for
 // an even flat index, value q in [-8,7] stored as q & 15 (qwen_decode_attention_kernel.cpp:44-60).
@@ -726,12 +731,12 @@ __global__ void __launch_bounds__(256 * TW) gemm_i8_pipe_kernel(GemmArgs a) {
     for (int n = 0; n < NT; ++n) {
       const int tok = tok0 + tw * 16 * NT + n * 16 + col;
       if (tok >= a.tokens) continue;
-      const double sx = (double)a.sx[tok];
+      const float sx = a.sx[tok];
       float out[4];
       if (partial) {
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-          out[q] = (float)(((double)accH[0][r][n][q] * 256.0 + (double)accL[0][r][n][q]) * sx) * sw[q];
+          out[q] = ((float)accH[0][r][n][q] * 256.0f + (float)accL[0][r][n][q]) * sx * sw[q];
         *reinterpret_cast<float4*>(a.part + ((size_t)blockIdx.z * a.tokens + tok) * a.out_dim + row0) =
             make_float4(out[0], out[1], out[2], out[3]);
         continue;
@@ -740,12 +745,14 @@ __global__ void __launch_bounds__(256 * TW) gemm_i8_pipe_kernel(GemmArgs a) {
       const int sl8 = 8 * a.sums[2 * tok + 1];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const double tot = (double)(accH[0][r][n][q] - sh8) * 256.0 + (double)(accL[0][r][n][q] - sl8);
-        const float v = (float)(tot * sx) * sw[q];
+        // fp32 dequantization: the int32 sums are exact; fp32 adds ~2^-24 relative, far inside the
+        // FAST tolerance, at a quarter of the cost of the fp64 form
+        const float tot = (float)(accH[0][r][n][q] - sh8) * 256.0f + (float)(accL[0][r][n][q] - sl8);
+        const float v = tot * sx * sw[q];
         if (EPI == kEpiSiluMul) {
-          const double tot2 = (double)(accH[D - 1][r][n][q] - sh8) * 256.0 + (double)(accL[D - 1][r][n][q] - sl8);
-          const float u = (float)(tot2 * sx) * sw2[q];
-          const float sg = a.prefill_silu ? silu_prefill(v) : silu_decode(v);
+          const float tot2 = (float)(accH[D - 1][r][n][q] - sh8) * 256.0f + (float)(accL[D - 1][r][n][q] - sl8);
+          const float u = tot2 * sx * sw2[q];
+          const float sg = a.prefill_silu ? silu_prefill_fast(v) : silu_decode(v);
           out[q] = sg * u;
         } else if (EPI == kEpiResidual) {
           out[q] = a.resid[(size_t)tok * a.resid_stride + row0 + q] + v;
