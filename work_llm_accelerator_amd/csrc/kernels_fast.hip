@@ -1447,170 +1447,14 @@ __global__ void zero_u32_kernel(unsigned* __restrict__ p, int n) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// Causal prefill attention on the fp32 matrix cores (qwen_prefill_attention_kernel.cpp:204-289
-// semantics: keys 0..i for query i, scale 0.08838834764831845f, approx_exp; online softmax).
-// Block (query tile qt of 16 queries, KV head kvh, sequence sq) = 6 waves, one per query head
-// of the group; each 16-key K/V tile is staged once in LDS (rows padded to 528 bytes, double
-// buffered) and consumed by all 6 waves.  Per wave and key tile (lane: col = l & 15, g = l >> 4):
-//   S = K . Q^T: A = K[key col][dim 4g+16j+e], B = Q[query col][same dim]  -> S[key 4g+r][query col]
-//   P = approx_exp(S - m) per query column (mask keys > query on the diagonal tile)
-//   O += P . V:  A = P[query col][key 4g+r] (own registers), B = V[key 4g+r][dim 4 col+e+64h]
-// O ends in lane l as O[query 4g+r'][dim 4col+e+64h]; rows are divided by l(query) at the end.
-// q rows: qkv + (sq*S + i)*qkv_stride + h*128; K/V rows: cache + sq*seq_stride + j*256 + kvh*128;
-// ctx: [sq*S + i][1536].  grid = (ceil(S/16), 2, nseq), block = 384.
-// ---------------------------------------------------------------------------------------------
-constexpr int kPfRow = QWEN_HEAD_DIM + 4;  // LDS floats per staged K/V row (16-byte pad)
-
-__global__ void __launch_bounds__(384) attn_prefill_mfma_kernel(const float* __restrict__ qkv, int qkv_stride,
-                                                                const float* __restrict__ k_cache,
-                                                                const float* __restrict__ v_cache, size_t seq_stride,
-                                                                int S, float* __restrict__ ctx) {
-  __shared__ __align__(16) float ks[2][16][kPfRow];
-  __shared__ __align__(16) float vs[2][16][kPfRow];
-  const int qt = blockIdx.x;
-  const int kvh = blockIdx.y;
-  const int sq = blockIdx.z;
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;  // query head within the group
-  const int col = lane & 15;
-  const int g = lane >> 4;
-  const int h = kvh * QWEN_GROUPS + wave;
-  const int q0 = qt * 16;
-  const float scaling = 0.08838834764831845f;
-
-  // Q operand: query q0 + col, dims 4g + 16j + e
-  float qr[32];
-  {
-    const int qi = min(q0 + col, S - 1);
-    const float* qp = qkv + ((size_t)sq * S + qi) * qkv_stride + h * QWEN_HEAD_DIM + 4 * g;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float4 q4 = *reinterpret_cast<const float4*>(qp + 16 * j);
-      qr[4 * j + 0] = q4.x * scaling;
-      qr[4 * j + 1] = q4.y * scaling;
-      qr[4 * j + 2] = q4.z * scaling;
-      qr[4 * j + 3] = q4.w * scaling;
-    }
-  }
-  const float* kb = k_cache + (size_t)sq * seq_stride + kvh * QWEN_HEAD_DIM;
-  const float* vb = v_cache + (size_t)sq * seq_stride + kvh * QWEN_HEAD_DIM;
-  const int ntiles = qt + 1;  // key tiles 0..qt (causal)
-
-  // staging: 16 rows x 32 float4 for K and for V = 1024 float4 over 384 threads
-  auto stage = [&](int t, int buf) {
-    for (int e = threadIdx.x; e < 1024; e += 384) {
-      const int which = e >> 9, r = (e >> 5) & 15, c4 = e & 31;
-      const int key = min(t * 16 + r, S - 1);
-      const float* src = (which ? vb : kb) + (size_t)key * QWEN_KV_WIDTH + 4 * c4;
-      const float4 v = *reinterpret_cast<const float4*>(src);
-      float* dst = which ? &vs[buf][r][4 * c4] : &ks[buf][r][4 * c4];
-      *reinterpret_cast<float4*>(dst) = v;
-    }
-  };
-
-  float m = -INFINITY, lp = 0.0f;
-  v4f acc[8];
-#pragma unroll
-  for (int k = 0; k < 8; ++k) acc[k] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-  stage(0, 0);
-  __syncthreads();
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
-    if (t + 1 < ntiles) stage(t + 1, buf ^ 1);
-    v4f sc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-    const float* kr = &ks[buf][col][4 * g];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float4 k4 = *reinterpret_cast<const float4*>(kr + 16 * j);
-      sc = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.x, qr[4 * j + 0], sc, 0, 0, 0);
-      sc = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.y, qr[4 * j + 1], sc, 0, 0, 0);
-      sc = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.z, qr[4 * j + 2], sc, 0, 0, 0);
-      sc = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.w, qr[4 * j + 3], sc, 0, 0, 0);
-    }
-    // causal mask on the diagonal tile: key (t*16 + 4g + r) > query (q0 + col)
-    float mt = -INFINITY;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int key = t * 16 + 4 * g + r;
-      if (key > q0 + col || key >= S) sc[r] = -INFINITY;
-      mt = fmaxf(mt, sc[r]);
-    }
-    mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));  // finite: key t*16 <= q0 + col for every query of the tile
-    const float mn = fmaxf(m, mt);
-    const float corr = approx_exp_fast(m - mn);
-    float p[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) p[r] = sc[r] == -INFINITY ? 0.0f : approx_exp_fast(sc[r] - mn);
-    lp = lp * corr + ((p[0] + p[1]) + (p[2] + p[3]));
-    m = mn;
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const float cr = __shfl(corr, 4 * g + rr, 64);  // lane 4g + rr holds query column 4g + rr
-#pragma unroll
-      for (int k = 0; k < 8; ++k) acc[k][rr] *= cr;
-    }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float* vr = &vs[buf][4 * g + r][4 * col];
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const float4 v4 = *reinterpret_cast<const float4*>(vr + 64 * hh);
-        acc[4 * hh + 0] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[r], v4.x, acc[4 * hh + 0], 0, 0, 0);
-        acc[4 * hh + 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[r], v4.y, acc[4 * hh + 1], 0, 0, 0);
-        acc[4 * hh + 2] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[r], v4.z, acc[4 * hh + 2], 0, 0, 0);
-        acc[4 * hh + 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[r], v4.w, acc[4 * hh + 3], 0, 0, 0);
-      }
-    }
-    __syncthreads();  // buffer `buf` is refilled at t+1; the next tile's stage has landed
-  }
-  lp += __shfl_xor(lp, 16, 64);
-  lp += __shfl_xor(lp, 32, 64);
-  const float inv = lp > 0.0f ? 1.0f / lp : 0.0f;  // per query column col
-#pragma unroll
-  for (int rr = 0; rr < 4; ++rr) {
-    const int qi = q0 + 4 * g + rr;
-    const float ir = __shfl(inv, 4 * g + rr, 64);
-    if (qi < S) {
-      float* op = ctx + ((size_t)sq * S + qi) * QWEN_HIDDEN + h * QWEN_HEAD_DIM + 4 * col;
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh)
-        *reinterpret_cast<float4*>(op + 64 * hh) = make_float4(acc[4 * hh + 0][rr] * ir, acc[4 * hh + 1][rr] * ir,
-                                                                acc[4 * hh + 2][rr] * ir, acc[4 * hh + 3][rr] * ir);
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------------------------
-// Causal prefill attention on the bf16 matrix cores (v_mfma_f32_16x16x32_bf16) with hi/lo
-// splitting: every fp32 operand x is carried as hi = bf16(x) and lo = bf16(x - hi), and each
-// product is hi*hi + lo*hi + hi*lo (the lo*lo term is below fp32 rounding of the sum), accumulated
-// in fp32.  Semantics of qwen_prefill_attention_kernel.cpp:204-289: keys 0..i for query i, scale
-// 0.08838834764831845f, online softmax (exp evaluated with __expf, inside the FAST tolerance).
-// Block (query tile of 32, KV head kvh, sequence sq): 6 waves, wave h = query head kvh*6 + h with
-// its 32 queries as two 16-query tiles.  Each 32-key K/V tile is converted once into LDS (K as
-// [key][dim], V transposed as [dim][key], hi and lo planes, double buffered; the next tile's fp32
-// rows are loaded into registers while the current one is used).  Per tile and wave:
-//   S^T = K . Q^T: A = K[key][32m + 8g..+7], B = Q[query][same dims] -> S[key 4g+r][query col];
-//   online softmax per query column; P to bf16 hi/lo, keys ordered kt*16 + 4g + r;
-//   O += P . V:    A = P[query col][those keys], B = V^T[dim 16n + col][the same keys].
-// q rows: qkv + (sq*S + i)*qkv_stride + h*128; K/V rows: cache + sq*seq_stride + j*256 + kvh*128;
-// ctx: [sq*S + i][1536].  grid = (ceil(S/32), 2, nseq) with query tiles in reverse order (the
-// longest causal rows start first), block = 384.
+// Prefill attention on the bf16 matrix cores (v_mfma_f32_16x16x32_bf16) with hi/lo splitting:
+// every fp32 operand x is carried as hi = bf16(x) and lo = bf16(x - hi), and each product is
+// hi*hi + lo*hi + hi*lo (the lo*lo term is below fp32 rounding of the sum), accumulated in fp32.
 // ---------------------------------------------------------------------------------------------
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-constexpr int kPfQ = 32;                     // queries per block
-constexpr int kPfKeys = 32;                  // keys per staged tile
-constexpr int kPfKRow = QWEN_HEAD_DIM + 8;   // bf16 per staged K row (16-byte pad)
-constexpr int kPfVRow = kPfKeys + 8;         // bf16 per staged V^T row (16-byte pad)
-
-struct __align__(16) PfTile {
-  __bf16 khi[kPfKeys][kPfKRow];
-  __bf16 klo[kPfKeys][kPfKRow];
-  __bf16 vhi[QWEN_HEAD_DIM][kPfVRow];
-  __bf16 vlo[QWEN_HEAD_DIM][kPfVRow];
-};
+constexpr int kPfQ = 32;     // queries per block
+constexpr int kPfKeys = 32;  // keys per tile
 
 __device__ __forceinline__ bf16x4 bf16_hi4(float4 x) {
   return bf16x4{(__bf16)x.x, (__bf16)x.y, (__bf16)x.z, (__bf16)x.w};
@@ -1618,187 +1462,6 @@ __device__ __forceinline__ bf16x4 bf16_hi4(float4 x) {
 __device__ __forceinline__ bf16x4 bf16_lo4(float4 x, bf16x4 h) {
   return bf16x4{(__bf16)(x.x - (float)h[0]), (__bf16)(x.y - (float)h[1]), (__bf16)(x.z - (float)h[2]),
                 (__bf16)(x.w - (float)h[3])};
-}
-
-__global__ void __launch_bounds__(384) attn_prefill_bf16x3_kernel(const float* __restrict__ qkv, int qkv_stride,
-                                                                  const float* __restrict__ k_cache,
-                                                                  const float* __restrict__ v_cache,
-                                                                  size_t seq_stride, int S, float* __restrict__ ctx) {
-  __shared__ PfTile tiles[2];
-  const int nqt = gridDim.x;
-  const int qt = nqt - 1 - blockIdx.x;  // longest rows first
-  const int kvh = blockIdx.y;
-  const int sq = blockIdx.z;
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int col = lane & 15;
-  const int g = lane >> 4;
-  const int h = kvh * QWEN_GROUPS + wave;
-  const int q0 = qt * kPfQ;
-  const int qlast = min(q0 + kPfQ, S) - 1;
-  const int ntiles = qlast / kPfKeys + 1;  // key tiles 0 .. qlast/32 (causal)
-  const float scaling = 0.08838834764831845f;
-  const float* kb = k_cache + (size_t)sq * seq_stride + kvh * QWEN_HEAD_DIM;
-  const float* vb = v_cache + (size_t)sq * seq_stride + kvh * QWEN_HEAD_DIM;
-
-  // staging: item e < 1024 of K is (key e >> 5, float4 e & 31); item e < 1024 of V is (key group
-  // e >> 7 of 4 keys, dim e & 127).  Thread t takes items t, t + 384, t + 768 (< 1024).
-  float4 kreg[3], vreg[3];
-  auto load_tile = [&](int t) {
-#pragma unroll
-    for (int u = 0; u < 3; ++u) {
-      const int e = threadIdx.x + 384 * u;
-      if (e < 1024) {
-        const int key = min(t * kPfKeys + (e >> 5), S - 1);
-        kreg[u] = *reinterpret_cast<const float4*>(kb + (size_t)key * QWEN_KV_WIDTH + 4 * (e & 31));
-        const int kq = e >> 7, d = e & 127;
-        const float* vp = vb + d;
-        const int k0 = t * kPfKeys + 4 * kq;
-        vreg[u] = make_float4(vp[(size_t)min(k0, S - 1) * QWEN_KV_WIDTH], vp[(size_t)min(k0 + 1, S - 1) * QWEN_KV_WIDTH],
-                              vp[(size_t)min(k0 + 2, S - 1) * QWEN_KV_WIDTH],
-                              vp[(size_t)min(k0 + 3, S - 1) * QWEN_KV_WIDTH]);
-      }
-    }
-  };
-  auto store_tile = [&](PfTile& T) {
-#pragma unroll
-    for (int u = 0; u < 3; ++u) {
-      const int e = threadIdx.x + 384 * u;
-      if (e < 1024) {
-        const bf16x4 kh = bf16_hi4(kreg[u]);
-        *reinterpret_cast<bf16x4*>(&T.khi[e >> 5][4 * (e & 31)]) = kh;
-        *reinterpret_cast<bf16x4*>(&T.klo[e >> 5][4 * (e & 31)]) = bf16_lo4(kreg[u], kh);
-        const bf16x4 vh = bf16_hi4(vreg[u]);
-        *reinterpret_cast<bf16x4*>(&T.vhi[e & 127][4 * (e >> 7)]) = vh;
-        *reinterpret_cast<bf16x4*>(&T.vlo[e & 127][4 * (e >> 7)]) = bf16_lo4(vreg[u], vh);
-      }
-    }
-  };
-
-  // Q operand, scaled: query q0 + 16qs + col, dims 32m + 8g .. +7, as hi and lo planes
-  bf16x8 qh[2][4], ql[2][4];
-#pragma unroll
-  for (int qs = 0; qs < 2; ++qs) {
-    const int qi = min(q0 + 16 * qs + col, S - 1);
-    const float* qp = qkv + ((size_t)sq * S + qi) * qkv_stride + h * QWEN_HEAD_DIM + 8 * g;
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const float4 x0 = *reinterpret_cast<const float4*>(qp + 32 * m);
-      const float4 x1 = *reinterpret_cast<const float4*>(qp + 32 * m + 4);
-      const float4 s0 = make_float4(x0.x * scaling, x0.y * scaling, x0.z * scaling, x0.w * scaling);
-      const float4 s1 = make_float4(x1.x * scaling, x1.y * scaling, x1.z * scaling, x1.w * scaling);
-      const bf16x4 h0 = bf16_hi4(s0), h1 = bf16_hi4(s1);
-      const bf16x4 l0 = bf16_lo4(s0, h0), l1 = bf16_lo4(s1, h1);
-      qh[qs][m] = bf16x8{h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
-      ql[qs][m] = bf16x8{l0[0], l0[1], l0[2], l0[3], l1[0], l1[1], l1[2], l1[3]};
-    }
-  }
-
-  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.0f, 0.0f};
-  v4f acc[2][8];
-#pragma unroll
-  for (int qs = 0; qs < 2; ++qs)
-#pragma unroll
-    for (int n = 0; n < 8; ++n) acc[qs][n] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-
-  load_tile(0);
-  store_tile(tiles[0]);
-  __syncthreads();
-  for (int t = 0; t < ntiles; ++t) {
-    const PfTile& T = tiles[t & 1];
-    if (t + 1 < ntiles) load_tile(t + 1);
-    // S^T for keys t*32 + kt*16 + 4g + r
-    v4f sc[2][2];
-#pragma unroll
-    for (int qs = 0; qs < 2; ++qs) sc[qs][0] = sc[qs][1] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        const bf16x8 ah = *reinterpret_cast<const bf16x8*>(&T.khi[kt * 16 + col][32 * m + 8 * g]);
-        const bf16x8 al = *reinterpret_cast<const bf16x8*>(&T.klo[kt * 16 + col][32 * m + 8 * g]);
-#pragma unroll
-        for (int qs = 0; qs < 2; ++qs) {
-          sc[qs][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, qh[qs][m], sc[qs][kt], 0, 0, 0);
-          sc[qs][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, qh[qs][m], sc[qs][kt], 0, 0, 0);
-          sc[qs][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, ql[qs][m], sc[qs][kt], 0, 0, 0);
-        }
-      }
-    // online softmax per query column, P to hi/lo
-    bf16x8 ph[2], pl[2];
-#pragma unroll
-    for (int qs = 0; qs < 2; ++qs) {
-      const int qi = q0 + 16 * qs + col;
-      float mt = -INFINITY;
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int key = t * kPfKeys + kt * 16 + 4 * g + r;
-          if (key > qi || key >= S) sc[qs][kt][r] = -INFINITY;
-          mt = fmaxf(mt, sc[qs][kt][r]);
-        }
-      mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-      mt = fmaxf(mt, __shfl_xor(mt, 32, 64));  // finite: key t*32 <= q0 <= qi
-      const float mn = fmaxf(m_run[qs], mt);
-      const float corr = __expf(m_run[qs] - mn);
-      float p[8];
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) p[kt * 4 + r] = __expf(sc[qs][kt][r] - mn);
-      l_run[qs] = l_run[qs] * corr + (((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7])));
-      m_run[qs] = mn;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        ph[qs][e] = (__bf16)p[e];
-        pl[qs][e] = (__bf16)(p[e] - (float)ph[qs][e]);
-      }
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const float cr = __shfl(corr, 4 * g + rr, 64);  // lane 4g + rr holds query column 4g + rr
-#pragma unroll
-        for (int n = 0; n < 8; ++n) acc[qs][n][rr] *= cr;
-      }
-    }
-    // O += P . V
-#pragma unroll
-    for (int n = 0; n < 8; ++n) {
-      const __bf16* vhr = &T.vhi[16 * n + col][0];
-      const __bf16* vlr = &T.vlo[16 * n + col][0];
-      const bf16x4 vh0 = *reinterpret_cast<const bf16x4*>(vhr + 4 * g);
-      const bf16x4 vh1 = *reinterpret_cast<const bf16x4*>(vhr + 16 + 4 * g);
-      const bf16x4 vl0 = *reinterpret_cast<const bf16x4*>(vlr + 4 * g);
-      const bf16x4 vl1 = *reinterpret_cast<const bf16x4*>(vlr + 16 + 4 * g);
-      const bf16x8 vh = bf16x8{vh0[0], vh0[1], vh0[2], vh0[3], vh1[0], vh1[1], vh1[2], vh1[3]};
-      const bf16x8 vl = bf16x8{vl0[0], vl0[1], vl0[2], vl0[3], vl1[0], vl1[1], vl1[2], vl1[3]};
-#pragma unroll
-      for (int qs = 0; qs < 2; ++qs) {
-        acc[qs][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph[qs], vh, acc[qs][n], 0, 0, 0);
-        acc[qs][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pl[qs], vh, acc[qs][n], 0, 0, 0);
-        acc[qs][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph[qs], vl, acc[qs][n], 0, 0, 0);
-      }
-    }
-    if (t + 1 < ntiles) store_tile(tiles[(t + 1) & 1]);
-    __syncthreads();  // the next tile is staged; this one is free for tile t + 2
-  }
-#pragma unroll
-  for (int qs = 0; qs < 2; ++qs) {
-    float lp = l_run[qs];
-    lp += __shfl_xor(lp, 16, 64);
-    lp += __shfl_xor(lp, 32, 64);
-    const float inv = lp > 0.0f ? 1.0f / lp : 0.0f;  // of query column col
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int qi = q0 + 16 * qs + 4 * g + rr;
-      const float ir = __shfl(inv, 4 * g + rr, 64);
-      if (qi < S) {
-        float* op = ctx + ((size_t)sq * S + qi) * QWEN_HIDDEN + h * QWEN_HEAD_DIM + col;
-#pragma unroll
-        for (int n = 0; n < 8; ++n) op[16 * n] = acc[qs][n][rr] * ir;
-      }
-    }
-  }
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1858,9 +1521,16 @@ __global__ void __launch_bounds__(256) kv_bf16_tiles_kernel(const float* __restr
 }
 
 // ---------------------------------------------------------------------------------------------
-// Causal prefill attention over the bf16 hi/lo tiles of kv_bf16_tiles_kernel, warp-specialized:
-// waves 0-5 compute (wave h = query head kvh*6 + h, 32 queries as two 16-query tiles, the same
-// arithmetic as attn_prefill_bf16x3_kernel), waves 6-7 only stream tiles into a 3-stage LDS ring
+// Causal prefill attention over the bf16 hi/lo tiles of kv_bf16_tiles_kernel.  Semantics of
+// qwen_prefill_attention_kernel.cpp:204-289: keys 0..i for query i, scale 0.08838834764831845f,
+// online softmax (exp evaluated with __expf, inside the FAST tolerance).  Per 32-key tile and
+// compute wave (lane: col = l & 15, g = l >> 4):
+//   S^T = K . Q^T: A = K[key][32m + 8g..+7], B = Q[query][same dims] -> S[key 4g+r][query col];
+//   online softmax per query column; P to bf16 hi/lo, keys ordered kt*16 + 4g + r;
+//   O += P . V:    A = P[query col][those keys], B = V^T[dim 16n + col][the same keys].
+// q rows: qkv + (sq*S + i)*qkv_stride + h*128; ctx: [sq*S + i][1536].
+// Warp-specialized: waves 0-5 compute (wave h = query head kvh*6 + h, 32 queries as two 16-query
+// tiles), waves 6-7 only stream tiles into a 3-stage LDS ring
 // with direct global->LDS loads (16 KiB each per tile).  The compute waves never have a load in
 // flight, so nothing drains their work; one barrier per tile hands a landed tile to them and frees
 // the stage of the tile they finished.  grid = (ceil(S/32), 2, nseq) with query tiles longest
@@ -2190,6 +1860,9 @@ void launch_rope_qkv(float* qkv, int qkv_stride, const int* pos, int seq_len, in
                      k_cache, v_cache, seq_stride);
 }
 
+constexpr int kAttnMinChunk = 64;
+constexpr int kAttnSoftSplits = 24;
+
 AttnDecodePlan plan_attn_decode(int batch, int max_keys) {
   // co-resident blocks of attn_decode_kernel on the current device (CUs x blocks per CU)
   static const int slots = [] {
@@ -2204,6 +1877,10 @@ AttnDecodePlan plan_attn_decode(int batch, int max_keys) {
   int nsplit = (3 * slots / 4) / (QWEN_KV_HEADS * (batch > 0 ? batch : 1));
   nsplit = nsplit < 1 ? 1 : (nsplit > kAttnMaxSplits ? kAttnMaxSplits : nsplit);
   int chunk = (max_keys + nsplit - 1) / nsplit;
+  // Small batches cannot fill the device: each extra split then costs more in the merge (one memory
+  // round trip per 8 splits) than it saves.  Measured on MI355X (batch 1-16, 544 and 4128 keys):
+  // at least 64 keys per split and at most 24 splits.
+  chunk = max(chunk, max(kAttnMinChunk, (max_keys + kAttnSoftSplits - 1) / kAttnSoftSplits));
   chunk = (chunk + 15) & ~15;  // whole 16-key tiles
   return AttnDecodePlan{(max_keys + chunk - 1) / chunk, chunk};
 }
