@@ -88,9 +88,29 @@ int qwen_hip_model_decode(qwen_hip_model* m, int mode, int batch, float* hidden,
 int qwen_hip_model_prefill(qwen_hip_model* m, int mode, int batch, int seq_len, float* hidden, float* k_cache,
                            float* v_cache, uint64_t seq_stride, uint64_t layer_stride);
 
-/* Embedding lookup from the synthetic model's bf16 table: hidden[i] = fp32(table[token_ids[i]]).
- * token_ids and hidden are device pointers. */
+/* Embedding lookup from the model's bf16 table: hidden[i] = fp32(table[token_ids[i]]) (ids outside
+ * [0, vocab) read row 0).  token_ids and hidden are device pointers. */
 int qwen_hip_model_embed(qwen_hip_model* m, const int* token_ids, int count, float* hidden);
+
+/* Model head of the reference's greedy driver (verification/real_host_top_backend.py:138-146 on the
+ * bf16 model of verification/torch_reference_backend.py:67; the argmax of
+ * verification/qwen_full_model_validation.py:128,159).  Synthetic models carry a head: their
+ * embedding table (tied lm_head) and a final norm weight of 1.0 (HF init).
+ *
+ * set_head uploads a tied bf16 embedding / lm_head table [vocab][1536] (vocab a positive multiple
+ * of 64) and the bf16 final RMSNorm weight [1536] (host pointers, raw bf16 bit patterns). */
+int qwen_hip_model_set_head(qwen_hip_model* m, int vocab, const uint16_t* embed_bf16, const uint16_t* norm_bf16);
+int qwen_hip_model_vocab(const qwen_hip_model* m);
+
+/* logits[i][v] for `count` hidden rows [count][1536] fp32: Qwen2RMSNorm on bf16 tensors
+ * (n = bf16(w * bf16(x * 1/sqrt(mean(x^2) + 1e-6))), x = bf16(hidden)), then the bf16 lm_head with
+ * fp32 accumulation, rounded to bf16 and stored as fp32 [count][vocab].  Device pointers. */
+int qwen_hip_model_logits(qwen_hip_model* m, const float* hidden, int count, float* logits);
+
+/* Greedy next tokens: token_ids[i] = the first index of the maximal logit of row i (torch.argmax;
+ * a NaN counts as the maximum), the logits being those of qwen_hip_model_logits (not stored).
+ * Device pointers. */
+int qwen_hip_model_greedy(qwen_hip_model* m, const float* hidden, int count, int* token_ids);
 
 /* Re-runs one kernel of the most recent decode/prefill call `reps` times in isolation, on the
  * model's stream between two HIP events, with that call's shapes and the weights of `layer`;

@@ -709,3 +709,66 @@ uint64_t oracle_count_expf_mismatches(uint32_t first, uint32_t stride, uint64_t 
   }
   return bad;
 }
+
+/* ---- model head ---------------------------------------------------------------------------- */
+
+/* torch's float -> bfloat16 conversion: round to nearest even; NaN becomes a quiet NaN. */
+static uint16_t head_bf16_bits(float x) {
+  uint32_t b;
+  memcpy(&b, &x, 4);
+  if ((b & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;
+  b += 0x7FFFu + ((b >> 16) & 1u);
+  return (uint16_t)(b >> 16);
+}
+static float head_bf16_value(uint16_t h) {
+  const uint32_t b = (uint32_t)h << 16;
+  float f;
+  memcpy(&f, &b, 4);
+  return f;
+}
+
+void oracle_head_norm(const float* x, int count, const uint16_t* w, uint16_t* out) {
+  for (int t = 0; t < count; ++t) {
+    const float* xr = x + (size_t)t * H;
+    float v[H];
+    double ss = 0.0;
+    for (int d = 0; d < H; ++d) {
+      v[d] = head_bf16_value(head_bf16_bits(xr[d]));
+      ss += (double)v[d] * (double)v[d];
+    }
+    const float var = (float)ss / (float)H;
+    const float r = 1.0f / sqrtf(var + QWEN_RMS_EPS);
+    for (int d = 0; d < H; ++d) {
+      const float y = head_bf16_value(head_bf16_bits(v[d] * r));
+      out[(size_t)t * H + d] = head_bf16_bits(head_bf16_value(w[d]) * y);
+    }
+  }
+}
+
+void oracle_lm_head(const uint16_t* xn, int count, const uint16_t* table, int vocab, float* logits) {
+  for (int t = 0; t < count; ++t) {
+    double n[H];
+    for (int k = 0; k < H; ++k) n[k] = head_bf16_value(xn[(size_t)t * H + k]);
+    for (int j = 0; j < vocab; ++j) {
+      const uint16_t* e = table + (size_t)j * H;
+      double acc = 0.0;
+      for (int k = 0; k < H; ++k) acc += n[k] * (double)head_bf16_value(e[k]);
+      logits[(size_t)t * vocab + j] = head_bf16_value(head_bf16_bits((float)acc));
+    }
+  }
+}
+
+void oracle_argmax(const float* logits, int count, int vocab, int* ids) {
+  for (int t = 0; t < count; ++t) {
+    const float* row = logits + (size_t)t * vocab;
+    int best = 0;
+    for (int j = 0; j < vocab; ++j) {
+      if (row[j] != row[j]) {  /* first NaN wins */
+        best = j;
+        break;
+      }
+      if (row[j] > row[best]) best = j;
+    }
+    ids[t] = best;
+  }
+}

@@ -133,6 +133,20 @@ int oracle_decode_layer_block(
     const float* input_token, int past_seq_len, const uint8_t* weight_ddr, const float* scale_ddr,
     float* k_cache, float* v_cache, float* output_token);
 
+/* ---- model head of the greedy driver (verification/real_host_top_backend.py:138-146 on the bf16 model
+ * of verification/torch_reference_backend.py:67; verification/qwen_full_model_validation.py:128,159).
+ * bf16 values travel as uint16 bit patterns.
+ *   oracle_head_norm: Qwen2RMSNorm on bf16 tensors: v = bf16(x), var = fp32(sum v^2) / 1536 (the sum
+ *     correctly rounded to fp32), r = 1 / sqrtf(var + 1e-6), out = bf16(w * bf16(v * r)).
+ *   oracle_lm_head: logits[t][j] = bf16(fp32(sum_k n[t][k] * E[j][k])), the products exact and the
+ *     sum accumulated in double, then rounded to fp32 and to bf16.
+ *   oracle_argmax: first index of the maximum of each row; a NaN is the maximum (torch.argmax).
+ * Pinning: tests/test_oracle_head.py (transformers' Qwen2RMSNorm, torch bf16 linear and
+ * torch.argmax on the CPU). */
+void oracle_head_norm(const float* x, int count, const uint16_t* w, uint16_t* out);
+void oracle_lm_head(const uint16_t* xn, int count, const uint16_t* table, int vocab, float* logits);
+void oracle_argmax(const float* logits, int count, int vocab, int* ids);
+
 /* Mismatch count of y[i] against the host expf of bit pattern first + i*stride (NaN == NaN). */
 uint64_t oracle_count_expf_mismatches(uint32_t first, uint32_t stride, uint64_t n, const float* y,
                                       uint32_t* first_bad);

@@ -56,6 +56,15 @@ def oracle() -> ctypes.CDLL:
     lib.oracle_prefill_layer_uncapped.restype = c_int
     lib.oracle_decode_layer_block.argtypes = [F32P, c_int, U8P, F32P, F32P, F32P, F32P]
     lib.oracle_decode_layer_block.restype = c_int
+    U16P = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
+    I32P = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
+    F32A = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+    lib.oracle_head_norm.argtypes = [F32A, c_int, U16P, U16P]
+    lib.oracle_head_norm.restype = None
+    lib.oracle_lm_head.argtypes = [U16P, c_int, U16P, c_int, F32A]
+    lib.oracle_lm_head.restype = None
+    lib.oracle_argmax.argtypes = [F32A, c_int, c_int, I32P]
+    lib.oracle_argmax.restype = None
     _oracle = lib
     return lib
 
@@ -71,3 +80,24 @@ def ref_decode() -> ctypes.CDLL | None:
             fn.argtypes = argtypes
             fn.restype = c_int
     return lib
+
+
+def head_logits(hidden: np.ndarray, norm_bf16: np.ndarray, table_bf16: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """Oracle final RMSNorm + lm_head: (normalized rows as bf16 bits [N,1536], logits [N,vocab] fp32)."""
+    lib = oracle()
+    x = np.ascontiguousarray(hidden, dtype=np.float32).reshape(-1, 1536)
+    n = x.shape[0]
+    xn = np.zeros((n, 1536), dtype=np.uint16)
+    lib.oracle_head_norm(x, n, np.ascontiguousarray(norm_bf16, dtype=np.uint16), xn)
+    vocab = table_bf16.shape[0]
+    logits = np.zeros((n, vocab), dtype=np.float32)
+    lib.oracle_lm_head(xn, n, np.ascontiguousarray(table_bf16, dtype=np.uint16), vocab, logits)
+    return xn, logits
+
+
+def argmax_rows(logits: np.ndarray) -> np.ndarray:
+    lib = oracle()
+    lg = np.ascontiguousarray(logits, dtype=np.float32)
+    ids = np.zeros(lg.shape[0], dtype=np.int32)
+    lib.oracle_argmax(lg, lg.shape[0], lg.shape[1], ids)
+    return ids

@@ -64,6 +64,10 @@ EXTRA_SIGNATURES: dict[str, tuple[list, object]] = {
     "qwen_hip_model_decode": ([P, c_int, c_int, P, P, c_int, P, P, c_u64, c_u64], c_int),
     "qwen_hip_model_prefill": ([P, c_int, c_int, c_int, P, P, P, c_u64, c_u64], c_int),
     "qwen_hip_model_embed": ([P, P, c_int, P], c_int),
+    "qwen_hip_model_set_head": ([P, c_int, P, P], c_int),
+    "qwen_hip_model_vocab": ([P], c_int),
+    "qwen_hip_model_logits": ([P, P, c_int, P], c_int),
+    "qwen_hip_model_greedy": ([P, P, c_int, P], c_int),
     "qwen_hip_model_time_kernel": ([P, c_int, c_int, c_int, ctypes.POINTER(ctypes.c_float)], c_int),
     "qwen_hip_quantize_int4": ([P, c_int, c_int, P, P, P], c_int),
     "qwen_hip_fill_kv_synthetic": ([P, c_u64, c_u64, P], c_int),

@@ -113,7 +113,15 @@ void launch_quantize_rows(const float* src, int out_dim, int in_dim, uint64_t st
 void launch_fill_vector(float* dst, size_t n, uint64_t stream, float sigma, int bf16, float constant, hipStream_t st);
 void launch_fill_bf16_table(uint16_t* dst, size_t n, uint64_t stream, float sigma, hipStream_t st);
 void launch_kv_synthetic(float* cache, uint64_t rows, uint64_t stream, hipStream_t st);
-void launch_embed(const uint16_t* table, const int* ids, int count, float* hidden, hipStream_t st);
+void launch_embed(const uint16_t* table, int vocab, const int* ids, int count, float* hidden, hipStream_t st);
 void launch_eval_expf(uint32_t first, uint32_t stride, uint64_t n, float* y, hipStream_t st);
+
+// ---- model head: kernels_head.hip ----
+// Final RMSNorm (bf16 weight norm_w[1536]) of `count` hidden rows, tied bf16 lm_head over
+// table[vocab][1536] (vocab a multiple of 64), bf16-rounded logits [count][vocab] (when logits is
+// not null) and greedy token ids [count] (when ids is not null).  workspace: head_workspace_bytes.
+size_t head_workspace_bytes(int count, int vocab);
+void launch_head(const float* hidden, int count, const uint16_t* norm_w, const uint16_t* table, int vocab,
+                 void* workspace, float* logits, int* ids, hipStream_t st);
 
 }  // namespace qwen

@@ -101,11 +101,11 @@ __global__ void __launch_bounds__(256) kv_synthetic_kernel(float* __restrict__ c
   }
 }
 
-__global__ void embed_kernel(const uint16_t* __restrict__ table, const int* __restrict__ ids, int count,
+__global__ void embed_kernel(const uint16_t* __restrict__ table, int vocab, const int* __restrict__ ids, int count,
                              float* __restrict__ hidden) {
   const int t = blockIdx.x;
   const int id = ids[t];
-  const size_t row = (size_t)(id >= 0 && id < QWEN_VOCAB ? id : 0) * QWEN_HIDDEN;  // out-of-range ids read row 0
+  const size_t row = (size_t)(id >= 0 && id < vocab ? id : 0) * QWEN_HIDDEN;  // out-of-range ids read row 0
   for (int d = threadIdx.x; d < QWEN_HIDDEN; d += blockDim.x)
     hidden[(size_t)t * QWEN_HIDDEN + d] = bits_f32((uint32_t)table[row + d] << 16);
 }
@@ -142,8 +142,8 @@ void launch_kv_synthetic(float* cache, uint64_t rows, uint64_t stream, hipStream
   hipLaunchKernelGGL(kv_synthetic_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, cache, rows, stream);
 }
 
-void launch_embed(const uint16_t* table, const int* ids, int count, float* hidden, hipStream_t st) {
-  hipLaunchKernelGGL(embed_kernel, dim3(count), dim3(256), 0, st, table, ids, count, hidden);
+void launch_embed(const uint16_t* table, int vocab, const int* ids, int count, float* hidden, hipStream_t st) {
+  hipLaunchKernelGGL(embed_kernel, dim3(count), dim3(256), 0, st, table, vocab, ids, count, hidden);
 }
 
 }  // namespace qwen

@@ -71,7 +71,10 @@ struct qwen_hip_model {
   std::vector<FastLayer> fast;
   float* rope_decode = nullptr;   // [QWEN_MAX_SEQ][128]
   float* rope_prefill = nullptr;  // [QWEN_MAX_SEQ][128]
-  uint16_t* embed = nullptr;      // synthetic models: [QWEN_VOCAB][1536] bf16
+  uint16_t* embed = nullptr;      // tied embedding / lm_head table [vocab][1536] bf16
+  uint16_t* head_norm = nullptr;  // final RMSNorm weight [1536] bf16
+  int vocab = 0;                  // rows of `embed` (0: no head)
+  DevBuf head_ws;                 // head: normalized rows and per-block argmax candidates
   Arena arena;                    // ORDERED per-layer intermediates
   DevBuf ws;                      // FAST workspace and ORDERED attention output
   unsigned arrivals_ready = 0;    // ws generation whose arrival counters were zeroed
@@ -209,6 +212,7 @@ struct qwen_hip_model {
     if (stream) (void)hipStreamSynchronize(stream);
     for (void* p : {static_cast<void*>(raw_w), static_cast<void*>(raw_s), static_cast<void*>(wp),
                     static_cast<void*>(rope_decode), static_cast<void*>(rope_prefill), static_cast<void*>(embed),
+                    static_cast<void*>(head_norm), head_ws.p,
                     ws.p})
       if (p) (void)hipFree(p);
     if (stream) (void)hipStreamDestroy(stream);
@@ -449,6 +453,11 @@ int qwen_hip_model_create_synthetic(int layers, uint64_t seed, qwen_hip_model** 
       const size_t table = (size_t)QWEN_VOCAB * QWEN_HIDDEN;
       QWEN_HIP(hipMalloc(reinterpret_cast<void**>(&m->embed), table * 2u));
       launch_fill_bf16_table(m->embed, table, synth_stream_host(seed, kEmbedKey), 0.02f, st);
+      m->vocab = QWEN_VOCAB;
+      const std::vector<uint16_t> ones(QWEN_HIDDEN, 0x3F80u);  // final norm weight 1.0 (HF init)
+      QWEN_HIP(hipMalloc(reinterpret_cast<void**>(&m->head_norm), QWEN_HIDDEN * 2u));
+      QWEN_HIP(hipMemcpyAsync(m->head_norm, ones.data(), QWEN_HIDDEN * 2u, hipMemcpyHostToDevice, st));
+      QWEN_HIP(hipStreamSynchronize(st));
       QWEN_HIP(hipGetLastError());
       m->build_fast();
     } catch (...) {
@@ -522,13 +531,58 @@ int qwen_hip_model_prefill(qwen_hip_model* m, int mode, int batch, int seq_len, 
 
 int qwen_hip_model_embed(qwen_hip_model* m, const int* token_ids, int count, float* hidden) {
   if (!m || !token_ids || !hidden || count <= 0) return invalid("invalid embed arguments");
-  if (!m->embed) return invalid("model has no embedding table (only synthetic models carry one)");
+  if (!m->embed) return invalid("model has no embedding table (synthetic models, or qwen_hip_model_set_head)");
   std::lock_guard<std::mutex> lock(m->mu);
   return guarded_model([&]() -> int {
-    launch_embed(m->embed, token_ids, count, hidden, m->stream);
+    launch_embed(m->embed, m->vocab, token_ids, count, hidden, m->stream);
     QWEN_HIP(hipGetLastError());
     return QWEN_OK;
   });
+}
+
+int qwen_hip_model_set_head(qwen_hip_model* m, int vocab, const uint16_t* embed_bf16, const uint16_t* norm_bf16) {
+  if (!m || !embed_bf16 || !norm_bf16 || vocab <= 0 || vocab % 64 != 0 || vocab > (1 << 24))
+    return invalid("invalid head arguments (vocab must be a positive multiple of 64)");
+  std::lock_guard<std::mutex> lock(m->mu);
+  return guarded_model([&]() -> int {
+    QWEN_HIP(hipStreamSynchronize(m->stream));
+    if (m->embed) QWEN_HIP(hipFree(m->embed));
+    m->embed = nullptr;
+    m->vocab = 0;
+    const size_t table = (size_t)vocab * QWEN_HIDDEN * 2u;
+    QWEN_HIP(hipMalloc(reinterpret_cast<void**>(&m->embed), table));
+    QWEN_HIP(hipMemcpy(m->embed, embed_bf16, table, hipMemcpyHostToDevice));
+    if (!m->head_norm) QWEN_HIP(hipMalloc(reinterpret_cast<void**>(&m->head_norm), QWEN_HIDDEN * 2u));
+    QWEN_HIP(hipMemcpy(m->head_norm, norm_bf16, QWEN_HIDDEN * 2u, hipMemcpyHostToDevice));
+    m->vocab = vocab;
+    return QWEN_OK;
+  });
+}
+
+int qwen_hip_model_vocab(const qwen_hip_model* m) { return m ? m->vocab : 0; }
+
+namespace {
+int run_head(qwen_hip_model* m, const float* hidden, int count, float* logits, int* token_ids) {
+  if (!m || !hidden || count <= 0 || count > (1 << 20)) return invalid("invalid head arguments");
+  if (!m->embed || !m->head_norm) return invalid("model has no head (synthetic models, or qwen_hip_model_set_head)");
+  std::lock_guard<std::mutex> lock(m->mu);
+  return guarded_model([&]() -> int {
+    void* ws = m->head_ws.get(head_workspace_bytes(count, m->vocab));
+    launch_head(hidden, count, m->head_norm, m->embed, m->vocab, ws, logits, token_ids, m->stream);
+    QWEN_HIP(hipGetLastError());
+    return QWEN_OK;
+  });
+}
+}  // namespace
+
+int qwen_hip_model_logits(qwen_hip_model* m, const float* hidden, int count, float* logits) {
+  if (!logits) return invalid("invalid logits buffer");
+  return run_head(m, hidden, count, logits, nullptr);
+}
+
+int qwen_hip_model_greedy(qwen_hip_model* m, const float* hidden, int count, int* token_ids) {
+  if (!token_ids) return invalid("invalid token id buffer");
+  return run_head(m, hidden, count, nullptr, token_ids);
 }
 
 int qwen_hip_model_time_kernel(qwen_hip_model* m, int kernel, int layer, int reps, float* avg_ms) {

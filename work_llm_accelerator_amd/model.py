@@ -136,6 +136,39 @@ class DeviceModel:
         st = self.lib.qwen_hip_model_embed(self.handle, _ptr(token_ids), int(token_ids.numel()), _ptr(hidden))
         _check(self.lib, st, "qwen_hip_model_embed")
 
+    @property
+    def vocab(self) -> int:
+        """Rows of the tied embedding / lm_head table (0 when the model has no head)."""
+        return int(self.lib.qwen_hip_model_vocab(self.handle))
+
+    def set_head(self, embed_bf16: np.ndarray, norm_bf16: np.ndarray) -> None:
+        """Uploads a tied bf16 embedding / lm_head table [vocab, 1536] and the bf16 final RMSNorm
+        weight [1536], both as uint16 bit patterns (vocab a multiple of 64)."""
+        embed = np.ascontiguousarray(embed_bf16, dtype=np.uint16)
+        norm = np.ascontiguousarray(norm_bf16, dtype=np.uint16)
+        if embed.ndim != 2 or embed.shape[1] != 1536 or norm.shape != (1536,):
+            raise ValueError("embed must be [vocab, 1536] and norm [1536] (bf16 bit patterns)")
+        st = self.lib.qwen_hip_model_set_head(self.handle, embed.shape[0], embed.ctypes.data_as(ctypes.c_void_p),
+                                              norm.ctypes.data_as(ctypes.c_void_p))
+        _check(self.lib, st, "qwen_hip_model_set_head")
+
+    def logits(self, hidden, logits, order: bool = True) -> None:
+        """Final RMSNorm + tied bf16 lm_head of hidden [N,1536] fp32 into logits [N,vocab] fp32
+        (bf16-rounded values, verification/real_host_top_backend.py:138-146)."""
+        if order:
+            self._enter()
+        n = hidden.numel() // 1536
+        st = self.lib.qwen_hip_model_logits(self.handle, _ptr(hidden), n, _ptr(logits))
+        _check(self.lib, st, "qwen_hip_model_logits")
+
+    def greedy(self, hidden, token_ids, order: bool = True) -> None:
+        """Greedy next token ids [N] int32 of hidden [N,1536] (torch.argmax of the logits)."""
+        if order:
+            self._enter()
+        n = hidden.numel() // 1536
+        st = self.lib.qwen_hip_model_greedy(self.handle, _ptr(hidden), n, _ptr(token_ids))
+        _check(self.lib, st, "qwen_hip_model_greedy")
+
     def time_kernel(self, kernel: int, layer: int = 0, reps: int = 20) -> float:
         """Mean milliseconds of one launch of `kernel`, re-run in isolation with the shapes of the
         last FAST call (HIP events on the model's stream)."""
