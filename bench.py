@@ -11,6 +11,10 @@ Printed: one JSON line with whole-job tok/s, the dominant kernel's roofline (dec
 streaming the fp32 KV cache, timed in isolation with HIP events on the model's stream) and the
 reference C++ host path timed on this machine's CPU on a bounded sample.
 
+--workload decode1 is batch-1 greedy generation (512-token prompt prefilled, then greedy steps
+through the final norm, the tied bf16 lm_head and argmax); --workload prefill is 8 x 2048 causal
+prefill.
+
     python bench.py [--steps K] [--warmup W] [--workload decode64|decode1|prefill] [--mode fast|ordered]
 """
 
@@ -211,6 +215,78 @@ def bench_decode(args, torch, batch: int, history: int, seed: int) -> dict:
     return res
 
 
+def bench_greedy(args, torch, prompt: int, seed: int) -> dict:
+    """Batch-1 greedy generation: a `prompt`-token prompt of uniform random ids is prefilled, its last
+    position's greedy token starts the loop, then each timed step is embedding -> 28 layers -> final
+    RMSNorm -> tied bf16 lm_head -> argmax -> the next step's token, all on the device."""
+    from work_llm_accelerator_amd.model import MODE_FAST, MODE_ORDERED, DeviceModel, KvCache
+
+    mode = MODE_FAST if args.mode == "fast" else MODE_ORDERED
+    nsteps = args.warmup + args.steps
+    positions = prompt + nsteps
+    model = DeviceModel(LAYERS, synthetic_seed=seed)
+    vocab = model.vocab
+    cache = KvCache.allocate(LAYERS, 1, positions)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    prompt_ids = torch.randint(0, vocab, (prompt,), dtype=torch.int32, device="cuda", generator=gen)
+    hp = torch.empty(1, prompt, 1536, dtype=torch.float32, device="cuda")
+    ids = torch.empty(1, dtype=torch.int32, device="cuda")
+    hidden = torch.empty(1, 1536, dtype=torch.float32, device="cuda")
+    pos = [torch.full((1,), prompt + i, dtype=torch.int32, device="cuda") for i in range(nsteps)]
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(model.stream)
+    model.embed(prompt_ids, hp, order=False)
+    model.prefill(mode, hp, cache, order=False)
+    model.greedy(hp[0, prompt - 1:], ids, order=False)
+    e1.record(model.stream)
+    model.synchronize()
+    prefill_ms = e0.elapsed_time(e1)
+
+    def step(i):
+        model.embed(ids, hidden, order=False)
+        model.decode(mode, hidden, pos[i], positions, cache, order=False)
+        model.greedy(hidden, ids, order=False)
+
+    for i in range(args.warmup):
+        step(i)
+    model.synchronize()
+    t0 = time.perf_counter()
+    e0.record(model.stream)
+    for i in range(args.warmup, nsteps):
+        step(i)
+    e1.record(model.stream)
+    model.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = e0.elapsed_time(e1) / args.steps
+    keys = prompt + nsteps  # KV rows read by the last step
+    table_bytes = vocab * 1536 * 2
+    res = {"value": 1.0 / (ms_step * 1e-3), "ms_per_step": ms_step, "wall_s": wall,
+           "prefill": {"prompt_tokens": prompt, "ms": prefill_ms, "tok_s": prompt / (prefill_ms * 1e-3)}}
+    step_bytes = LAYERS * (23_508_992 + keys * 2 * KV_ROW_BYTES + 2 * KV_ROW_BYTES + 2 * 1536 * 4) + table_bytes
+    res["step_roofline"] = {"bound": "hbm", "algorithmic_bytes": step_bytes, "note": "includes the bf16 lm_head",
+                            "achieved_GBs": step_bytes / (ms_step * 1e-3) / 1e9,
+                            "frac": step_bytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    # dominant kernel: the lm_head streaming the bf16 table (its norm and argmax kernels included)
+    reps = 20
+    e0.record(model.stream)
+    for _ in range(reps):
+        model.greedy(hidden, ids, order=False)
+    e1.record(model.stream)
+    model.synchronize()
+    head_ms = e0.elapsed_time(e1) / reps
+    head_bytes = table_bytes + 1536 * 4 + 1536 * 2
+    res["roofline"] = {"bound": "hbm", "kernel": "lm_head_kernel (with head_norm_kernel and argmax_finalize_kernel)",
+                       "achieved": head_bytes / (head_ms * 1e-3) / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                       "frac": head_bytes / (head_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "traffic": None,
+                       "avg_launch_us": head_ms * 1e3, "algorithmic_bytes_per_launch": head_bytes}
+    model.close()
+    del cache
+    torch.cuda.empty_cache()
+    return res
+
+
 def bench_prefill(args, torch, batch: int, seq: int, seed: int) -> dict:
     from work_llm_accelerator_amd.model import (KERNEL_ATTN_PREFILL, KERNEL_GEMM_GATE_UP, MODE_FAST, MODE_ORDERED,
                                                 DeviceModel, KvCache)
@@ -278,11 +354,14 @@ def main():
                   "layers": LAYERS, "batch": batch, "kv_length": f"{history + 1}..{history + 32}", "mode": args.mode}
         unit, cpu_past = "tok/s", history
     elif args.workload == "decode1":
-        batch, history, seed = 1, 512, 2
-        r = bench_decode(args, torch, batch, history, seed)
-        config = {"workload": "28-layer Qwen2.5-1.5B-shaped decode, batch 1, KV 513..544 after a 512-token "
-                              "history, seed 2", "layers": LAYERS, "batch": 1, "mode": args.mode}
-        unit, cpu_past = "tok/s", history
+        prompt, seed = 512, 2
+        r = bench_greedy(args, torch, prompt, seed)
+        config = {"workload": "28-layer Qwen2.5-1.5B-shaped greedy generation, batch 1: a 512-token prompt of "
+                              "uniform random ids prefilled, then greedy decode steps (embedding, 28 layers, final "
+                              "RMSNorm, tied bf16 lm_head over 151936 tokens, argmax), seed 2",
+                  "layers": LAYERS, "batch": 1, "prompt": prompt,
+                  "kv_length": f"{prompt + args.warmup + 1}..{prompt + args.warmup + args.steps}", "mode": args.mode}
+        unit, cpu_past = "tok/s", prompt
     else:
         batch, seq, seed = 8, 2048, 3
         r = bench_prefill(args, torch, batch, seq, seed)
@@ -294,7 +373,7 @@ def main():
             "warmup": args.warmup, "ms_per_step": r["ms_per_step"], "higher_is_better": True, "scaling": "weak",
             "vs_baseline": None, "dtype": "int4 weights x int8 two-limb MFMA, f32" if args.mode == "fast" else "f32",
             "data": "synthetic (random-init weights, random tokens, N(0,1) quantized KV)", "config": config}
-    for k in ("roofline", "step_roofline", "kernels"):
+    for k in ("roofline", "step_roofline", "kernels", "prefill"):
         if k in r:
             line[k] = r[k]
     line["copy_bandwidth"] = copy_bandwidth(torch)

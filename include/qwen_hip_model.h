@@ -98,7 +98,7 @@ int qwen_hip_model_embed(qwen_hip_model* m, const int* token_ids, int count, flo
  * embedding table (tied lm_head) and a final norm weight of 1.0 (HF init).
  *
  * set_head uploads a tied bf16 embedding / lm_head table [vocab][1536] (vocab a positive multiple
- * of 64) and the bf16 final RMSNorm weight [1536] (host pointers, raw bf16 bit patterns). */
+ * of 128) and the bf16 final RMSNorm weight [1536] (host pointers, raw bf16 bit patterns). */
 int qwen_hip_model_set_head(qwen_hip_model* m, int vocab, const uint16_t* embed_bf16, const uint16_t* norm_bf16);
 int qwen_hip_model_vocab(const qwen_hip_model* m);
 

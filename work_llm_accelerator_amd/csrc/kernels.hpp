@@ -118,7 +118,7 @@ void launch_eval_expf(uint32_t first, uint32_t stride, uint64_t n, float* y, hip
 
 // ---- model head: kernels_head.hip ----
 // Final RMSNorm (bf16 weight norm_w[1536]) of `count` hidden rows, tied bf16 lm_head over
-// table[vocab][1536] (vocab a multiple of 64), bf16-rounded logits [count][vocab] (when logits is
+// table[vocab][1536] (vocab a multiple of 128), bf16-rounded logits [count][vocab] (when logits is
 // not null) and greedy token ids [count] (when ids is not null).  workspace: head_workspace_bytes.
 size_t head_workspace_bytes(int count, int vocab);
 void launch_head(const float* hidden, int count, const uint16_t* norm_w, const uint16_t* table, int vocab,

@@ -25,7 +25,7 @@ typedef __bf16 hbf16x8 __attribute__((ext_vector_type(8)));
 typedef float hf32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kHeadRow = QWEN_HIDDEN + 8;  // bf16 per staged activation row (16-byte pad)
-constexpr int kHeadBlockRows = 64;         // vocab rows per lm_head block (4 waves x 16)
+constexpr int kHeadBlockRows = 64;         // vocab rows of one tile set of an lm_head block (4 waves x 16)
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t h) { return bits_f32((uint32_t)h << 16); }
 // torch's float -> bfloat16 conversion: round to nearest even, NaN kept as a quiet NaN.
@@ -76,78 +76,101 @@ __global__ void __launch_bounds__(256) head_norm_kernel(const float* __restrict_
   }
 }
 
-// K steps [8*kb, 8*kb + 8) of one wave: MFMAs on `cur` while `nxt` receives the next 8 steps.
-__device__ __forceinline__ void head_ksteps(const uint4 (&cur)[8], uint4 (&nxt)[8], bool prefetch, const uint4* ap,
-                                            int kb, const uint16_t* xrow, hf32x4& acc) {
+// K steps [4*kb, 4*kb + 4) of one wave for its two row tiles: MFMAs on cur0/cur1 while nxt0/nxt1
+// receive the next 4 steps.  B (the token tile's normalized rows) is read from LDS; lanes whose token
+// is past the tile's live rows use zeros.
+__device__ __forceinline__ void head_ksteps(const uint4 (&cur0)[4], const uint4 (&cur1)[4], uint4 (&nxt0)[4],
+                                            uint4 (&nxt1)[4], bool prefetch, const uint4* ap0, const uint4* ap1,
+                                            int kb, const uint16_t* xrow, bool live, hf32x4& acc0, hf32x4& acc1) {
   if (prefetch) {
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const uint4* p = ap + 4 * (8 * (kb + 1) + s);
-      const hf32x4 raw = __builtin_nontemporal_load(reinterpret_cast<const hf32x4*>(p));  // read once per call
-      nxt[s] = make_uint4(__float_as_uint(raw[0]), __float_as_uint(raw[1]), __float_as_uint(raw[2]),
-                          __float_as_uint(raw[3]));
+    for (int s = 0; s < 4; ++s) {
+      const int off = 4 * (4 * (kb + 1) + s);
+      const hf32x4 r0 = __builtin_nontemporal_load(reinterpret_cast<const hf32x4*>(ap0 + off));  // read once
+      const hf32x4 r1 = __builtin_nontemporal_load(reinterpret_cast<const hf32x4*>(ap1 + off));
+      nxt0[s] = make_uint4(__float_as_uint(r0[0]), __float_as_uint(r0[1]), __float_as_uint(r0[2]), __float_as_uint(r0[3]));
+      nxt1[s] = make_uint4(__float_as_uint(r1[0]), __float_as_uint(r1[1]), __float_as_uint(r1[2]), __float_as_uint(r1[3]));
     }
   }
 #pragma unroll
-  for (int s = 0; s < 8; ++s) {
-    const hbf16x8 b = *reinterpret_cast<const hbf16x8*>(xrow + 32 * (8 * kb + s));
-    hbf16x8 a;
-    __builtin_memcpy(&a, &cur[s], 16);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+  for (int s = 0; s < 4; ++s) {
+    hbf16x8 b = {};
+    if (live) b = *reinterpret_cast<const hbf16x8*>(xrow + 32 * (4 * kb + s));
+    hbf16x8 a0, a1;
+    __builtin_memcpy(&a0, &cur0[s], 16);
+    __builtin_memcpy(&a1, &cur1[s], 16);
+    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b, acc0, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b, acc1, 0, 0, 0);
   }
 }
 
-// grid = (vocab / 64, ceil(count / 16)), block = 256.  Wave w of block (vb, tt) computes the 16 x 16
-// logits of vocab rows vb*64 + 16w .. +15 and tokens tt*16 .. +15 over K = 1536 (48 MFMA steps of 32):
-//   A = E[row l&15][k = 32s + 8(l>>4) .. +7] straight from HBM (8 steps prefetched),
-//   B = n[token l&15][same k] from the LDS copy of the token tile  ->  D[row 4(l>>4)+i][token l&15].
-// Each logit is rounded to bf16 (written to `logits` when LOGITS), and the block's best
-// (order_key(logit) << 32 | ~row) per token goes to best[token][vb].
+// The block's best key per token column from the 4 logits a lane holds for rows rbase + 4g + i.
+__device__ __forceinline__ unsigned long long head_best(const hf32x4& acc, int rbase, int g, float (&lf)[4]) {
+  unsigned long long bk = 0ull;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    lf[i] = to_bf16(acc[i]);
+    const uint32_t v = (uint32_t)(rbase + 4 * g + i);
+    const unsigned long long key = ((unsigned long long)order_key(lf[i]) << 32) | (unsigned long long)(~v);
+    bk = key > bk ? key : bk;
+  }
+  return bk;
+}
+
+// grid = (vocab / 128, ceil(count / 16)), block = 256, dynamic LDS = live rows x kHeadRow bf16.
+// Wave w of block (vb, tt) computes the logits of the two 16-row tiles vb*128 + 16w and vb*128 + 64 +
+// 16w for tokens tt*16 .. +15 over K = 1536 (48 MFMA steps of 32, 4 steps prefetched):
+//   A = E[row l&15][k = 32s + 8(l>>4) .. +7] straight from HBM,
+//   B = n[token l&15][same k] from the LDS copy of the tile's live token rows  ->  D[row 4(l>>4)+i][token l&15].
+// One launch over 151936 rows is 1187 blocks of 4 waves: every block is resident at once, and every
+// wave streams the same 96 KiB.  Each logit is rounded to bf16 (written to `logits` when LOGITS), and
+// the block's best (order_key(logit) << 32 | ~row) per token goes to best[token][vb].
 template <bool LOGITS>
-__global__ void __launch_bounds__(256) lm_head_kernel(const uint16_t* __restrict__ table, int vocab,
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) lm_head_kernel(const uint16_t* __restrict__ table, int vocab,
                                                       const uint16_t* __restrict__ xn, int count,
                                                       float* __restrict__ logits,
                                                       unsigned long long* __restrict__ best) {
-  __shared__ __align__(16) uint16_t xs[16 * kHeadRow];
+  extern __shared__ __align__(16) uint16_t xs[];
   __shared__ unsigned long long red[4][16];
   const int tt = blockIdx.y;
+  const int live_rows = min(16, count - tt * 16);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, col = lane & 15, g = lane >> 4;
-  const int row0 = blockIdx.x * kHeadBlockRows + wave * 16;
-  const uint4* ap = reinterpret_cast<const uint4*>(table + (size_t)(row0 + col) * QWEN_HIDDEN) + g;
-  uint4 a0[8], a1[8];
+  const int row0 = blockIdx.x * (2 * kHeadBlockRows) + wave * 16;  // second tile: row0 + 64
+  const uint4* ap0 = reinterpret_cast<const uint4*>(table + (size_t)(row0 + col) * QWEN_HIDDEN) + g;
+  const uint4* ap1 = ap0 + (size_t)kHeadBlockRows * (QWEN_HIDDEN / 8);
+  uint4 a0[4], a1[4], b0[4], b1[4];
 #pragma unroll
-  for (int s = 0; s < 8; ++s) {
-    const hf32x4 raw = __builtin_nontemporal_load(reinterpret_cast<const hf32x4*>(ap + 4 * s));
-    a0[s] = make_uint4(__float_as_uint(raw[0]), __float_as_uint(raw[1]), __float_as_uint(raw[2]),
-                       __float_as_uint(raw[3]));
+  for (int s = 0; s < 4; ++s) {
+    const hf32x4 r0 = __builtin_nontemporal_load(reinterpret_cast<const hf32x4*>(ap0 + 4 * s));
+    const hf32x4 r1 = __builtin_nontemporal_load(reinterpret_cast<const hf32x4*>(ap1 + 4 * s));
+    a0[s] = make_uint4(__float_as_uint(r0[0]), __float_as_uint(r0[1]), __float_as_uint(r0[2]), __float_as_uint(r0[3]));
+    a1[s] = make_uint4(__float_as_uint(r1[0]), __float_as_uint(r1[1]), __float_as_uint(r1[2]), __float_as_uint(r1[3]));
   }
-  for (int i = threadIdx.x; i < 16 * (QWEN_HIDDEN / 8); i += 256) {
+  for (int i = threadIdx.x; i < live_rows * (QWEN_HIDDEN / 8); i += 256) {
     const int r = i / (QWEN_HIDDEN / 8), c = i % (QWEN_HIDDEN / 8);
     *reinterpret_cast<uint4*>(xs + r * kHeadRow + 8 * c) =
         *reinterpret_cast<const uint4*>(xn + (size_t)(tt * 16 + r) * QWEN_HIDDEN + 8 * c);
   }
   __syncthreads();
-  const uint16_t* xrow = xs + col * kHeadRow + 8 * g;
-  hf32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  head_ksteps(a0, a1, true, ap, 0, xrow, acc);
-  head_ksteps(a1, a0, true, ap, 1, xrow, acc);
-  head_ksteps(a0, a1, true, ap, 2, xrow, acc);
-  head_ksteps(a1, a0, true, ap, 3, xrow, acc);
-  head_ksteps(a0, a1, true, ap, 4, xrow, acc);
-  head_ksteps(a1, a0, false, ap, 5, xrow, acc);
+  const bool live = col < live_rows;
+  const uint16_t* xrow = xs + (live ? col : 0) * kHeadRow + 8 * g;
+  hf32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int kb = 0; kb < 12; kb += 2) {
+    head_ksteps(a0, a1, b0, b1, true, ap0, ap1, kb, xrow, live, acc0, acc1);
+    head_ksteps(b0, b1, a0, a1, kb + 2 < 12, ap0, ap1, kb + 1, xrow, live, acc0, acc1);
+  }
 
   const int tok = tt * 16 + col;
-  unsigned long long bk = 0ull;
-  float lf[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    lf[i] = to_bf16(acc[i]);
-    const uint32_t v = (uint32_t)(row0 + 4 * g + i);
-    const unsigned long long key = ((unsigned long long)order_key(lf[i]) << 32) | (unsigned long long)(~v);
-    bk = key > bk ? key : bk;
+  float lf0[4], lf1[4];
+  const unsigned long long k0 = head_best(acc0, row0, g, lf0);
+  const unsigned long long k1 = head_best(acc1, row0 + kHeadBlockRows, g, lf1);
+  unsigned long long bk = k0 > k1 ? k0 : k1;
+  if (LOGITS && tok < count) {
+    float* lrow = logits + (size_t)tok * vocab + row0 + 4 * g;
+    *reinterpret_cast<float4*>(lrow) = make_float4(lf0[0], lf0[1], lf0[2], lf0[3]);
+    *reinterpret_cast<float4*>(lrow + kHeadBlockRows) = make_float4(lf1[0], lf1[1], lf1[2], lf1[3]);
   }
-  if (LOGITS && tok < count)
-    *reinterpret_cast<float4*>(logits + (size_t)tok * vocab + row0 + 4 * g) = make_float4(lf[0], lf[1], lf[2], lf[3]);
 #pragma unroll
   for (int off = 16; off < 64; off <<= 1) {
     const unsigned long long o = __shfl_xor(bk, off, 64);
@@ -187,7 +210,7 @@ __global__ void __launch_bounds__(256) argmax_finalize_kernel(const unsigned lon
 
 size_t head_workspace_bytes(int count, int vocab) {
   const size_t rows = (size_t)((count + 15) / 16) * 16;
-  return rows * QWEN_HIDDEN * 2u + (size_t)count * (size_t)(vocab / kHeadBlockRows) * 8u + 256u;
+  return rows * QWEN_HIDDEN * 2u + (size_t)count * (size_t)(vocab / (2 * kHeadBlockRows)) * 8u + 256u;
 }
 
 void launch_head(const float* hidden, int count, const uint16_t* norm_w, const uint16_t* table, int vocab,
@@ -197,13 +220,14 @@ void launch_head(const float* hidden, int count, const uint16_t* norm_w, const u
   const size_t xn_bytes = (size_t)tiles * 16 * QWEN_HIDDEN * 2u;
   unsigned long long* best =
       reinterpret_cast<unsigned long long*>(static_cast<char*>(workspace) + ((xn_bytes + 255u) & ~size_t(255u)));
-  const int nblk = vocab / kHeadBlockRows;
+  const int nblk = vocab / (2 * kHeadBlockRows);
+  const size_t lds = (size_t)(count < 16 ? count : 16) * kHeadRow * 2u;  // live token rows of a tile
   hipLaunchKernelGGL(head_norm_kernel, dim3(tiles * 16), dim3(256), 0, st, hidden, count, norm_w, xn);
   if (logits)
-    hipLaunchKernelGGL(lm_head_kernel<true>, dim3(nblk, tiles), dim3(256), 0, st, table, vocab, xn, count, logits,
+    hipLaunchKernelGGL(lm_head_kernel<true>, dim3(nblk, tiles), dim3(256), lds, st, table, vocab, xn, count, logits,
                        best);
   else
-    hipLaunchKernelGGL(lm_head_kernel<false>, dim3(nblk, tiles), dim3(256), 0, st, table, vocab, xn, count, logits,
+    hipLaunchKernelGGL(lm_head_kernel<false>, dim3(nblk, tiles), dim3(256), lds, st, table, vocab, xn, count, logits,
                        best);
   if (ids) hipLaunchKernelGGL(argmax_finalize_kernel, dim3(count), dim3(256), 0, st, best, nblk, ids);
 }

@@ -541,8 +541,8 @@ int qwen_hip_model_embed(qwen_hip_model* m, const int* token_ids, int count, flo
 }
 
 int qwen_hip_model_set_head(qwen_hip_model* m, int vocab, const uint16_t* embed_bf16, const uint16_t* norm_bf16) {
-  if (!m || !embed_bf16 || !norm_bf16 || vocab <= 0 || vocab % 64 != 0 || vocab > (1 << 24))
-    return invalid("invalid head arguments (vocab must be a positive multiple of 64)");
+  if (!m || !embed_bf16 || !norm_bf16 || vocab <= 0 || vocab % 128 != 0 || vocab > (1 << 24))
+    return invalid("invalid head arguments (vocab must be a positive multiple of 128)");
   std::lock_guard<std::mutex> lock(m->mu);
   return guarded_model([&]() -> int {
     QWEN_HIP(hipStreamSynchronize(m->stream));

@@ -143,7 +143,7 @@ class DeviceModel:
 
     def set_head(self, embed_bf16: np.ndarray, norm_bf16: np.ndarray) -> None:
         """Uploads a tied bf16 embedding / lm_head table [vocab, 1536] and the bf16 final RMSNorm
-        weight [1536], both as uint16 bit patterns (vocab a multiple of 64)."""
+        weight [1536], both as uint16 bit patterns (vocab a multiple of 128)."""
         embed = np.ascontiguousarray(embed_bf16, dtype=np.uint16)
         norm = np.ascontiguousarray(norm_bf16, dtype=np.uint16)
         if embed.ndim != 2 or embed.shape[1] != 1536 or norm.shape != (1536,):
