@@ -88,6 +88,15 @@ int qwen_hip_model_decode(qwen_hip_model* m, int mode, int batch, float* hidden,
 int qwen_hip_model_prefill(qwen_hip_model* m, int mode, int batch, int seq_len, float* hidden, float* k_cache,
                            float* v_cache, uint64_t seq_stride, uint64_t layer_stride);
 
+/* Chunked prefill: seq_len new tokens per sequence at positions past..past+seq_len-1 of sequences
+ * whose cache rows 0..past-1 already hold the earlier tokens (a previous prefill or chunk).  Query
+ * past+i attends keys 0..past+i; rows past..past+seq_len-1 are written.  The reference has no
+ * continuation entry (its prefill starts at position 0); the arithmetic per token is the reference
+ * prefill's, so splitting a prompt into chunks reproduces the single prefill: bit-exactly in
+ * QWEN_MODE_ORDERED.  seq_stride must hold past + seq_len rows. */
+int qwen_hip_model_prefill_chunk(qwen_hip_model* m, int mode, int batch, int seq_len, int past, float* hidden,
+                                 float* k_cache, float* v_cache, uint64_t seq_stride, uint64_t layer_stride);
+
 /* Embedding lookup from the model's bf16 table: hidden[i] = fp32(table[token_ids[i]]) (ids outside
  * [0, vocab) read row 0).  token_ids and hidden are device pointers. */
 int qwen_hip_model_embed(qwen_hip_model* m, const int* token_ids, int count, float* hidden);

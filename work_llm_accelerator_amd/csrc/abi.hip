@@ -274,7 +274,7 @@ int prefill_layer_host(const HostLayer& h, const float* x, int S, float* k_cache
     float* kc_d = A.alloc_n<float>((size_t)S * QWEN_KV_WIDTH);
     float* vc_d = A.alloc_n<float>((size_t)S * QWEN_KV_WIDTH);
     float* att_d = A.alloc_n<float>((size_t)S * QWEN_HIDDEN);
-    run_prefill_attention(d, x_d, S, rope, kc_d, vc_d, att_d, A, st);
+    run_prefill_attention(d, x_d, S, 0, rope, kc_d, vc_d, att_d, A, st);
     copy_out(k_cache, kc_d, (size_t)S * QWEN_KV_WIDTH, st);
     copy_out(v_cache, vc_d, (size_t)S * QWEN_KV_WIDTH, st);
     if (att_host) copy_out(att_host, att_d, (size_t)S * QWEN_HIDDEN, st);

@@ -17,8 +17,10 @@ void launch_rope_append_decode(float* q, const float* k, const float* v, const i
                                int max_keys, int tokens, hipStream_t st);
 void launch_rope_prefill(float* q, float* k_rows, const float* rope, int tokens, hipStream_t st);
 void launch_rope_table_prefill(float* rope, int first, int count, hipStream_t st);
+// prefill: token b is the query at position past + b over keys 0..past+b of one sequence's rows.
 void launch_attention_ordered(const float* q, const float* k_cache, const float* v_cache, size_t cache_stride,
-                              const int* pos, int max_keys, int tokens, bool prefill, float* ctx, hipStream_t st);
+                              const int* pos, int max_keys, int tokens, bool prefill, int past, float* ctx,
+                              hipStream_t st);
 
 // ---- FAST kernels: kernels_fast.hip ----
 constexpr int kKChunk = 128;        // K values per repacked weight chunk
@@ -80,7 +82,9 @@ void launch_repack_int4(const uint8_t* W, int out_dim, int in_dim, uint8_t* WP, 
 void launch_norm_quant(const float* x, size_t x_stride, int rows, int n, const float* w, int norm, int8_t* xq,
                        float* sx, int* sums, float* xn, hipStream_t st);
 void launch_gemm_i8(const GemmArgs& a, int epi, hipStream_t st);
-void launch_rope_qkv(float* qkv, int qkv_stride, const int* pos, int seq_len, int limit, int tokens,
+// Decode (pos given): token t is sequence t at position pos[t].  Prefill (pos null): token t is
+// sequence t / seq_len at position past + t % seq_len.  Positions outside [0, limit) are skipped.
+void launch_rope_qkv(float* qkv, int qkv_stride, const int* pos, int seq_len, int past, int limit, int tokens,
                      const float* rope, float* k_cache, float* v_cache, size_t seq_stride, hipStream_t st);
 // Decode attention split: nsplit blocks of `chunk` keys (a multiple of 16) per sequence and KV
 // head, sized so that one launch fills the device once.  Workspace: part [batch][12][nsplit][128]
@@ -95,11 +99,13 @@ void launch_attn_decode(const float* qkv, int qkv_stride, const float* k_cache, 
                         size_t seq_stride, const int* pos, int batch, int max_keys, const AttnDecodePlan& plan,
                         float* part, float2* pml, unsigned* arrivals, float* ctx, int8_t* xq, float* sx, int* sums,
                         hipStream_t st);
-// Prefill attention: K/V converted once into bf16 hi/lo tiles (workspace of
-// attn_prefill_workspace_bytes), then the causal attention over them.
-size_t attn_prefill_workspace_bytes(int S, int nseq);
+// Prefill attention of S new tokens per sequence at positions past..past+S-1 over the cache rows
+// 0..past+S-1: K/V converted once into bf16 hi/lo tiles (workspace of
+// attn_prefill_workspace_bytes(past + S, nseq)), then the causal attention over them.
+size_t attn_prefill_workspace_bytes(int keys, int nseq);
 void launch_attn_prefill(const float* qkv, int qkv_stride, const float* k_cache, const float* v_cache,
-                         size_t seq_stride, int S, int nseq, uint8_t* kv_tiles, float* ctx, hipStream_t st);
+                         size_t seq_stride, int S, int past, int nseq, uint8_t* kv_tiles, float* ctx,
+                         hipStream_t st);
 void launch_round_bf16(float* x, size_t n, hipStream_t st);
 
 }  // namespace qwen

@@ -1162,13 +1162,13 @@ __global__ void __launch_bounds__(256) reduce_norm_quant_kernel(GemmArgs a, int 
 // grid = tokens, block = 64 (one rotation pair per thread).
 // ---------------------------------------------------------------------------------------------
 __global__ void __launch_bounds__(64) rope_qkv_kernel(float* __restrict__ qkv, int qkv_stride,
-                                                      const int* __restrict__ pos, int seq_len, int limit,
+                                                      const int* __restrict__ pos, int seq_len, int past, int limit,
                                                       const float* __restrict__ rope, float* __restrict__ k_cache,
                                                       float* __restrict__ v_cache, size_t seq_stride) {
   const int t = blockIdx.x;
   const int p = threadIdx.x;
   const int seq = pos ? t : t / seq_len;
-  const int P = pos ? pos[t] : t % seq_len;
+  const int P = pos ? pos[t] : past + t % seq_len;
   if (P < 0 || P >= limit) return;  // position outside the cache rows the caller sized
   const float c = rope[(size_t)P * 128 + p];
   const float sn = rope[(size_t)P * 128 + 64 + p];
@@ -1522,7 +1522,8 @@ __global__ void __launch_bounds__(256) kv_bf16_tiles_kernel(const float* __restr
 
 // ---------------------------------------------------------------------------------------------
 // Causal prefill attention over the bf16 hi/lo tiles of kv_bf16_tiles_kernel.  Semantics of
-// qwen_prefill_attention_kernel.cpp:204-289: keys 0..i for query i, scale 0.08838834764831845f,
+// qwen_prefill_attention_kernel.cpp:204-289 (keys 0..p for the query at position p, scale
+// 0.08838834764831845f), for S new queries at positions past..past+S-1 over past+S keys;
 // online softmax (exp evaluated with __expf, inside the FAST tolerance).  Per 32-key tile and
 // compute wave (lane: col = l & 15, g = l >> 4):
 //   S^T = K . Q^T: A = K[key][32m + 8g..+7], B = Q[query][same dims] -> S[key 4g+r][query col];
@@ -1539,7 +1540,7 @@ __global__ void __launch_bounds__(256) kv_bf16_tiles_kernel(const float* __restr
 constexpr int kPfStages = 3;
 
 __global__ void __launch_bounds__(512) attn_prefill_tiles_kernel(const float* __restrict__ qkv, int qkv_stride,
-                                                                 const uint8_t* __restrict__ kvt, int S,
+                                                                 const uint8_t* __restrict__ kvt, int S, int past,
                                                                  float* __restrict__ ctx) {
   __shared__ __align__(16) uint8_t stages[kPfStages][kPfTileBytes];
   const int nqt = gridDim.x;
@@ -1548,10 +1549,11 @@ __global__ void __launch_bounds__(512) attn_prefill_tiles_kernel(const float* __
   const int sq = blockIdx.z;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int q0 = qt * kPfQ;
-  const int qlast = min(q0 + kPfQ, S) - 1;
-  const int ntiles = qlast / kPfKeys + 1;  // key tiles 0 .. qlast/32 (causal)
-  const int ntile_all = (S + kPfKeys - 1) / kPfKeys;
+  const int q0 = qt * kPfQ;                   // local query rows q0.. of the S new tokens
+  const int nkeys = past + S;                 // keys of the sequence (past rows, then the new ones)
+  const int qlast = past + min(q0 + kPfQ, S) - 1;  // last query position of the block
+  const int ntiles = qlast / kPfKeys + 1;     // key tiles 0 .. qlast/32 (causal)
+  const int ntile_all = (nkeys + kPfKeys - 1) / kPfKeys;
   const uint8_t* tiles = kvt + (size_t)(sq * 2 + kvh) * ntile_all * kPfTileBytes;
 
   if (wave >= QWEN_GROUPS) {
@@ -1632,18 +1634,20 @@ __global__ void __launch_bounds__(512) attn_prefill_tiles_kernel(const float* __
     bf16x8 ph[2], pl[2];
 #pragma unroll
     for (int qs = 0; qs < 2; ++qs) {
-      const int qi = q0 + 16 * qs + col;
+      const int qpos = past + q0 + 16 * qs + col;  // position of this column's query
       float mt = -INFINITY;
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int key = t * kPfKeys + kt * 16 + 4 * g + r;
-          if (key > qi || key >= S) sc[qs][kt][r] = -INFINITY;
+          if (key > qpos || key >= nkeys) sc[qs][kt][r] = -INFINITY;
           mt = fmaxf(mt, sc[qs][kt][r]);
         }
       mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-      mt = fmaxf(mt, __shfl_xor(mt, 32, 64));  // finite: key t*32 <= q0 <= qi
+      // Tile 0 holds key 0 <= qpos, so m_run is finite from tile 0 on; a later tile with every key
+      // past qpos gives mt = -inf, corr = 1 and p = 0, leaving the column's state unchanged.
+      mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
       const float mn = fmaxf(m_run[qs], mt);
       const float corr = __expf(m_run[qs] - mn);
       float p[8];
@@ -1854,10 +1858,10 @@ void launch_gemm_i8(const GemmArgs& a, int epi, hipStream_t st) {
   }
 }
 
-void launch_rope_qkv(float* qkv, int qkv_stride, const int* pos, int seq_len, int limit, int tokens,
+void launch_rope_qkv(float* qkv, int qkv_stride, const int* pos, int seq_len, int past, int limit, int tokens,
                      const float* rope, float* k_cache, float* v_cache, size_t seq_stride, hipStream_t st) {
-  hipLaunchKernelGGL(rope_qkv_kernel, dim3(tokens), dim3(64), 0, st, qkv, qkv_stride, pos, seq_len, limit, rope,
-                     k_cache, v_cache, seq_stride);
+  hipLaunchKernelGGL(rope_qkv_kernel, dim3(tokens), dim3(64), 0, st, qkv, qkv_stride, pos, seq_len, past, limit,
+                     rope, k_cache, v_cache, seq_stride);
 }
 
 constexpr int kAttnMinChunk = 64;
@@ -1897,17 +1901,19 @@ void launch_attn_decode(const float* qkv, int qkv_stride, const float* k_cache, 
                      k_cache, v_cache, seq_stride, pos, plan.chunk, max_keys, part, pml, arrivals, ctx, xq, sx, sums);
 }
 
-size_t attn_prefill_workspace_bytes(int S, int nseq) {
-  return (size_t)nseq * QWEN_KV_HEADS * ((S + kPfKeys - 1) / kPfKeys) * kPfTileBytes;
+size_t attn_prefill_workspace_bytes(int keys, int nseq) {
+  return (size_t)nseq * QWEN_KV_HEADS * ((keys + kPfKeys - 1) / kPfKeys) * kPfTileBytes;
 }
 
 void launch_attn_prefill(const float* qkv, int qkv_stride, const float* k_cache, const float* v_cache,
-                         size_t seq_stride, int S, int nseq, uint8_t* kv_tiles, float* ctx, hipStream_t st) {
-  const int ntile = (S + kPfKeys - 1) / kPfKeys;
+                         size_t seq_stride, int S, int past, int nseq, uint8_t* kv_tiles, float* ctx,
+                         hipStream_t st) {
+  const int keys = past + S;
+  const int ntile = (keys + kPfKeys - 1) / kPfKeys;
   hipLaunchKernelGGL(kv_bf16_tiles_kernel, dim3(ntile, QWEN_KV_HEADS, nseq), dim3(256), 0, st, k_cache, v_cache,
-                     seq_stride, S, kv_tiles);
+                     seq_stride, keys, kv_tiles);
   hipLaunchKernelGGL(attn_prefill_tiles_kernel, dim3((S + kPfQ - 1) / kPfQ, QWEN_KV_HEADS, nseq), dim3(512), 0, st,
-                     qkv, qkv_stride, kv_tiles, S, ctx);
+                     qkv, qkv_stride, kv_tiles, S, past, ctx);
 }
 
 void launch_round_bf16(float* x, size_t n, hipStream_t st) {

@@ -251,7 +251,7 @@ __global__ void __launch_bounds__(128) attention_ordered_kernel(const float* __r
                                                                 const float* __restrict__ k_cache,
                                                                 const float* __restrict__ v_cache, size_t cache_stride,
                                                                 const int* __restrict__ pos, int max_keys, int prefill,
-                                                                float* __restrict__ ctx) {
+                                                                int past, float* __restrict__ ctx) {
   __shared__ float qs[QWEN_HEAD_DIM];
   __shared__ float es[128];
   __shared__ float red[128];
@@ -260,7 +260,7 @@ __global__ void __launch_bounds__(128) attention_ordered_kernel(const float* __r
   const int b = blockIdx.y;
   const int tid = threadIdx.x;
   const int kvh = h / QWEN_GROUPS;
-  const int n = prefill ? b + 1 : min(max(pos[b], 0) + 1, max_keys);
+  const int n = prefill ? past + b + 1 : min(max(pos[b], 0) + 1, max_keys);
   // Decode's (float)(1.0/sqrt(128.0)) and prefill's 0.08838834764831845f are the same float
   // (bits 0x3db504f3; checked by tests/test_oracle_math.py).
   const float scaling = 0.08838834764831845f;
@@ -354,9 +354,10 @@ void launch_rope_table_prefill(float* rope, int first, int count, hipStream_t st
 }
 
 void launch_attention_ordered(const float* q, const float* k_cache, const float* v_cache, size_t cache_stride,
-                              const int* pos, int max_keys, int tokens, bool prefill, float* ctx, hipStream_t st) {
+                              const int* pos, int max_keys, int tokens, bool prefill, int past, float* ctx,
+                              hipStream_t st) {
   hipLaunchKernelGGL(attention_ordered_kernel, dim3(QWEN_Q_HEADS, tokens), dim3(128), 0, st, q, k_cache, v_cache,
-                     cache_stride, pos, max_keys, prefill ? 1 : 0, ctx);
+                     cache_stride, pos, max_keys, prefill ? 1 : 0, past, ctx);
 }
 
 }  // namespace qwen

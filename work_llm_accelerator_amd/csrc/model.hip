@@ -53,7 +53,7 @@ struct DevBuf {
 
 struct LastCall {
   int kind = 0;  // 0 none, 1 decode, 2 prefill
-  int mode = 0, batch = 0, seq_len = 0, max_keys = 0;
+  int mode = 0, batch = 0, seq_len = 0, max_keys = 0, past = 0;
   const int* positions = nullptr;
   float *k_cache = nullptr, *v_cache = nullptr;
   uint64_t seq_stride = 0, layer_stride = 0;
@@ -274,7 +274,7 @@ struct qwen_hip_model {
              nullptr, 0, 0, &fq);
       } else {
         gemm(w, B, QWEN_HIDDEN, (int)kQkvRows, f.qkv, f.sw_qkv, f.b_qkv, w.qkv, kQkvRows, kEpiStore);
-        launch_rope_qkv(w.qkv, (int)kQkvRows, pos, 1, max_keys, B, rope_decode, kc, vc, ss, stream);
+        launch_rope_qkv(w.qkv, (int)kQkvRows, pos, 1, 0, max_keys, B, rope_decode, kc, vc, ss, stream);
       }
       launch_attn_decode(w.qkv, (int)kQkvRows, kc, vc, ss, pos, B, max_keys, plan, w.part, w.pml, w.arrivals,
                          nullptr, w.xq, w.sx, w.sums, stream);
@@ -305,9 +305,12 @@ struct qwen_hip_model {
     QWEN_HIP(hipGetLastError());
   }
 
-  void prefill_fast(int B, int S, float* hidden, float* kc0, float* vc0, uint64_t ss, uint64_t ls, int round) {
+  // FAST prefill of S new tokens per sequence at positions past..past+S-1 (cache rows 0..past-1 hold
+  // the earlier tokens of each sequence).
+  void prefill_fast(int B, int S, int past, float* hidden, float* kc0, float* vc0, uint64_t ss, uint64_t ls,
+                    int round) {
     const int T = B * S;
-    const Ws w = carve(T, 1, 1, attn_prefill_workspace_bytes(S, B));
+    const Ws w = carve(T, 1, 1, attn_prefill_workspace_bytes(past + S, B));
     for (int l = 0; l < layers; ++l) {
       const FastLayer& f = fast[l];
       float* kc = kc0 + (size_t)l * ls;
@@ -315,8 +318,8 @@ struct qwen_hip_model {
       launch_norm_quant(hidden, QWEN_HIDDEN, T, QWEN_HIDDEN, f.ln, kNormPrefill, w.xq, w.sx, w.sums, nullptr,
                         stream);
       gemm(w, T, QWEN_HIDDEN, (int)kQkvRows, f.qkv, f.sw_qkv, f.b_qkv, w.qkv, kQkvRows, kEpiStore);
-      launch_rope_qkv(w.qkv, (int)kQkvRows, nullptr, S, S, T, rope_prefill, kc, vc, ss, stream);
-      launch_attn_prefill(w.qkv, (int)kQkvRows, kc, vc, ss, S, B, w.kvt, w.ctx, stream);
+      launch_rope_qkv(w.qkv, (int)kQkvRows, nullptr, S, past, past + S, T, rope_prefill, kc, vc, ss, stream);
+      launch_attn_prefill(w.qkv, (int)kQkvRows, kc, vc, ss, S, past, B, w.kvt, w.ctx, stream);
       launch_norm_quant(w.ctx, QWEN_HIDDEN, T, QWEN_HIDDEN, nullptr, kNormNone, w.xq, w.sx, w.sums, nullptr, stream);
       gemm(w, T, QWEN_HIDDEN, QWEN_HIDDEN, f.o, f.sw_o, nullptr, w.att, QWEN_HIDDEN, kEpiStore);
       launch_norm_quant(w.att, QWEN_HIDDEN, T, QWEN_HIDDEN, f.post_ln, kNormPrefill, w.xq, w.sx, w.sums, nullptr,
@@ -347,7 +350,8 @@ struct qwen_hip_model {
     QWEN_HIP(hipGetLastError());
   }
 
-  void prefill_ordered(int B, int S, float* hidden, float* kc0, float* vc0, uint64_t ss, uint64_t ls, int round) {
+  void prefill_ordered(int B, int S, int past, float* hidden, float* kc0, float* vc0, uint64_t ss, uint64_t ls,
+                       int round) {
     float* att = scratch((size_t)S * QWEN_HIDDEN * 4u);
     for (int l = 0; l < layers; ++l) {
       const DevLayer d = dev_layer(l);
@@ -355,7 +359,7 @@ struct qwen_hip_model {
         float* x = hidden + (size_t)b * S * QWEN_HIDDEN;
         arena.reset();
         arena.reserve(prefill_workspace_bytes(S));
-        run_prefill_attention(d, x, S, rope_prefill, kc0 + (size_t)l * ls + (size_t)b * ss,
+        run_prefill_attention(d, x, S, past, rope_prefill, kc0 + (size_t)l * ls + (size_t)b * ss,
                               vc0 + (size_t)l * ls + (size_t)b * ss, att, arena, stream);
         run_prefill_mlp(d, att, S, x, arena, stream);
       }
@@ -503,30 +507,38 @@ int qwen_hip_model_decode(qwen_hip_model* m, int mode, int batch, float* hidden,
       m->decode_fast(batch, hidden, positions, max_keys, k_cache, v_cache, seq_stride, layer_stride, round);
     else
       m->decode_ordered(batch, hidden, positions, max_keys, k_cache, v_cache, seq_stride, layer_stride, round);
-    m->last = LastCall{1, mode, batch, 1, max_keys, positions, k_cache, v_cache, seq_stride, layer_stride};
+    m->last = LastCall{1, mode, batch, 1, max_keys, 0, positions, k_cache, v_cache, seq_stride, layer_stride};
+    return QWEN_OK;
+  });
+}
+
+int qwen_hip_model_prefill_chunk(qwen_hip_model* m, int mode, int batch, int seq_len, int past, float* hidden,
+                                 float* k_cache, float* v_cache, uint64_t seq_stride, uint64_t layer_stride) {
+  if (!m || !hidden || !k_cache || !v_cache) return invalid("null argument");
+  const int round = (mode & QWEN_FLAG_NO_BF16_ROUND) ? 0 : 1;
+  mode &= ~QWEN_FLAG_NO_BF16_ROUND;
+  if (batch <= 0 || seq_len <= 0 || past < 0 || past > QWEN_MAX_SEQ - seq_len || seq_len > QWEN_MAX_SEQ ||
+      (mode != QWEN_MODE_ORDERED && mode != QWEN_MODE_FAST))
+    return invalid("invalid prefill shape, past length or mode");
+  const uint64_t rows = (uint64_t)past + (uint64_t)seq_len;
+  if (seq_stride < rows * QWEN_KV_WIDTH || (batch > 1 && layer_stride < (uint64_t)batch * seq_stride) ||
+      (m->layers > 1 && layer_stride == 0))
+    return invalid("KV strides too small for past + seq_len / batch");
+  std::lock_guard<std::mutex> lock(m->mu);
+  return guarded_model([&]() -> int {
+    if (mode == QWEN_MODE_FAST)
+      m->prefill_fast(batch, seq_len, past, hidden, k_cache, v_cache, seq_stride, layer_stride, round);
+    else
+      m->prefill_ordered(batch, seq_len, past, hidden, k_cache, v_cache, seq_stride, layer_stride, round);
+    m->last = LastCall{2, mode, batch, seq_len, past + seq_len, past, nullptr, k_cache, v_cache, seq_stride,
+                       layer_stride};
     return QWEN_OK;
   });
 }
 
 int qwen_hip_model_prefill(qwen_hip_model* m, int mode, int batch, int seq_len, float* hidden, float* k_cache,
                            float* v_cache, uint64_t seq_stride, uint64_t layer_stride) {
-  if (!m || !hidden || !k_cache || !v_cache) return invalid("null argument");
-  const int round = (mode & QWEN_FLAG_NO_BF16_ROUND) ? 0 : 1;
-  mode &= ~QWEN_FLAG_NO_BF16_ROUND;
-  if (batch <= 0 || seq_len <= 0 || seq_len > QWEN_MAX_SEQ || (mode != QWEN_MODE_ORDERED && mode != QWEN_MODE_FAST))
-    return invalid("invalid prefill shape or mode");
-  if (seq_stride < (uint64_t)seq_len * QWEN_KV_WIDTH || (batch > 1 && layer_stride < (uint64_t)batch * seq_stride) ||
-      (m->layers > 1 && layer_stride == 0))
-    return invalid("KV strides too small for seq_len / batch");
-  std::lock_guard<std::mutex> lock(m->mu);
-  return guarded_model([&]() -> int {
-    if (mode == QWEN_MODE_FAST)
-      m->prefill_fast(batch, seq_len, hidden, k_cache, v_cache, seq_stride, layer_stride, round);
-    else
-      m->prefill_ordered(batch, seq_len, hidden, k_cache, v_cache, seq_stride, layer_stride, round);
-    m->last = LastCall{2, mode, batch, seq_len, seq_len, nullptr, k_cache, v_cache, seq_stride, layer_stride};
-    return QWEN_OK;
-  });
+  return qwen_hip_model_prefill_chunk(m, mode, batch, seq_len, 0, hidden, k_cache, v_cache, seq_stride, layer_stride);
 }
 
 int qwen_hip_model_embed(qwen_hip_model* m, const int* token_ids, int count, float* hidden) {
@@ -597,7 +609,7 @@ int qwen_hip_model_time_kernel(qwen_hip_model* m, int kernel, int layer, int rep
     const int T = c.batch * c.seq_len;
     const AttnDecodePlan plan = plan_attn_decode(decode ? c.batch : 1, c.max_keys);
     const qwen_hip_model::Ws w = m->carve(T, decode ? c.batch : 1, decode ? plan.nsplit : 1,
-                                          decode ? 0 : attn_prefill_workspace_bytes(c.seq_len, c.batch));
+                                          decode ? 0 : attn_prefill_workspace_bytes(c.max_keys, c.batch));
     const FastLayer& f = m->fast[layer];
     float* kc = c.k_cache + (size_t)layer * c.layer_stride;
     float* vc = c.v_cache + (size_t)layer * c.layer_stride;
@@ -622,7 +634,7 @@ int qwen_hip_model_time_kernel(qwen_hip_model* m, int kernel, int layer, int rep
           m->gemm(w, T, QWEN_HIDDEN, QWEN_HIDDEN, f.o, f.sw_o, nullptr, w.tmp, QWEN_HIDDEN, kEpiStore);
           break;
         case QWEN_KERNEL_ATTN_PREFILL:
-          launch_attn_prefill(w.qkv, (int)kQkvRows, kc, vc, c.seq_stride, c.seq_len, c.batch, w.kvt, w.ctx,
+          launch_attn_prefill(w.qkv, (int)kQkvRows, kc, vc, c.seq_stride, c.seq_len, c.past, c.batch, w.kvt, w.ctx,
                               m->stream);
           break;
         default:

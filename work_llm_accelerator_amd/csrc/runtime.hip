@@ -175,7 +175,7 @@ void run_decode_attention(const DevLayer& L, const float* x, const DecodeBatch& 
   launch_project_ordered(xn, T, QWEN_HIDDEN, L.vw, L.vs, L.vb, QWEN_KV_WIDTH, v, nullptr, st);
   launch_rope_append_decode(q, k, v, b.pos, b.rope, b.rope_per_token, b.k_cache, b.v_cache, b.cache_stride,
                             b.max_keys, T, st);
-  launch_attention_ordered(q, b.k_cache, b.v_cache, b.cache_stride, b.pos, b.max_keys, T, false, ctx, st);
+  launch_attention_ordered(q, b.k_cache, b.v_cache, b.cache_stride, b.pos, b.max_keys, T, false, 0, ctx, st);
   launch_project_ordered(ctx, T, QWEN_HIDDEN, L.ow, L.os, nullptr, QWEN_HIDDEN, att, nullptr, st);
   QWEN_HIP(hipGetLastError());
 }
@@ -193,17 +193,19 @@ void run_decode_mlp(const DevLayer& L, const float* att, int T, float* out, Aren
   QWEN_HIP(hipGetLastError());
 }
 
-void run_prefill_attention(const DevLayer& L, const float* x, int T, const float* rope, float* k_rows, float* v_rows,
-                           float* att, Arena& a, hipStream_t st) {
+void run_prefill_attention(const DevLayer& L, const float* x, int T, int past, const float* rope, float* k_rows,
+                           float* v_rows, float* att, Arena& a, hipStream_t st) {
+  float* k_new = k_rows + (size_t)past * QWEN_KV_WIDTH;
+  float* v_new = v_rows + (size_t)past * QWEN_KV_WIDTH;
   float* xn = a.alloc_n<float>((size_t)T * QWEN_HIDDEN);
   float* q = a.alloc_n<float>((size_t)T * QWEN_HIDDEN);
   float* ctx = a.alloc_n<float>((size_t)T * QWEN_HIDDEN);
   launch_rmsnorm_ordered(x, L.ln, xn, T, true, st);
-  launch_project_ordered(xn, T, QWEN_HIDDEN, L.kw, L.ks, L.kb, QWEN_KV_WIDTH, k_rows, nullptr, st);
-  launch_project_ordered(xn, T, QWEN_HIDDEN, L.vw, L.vs, L.vb, QWEN_KV_WIDTH, v_rows, nullptr, st);
+  launch_project_ordered(xn, T, QWEN_HIDDEN, L.kw, L.ks, L.kb, QWEN_KV_WIDTH, k_new, nullptr, st);
+  launch_project_ordered(xn, T, QWEN_HIDDEN, L.vw, L.vs, L.vb, QWEN_KV_WIDTH, v_new, nullptr, st);
   launch_project_ordered(xn, T, QWEN_HIDDEN, L.qw, L.qs, L.qb, QWEN_HIDDEN, q, nullptr, st);
-  launch_rope_prefill(q, k_rows, rope, T, st);
-  launch_attention_ordered(q, k_rows, v_rows, 0, nullptr, T, T, true, ctx, st);
+  launch_rope_prefill(q, k_new, rope + (size_t)past * 128, T, st);
+  launch_attention_ordered(q, k_rows, v_rows, 0, nullptr, past + T, T, true, past, ctx, st);
   launch_project_ordered(ctx, T, QWEN_HIDDEN, L.ow, L.os, nullptr, QWEN_HIDDEN, att, nullptr, st);
   QWEN_HIP(hipGetLastError());
 }

@@ -124,7 +124,9 @@ size_t prefill_workspace_bytes(int tokens);
 void run_decode_attention(const DevLayer& L, const float* x, const DecodeBatch& b, float* att, Arena& a,
                           hipStream_t st);
 void run_decode_mlp(const DevLayer& L, const float* att, int tokens, float* out, Arena& a, hipStream_t st);
-void run_prefill_attention(const DevLayer& L, const float* x, int tokens, const float* rope, float* k_rows,
+// Prefill attention of `tokens` new tokens at positions past..past+tokens-1 of one sequence whose cache
+// rows start at k_rows / v_rows (rows 0..past-1 hold the earlier tokens; the new rows are written).
+void run_prefill_attention(const DevLayer& L, const float* x, int tokens, int past, const float* rope, float* k_rows,
                            float* v_rows, float* att, Arena& a, hipStream_t st);
 void run_prefill_mlp(const DevLayer& L, const float* att, int tokens, float* out, Arena& a, hipStream_t st);
 

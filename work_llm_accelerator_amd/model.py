@@ -121,14 +121,15 @@ class DeviceModel:
                                             _ptr(cache.k), _ptr(cache.v), cache.seq_stride, cache.layer_stride)
         _check(self.lib, st, "qwen_hip_model_decode")
 
-    def prefill(self, mode: int, hidden, cache: KvCache, order: bool = True) -> None:
-        """hidden [B,S,1536] fp32 (in/out); cache rows 0..S-1 of sequences 0..B-1 are written."""
+    def prefill(self, mode: int, hidden, cache: KvCache, order: bool = True, past: int = 0) -> None:
+        """hidden [B,S,1536] fp32 (in/out) at positions past..past+S-1; cache rows past..past+S-1 of
+        sequences 0..B-1 are written (rows 0..past-1 hold the earlier tokens)."""
         if order:
             self._enter()
         B, S = hidden.shape[0], hidden.shape[1]
-        st = self.lib.qwen_hip_model_prefill(self.handle, mode, B, S, _ptr(hidden), _ptr(cache.k), _ptr(cache.v),
-                                             cache.seq_stride, cache.layer_stride)
-        _check(self.lib, st, "qwen_hip_model_prefill")
+        st = self.lib.qwen_hip_model_prefill_chunk(self.handle, mode, B, S, int(past), _ptr(hidden), _ptr(cache.k),
+                                                   _ptr(cache.v), cache.seq_stride, cache.layer_stride)
+        _check(self.lib, st, "qwen_hip_model_prefill_chunk")
 
     def embed(self, token_ids, hidden, order: bool = True) -> None:
         if order:
