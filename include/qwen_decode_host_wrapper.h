@@ -75,6 +75,20 @@ int qwen_decode_dispatch_layers_forward(
     const float* scale_ddr, float* kv_cache_ddr, float* activation_ddr, uint8_t* weight_sram, float* kv_sram,
     int32_t* partial_sum_sram, float* softmax_sram, float* control_sram, int* completed_layer_count);
 
+/* Replaces qwen_decode_host_wrapper.h:89-113 (impl qwen_decode_layer0_reference_wrapper.cpp:75-209):
+ * the unquantized layer with fp32 weights [out][in] (biases may be null), every linear accumulated in
+ * double and rounded to bf16, double softmax, attention residual kept.  Caches are HF head-major:
+ * past_k/v_cache [2][past_seq_len][128] in, next_k/v_cache [2][past_seq_len+1][128] out.  Returns 1
+ * for a null input/output/cache pointer or a negative past length (as the reference), and also for
+ * null weights or past caches the reference would dereference. */
+int qwen_decode_layer0_reference_forward(
+    const float* input_token, int past_seq_len, const float* past_k_cache, const float* past_v_cache,
+    const float* input_layernorm_weight, const float* q_weight, const float* q_bias, const float* k_weight,
+    const float* k_bias, const float* v_weight, const float* v_bias, const float* o_weight, const float* o_bias,
+    const float* post_attention_layernorm_weight, const float* gate_weight, const float* gate_bias,
+    const float* up_weight, const float* up_bias, const float* down_weight, const float* down_bias, float rms_eps,
+    float* output_token, float* next_k_cache, float* next_v_cache);
+
 #ifdef __cplusplus
 }
 #endif

@@ -103,6 +103,25 @@ int qwen_prefill_dispatch_layers_forward(
     const float* scale_ddr, float* kv_cache_ddr, float* activation_ddr, uint8_t* weight_sram, float* kv_sram,
     int32_t* partial_sum_sram, float* softmax_sram, float* control_sram, int* completed_layer_count);
 
+/* Replace qwen_prefill_host_wrapper.h:171-215 (impl qwen_prefill_layer0_reference_wrapper.cpp:60-347):
+ * the unquantized layer over seq_len tokens at positions 0..seq_len-1 with fp32 weights (biases may
+ * be null), double-accumulated linears rounded to bf16, bf16-rounded RoPE, causal double softmax,
+ * attention residual kept; _with_cache also writes the bf16-rounded K/V as HF head-major
+ * [2][seq_len][128].  Return 1 for a null input/output, seq_len outside [1, 32768], or exactly one
+ * null cache pointer (as the reference), and also for null weights. */
+int qwen_prefill_layer0_reference_forward(
+    const float* input_sequence, int seq_len, const float* input_layernorm_weight, const float* q_weight,
+    const float* q_bias, const float* k_weight, const float* k_bias, const float* v_weight, const float* v_bias,
+    const float* o_weight, const float* o_bias, const float* post_attention_layernorm_weight, const float* gate_weight,
+    const float* gate_bias, const float* up_weight, const float* up_bias, const float* down_weight,
+    const float* down_bias, float rms_eps, float* output_sequence);
+int qwen_prefill_layer0_reference_forward_with_cache(
+    const float* input_sequence, int seq_len, const float* input_layernorm_weight, const float* q_weight,
+    const float* q_bias, const float* k_weight, const float* k_bias, const float* v_weight, const float* v_bias,
+    const float* o_weight, const float* o_bias, const float* post_attention_layernorm_weight, const float* gate_weight,
+    const float* gate_bias, const float* up_weight, const float* up_bias, const float* down_weight,
+    const float* down_bias, float rms_eps, float* output_sequence, float* k_cache, float* v_cache);
+
 #ifdef __cplusplus
 }
 #endif

@@ -17,6 +17,7 @@ from work_llm_accelerator_amd.abi import F32P, SIGNATURES, U8P, c_int
 ROOT = Path(__file__).resolve().parents[1]
 ORACLE_LIB = ROOT / "oracle" / "build" / "libqwen_oracle.so"
 REF_DECODE_LIB = ROOT / "oracle" / "_ref" / "libqwen_decode_ref.so"
+REF_PREFILL_L0_LIB = ROOT / "oracle" / "_ref" / "libqwen_prefill_layer0_ref.so"
 
 _oracle = None
 
@@ -29,7 +30,7 @@ def oracle() -> ctypes.CDLL:
         subprocess.run(["make", "-C", str(ROOT / "oracle"), "oracle"], check=True, capture_output=True)
     lib = ctypes.CDLL(str(ORACLE_LIB))
     for name, argtypes in SIGNATURES.items():
-        if "dispatch" in name:
+        if "dispatch" in name or "layer0" in name:  # layer-0 wrappers: pinned by the compiled reference
             continue
         fn = getattr(lib, "oracle_" + name.removeprefix("qwen_"))
         fn.argtypes = argtypes
@@ -66,6 +67,18 @@ def oracle() -> ctypes.CDLL:
     lib.oracle_argmax.argtypes = [F32A, c_int, c_int, I32P]
     lib.oracle_argmax.restype = None
     _oracle = lib
+    return lib
+
+
+def ref_prefill_layer0() -> ctypes.CDLL | None:
+    """The reference's unquantized prefill layer-0 wrapper built from its own source, or None."""
+    if not REF_PREFILL_L0_LIB.exists():
+        return None
+    lib = ctypes.CDLL(str(REF_PREFILL_L0_LIB))
+    for name in ("qwen_prefill_layer0_reference_forward", "qwen_prefill_layer0_reference_forward_with_cache"):
+        fn = getattr(lib, name)
+        fn.argtypes = SIGNATURES[name]
+        fn.restype = c_int
     return lib
 
 

@@ -48,6 +48,12 @@ SIGNATURES: dict[str, list] = {
     + [U8P, F32P, F32P, F32P] + _SRAM,
     "qwen_decode_dispatch_layers_forward": [c_void_p, c_int, U8P, F32P, F32P, F32P] + _SRAM + [c_void_p],
     "qwen_prefill_dispatch_layers_forward": [c_void_p, c_int, U8P, F32P, F32P, F32P] + _SRAM + [c_void_p],
+    # unquantized layer-0 reference wrappers: 16 weight / bias pointers (biases may be None)
+    "qwen_decode_layer0_reference_forward": [F32P, c_int, c_void_p, c_void_p] + [c_void_p] * 16
+    + [ctypes.c_float, F32P, F32P, F32P],
+    "qwen_prefill_layer0_reference_forward": [F32P, c_int] + [c_void_p] * 16 + [ctypes.c_float, F32P],
+    "qwen_prefill_layer0_reference_forward_with_cache": [F32P, c_int] + [c_void_p] * 16
+    + [ctypes.c_float, F32P, c_void_p, c_void_p],
 }
 
 # Additive entry points of this build (no counterpart in the reference): the device-resident

@@ -5,6 +5,7 @@
 // exactly the spans the reference writes.
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -13,7 +14,9 @@
 #include <string>
 #include <vector>
 
+#include "kernels.hpp"
 #include "qwen_decode_host_wrapper.h"
+#include "qwen_device_math.hpp"
 #include "qwen_prefill_host_wrapper.h"
 #include "runtime.hpp"
 
@@ -470,6 +473,172 @@ int qwen_prefill_dispatch_layers_forward(const qwen_prefill_descriptor* dsc, int
   }
   if (completed) *completed = n;
   return QWEN_OK;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Unquantized layer-0 reference wrappers (qwen_decode_layer0_reference_wrapper.cpp:75-209,
+// qwen_prefill_layer0_reference_wrapper.cpp:60-347): fp32 weights, double accumulation, HF
+// head-major caches [kv_head][T][128].  Biases may be null (no bias).
+// ---------------------------------------------------------------------------------------------
+}  // extern "C"
+
+namespace {
+
+struct HostL0 {
+  const float *ln, *qw, *qb, *kw, *kb, *vw, *vb, *ow, *ob, *post_ln, *gw, *gb, *uw, *ub, *dw, *db;
+  bool weights_present() const { return !any_null({ln, qw, kw, vw, ow, post_ln, gw, uw, dw}); }
+};
+
+size_t l0_weight_floats() {
+  return (size_t)QWEN_HIDDEN * (2 * QWEN_HIDDEN + 2 * QWEN_KV_WIDTH + 3 * QWEN_INTERMEDIATE) +
+         (size_t)(5 * QWEN_HIDDEN + 2 * QWEN_KV_WIDTH + 2 * QWEN_INTERMEDIATE);
+}
+
+Layer0Weights stage_l0(Arena& A, const HostL0& h, hipStream_t st) {
+  auto opt = [&](const float* p, size_t n) -> const float* { return p ? stage_in(A, p, n, st) : nullptr; };
+  const size_t H = QWEN_HIDDEN, KV = QWEN_KV_WIDTH, I = QWEN_INTERMEDIATE;
+  Layer0Weights w;
+  w.ln = stage_in(A, h.ln, H, st);
+  w.qw = stage_in(A, h.qw, H * H, st);
+  w.qb = opt(h.qb, H);
+  w.kw = stage_in(A, h.kw, KV * H, st);
+  w.kb = opt(h.kb, KV);
+  w.vw = stage_in(A, h.vw, KV * H, st);
+  w.vb = opt(h.vb, KV);
+  w.ow = stage_in(A, h.ow, H * H, st);
+  w.ob = opt(h.ob, H);
+  w.post_ln = stage_in(A, h.post_ln, H, st);
+  w.gw = stage_in(A, h.gw, I * H, st);
+  w.gb = opt(h.gb, I);
+  w.uw = stage_in(A, h.uw, I * H, st);
+  w.ub = opt(h.ub, I);
+  w.dw = stage_in(A, h.dw, H * I, st);
+  w.db = opt(h.db, H);
+  return w;
+}
+
+// RoPE rows of the layer-0 wrappers: angle = position * pow(1e6, -2p/128) in double with the host libm
+// (decode_layer0 :113-116,51-63; prefill_layer0 :107-109,125-160); prefill rounds cos/sin to bf16.
+std::vector<float> l0_rope_rows(int first, int count, bool prefill) {
+  std::vector<double> inv_freq(QWEN_HEAD_DIM / 2);
+  for (int i = 0; i < QWEN_HEAD_DIM / 2; ++i)
+    inv_freq[i] = std::pow(1000000.0, -2.0 * static_cast<double>(i) / static_cast<double>(QWEN_HEAD_DIM));
+  std::vector<float> tab((size_t)count * 128);
+  for (int r = 0; r < count; ++r)
+    for (int p = 0; p < QWEN_HEAD_DIM / 2; ++p) {
+      const double angle = static_cast<double>(first + r) * inv_freq[p];
+      float c = static_cast<float>(std::cos(angle));
+      float s = static_cast<float>(std::sin(angle));
+      if (prefill) {
+        c = round_bf16(c);
+        s = round_bf16(s);
+      }
+      tab[(size_t)r * 128 + p] = c;
+      tab[(size_t)r * 128 + 64 + p] = s;
+    }
+  return tab;
+}
+
+int prefill_layer0(const float* x, int S, const HostL0& h, float eps, float* out, float* k_cache, float* v_cache) {
+  if (!x || !out || S <= 0 || S > QWEN_MAX_SEQ) return QWEN_ERR_KERNEL;
+  if ((k_cache == nullptr) != (v_cache == nullptr)) return QWEN_ERR_KERNEL;
+  if (!h.weights_present()) return QWEN_ERR_KERNEL;
+  return guarded([&]() -> int {
+    const size_t kvn = (size_t)QWEN_KV_HEADS * S * QWEN_HEAD_DIM;
+    CallScope cs(l0_weight_floats() * 4 + 64 * 256 + layer0_workspace_bytes(S, 0, false) +
+                 ((size_t)S * (2 * QWEN_HIDDEN + 128) + 2 * kvn) * 4);
+    Arena& A = cs.A();
+    const hipStream_t st = cs.st();
+    const Layer0Weights w = stage_l0(A, h, st);
+    const float* x_d = stage_in(A, x, (size_t)S * QWEN_HIDDEN, st);
+    const std::vector<float> tab = l0_rope_rows(0, S, true);
+    const float* tab_d = stage_in(A, tab.data(), tab.size(), st);
+    float* out_d = A.alloc_n<float>((size_t)S * QWEN_HIDDEN);
+    float* k_d = k_cache ? A.alloc_n<float>(kvn) : nullptr;
+    float* v_d = k_cache ? A.alloc_n<float>(kvn) : nullptr;
+    void* ws = A.alloc(layer0_workspace_bytes(S, 0, false));
+    run_layer0_reference(w, eps, false, x_d, S, 0, tab_d, nullptr, nullptr, out_d, k_d, v_d, ws, st);
+    QWEN_HIP(hipGetLastError());
+    copy_out(out, out_d, (size_t)S * QWEN_HIDDEN, st);
+    if (k_cache) {
+      copy_out(k_cache, k_d, kvn, st);
+      copy_out(v_cache, v_d, kvn, st);
+    }
+    cs.sync();
+    return QWEN_OK;
+  });
+}
+
+}  // namespace
+
+extern "C" {
+
+int qwen_decode_layer0_reference_forward(const float* input_token, int past_seq_len, const float* past_k_cache,
+                                         const float* past_v_cache, const float* input_layernorm_weight,
+                                         const float* q_weight, const float* q_bias, const float* k_weight,
+                                         const float* k_bias, const float* v_weight, const float* v_bias,
+                                         const float* o_weight, const float* o_bias,
+                                         const float* post_attention_layernorm_weight, const float* gate_weight,
+                                         const float* gate_bias, const float* up_weight, const float* up_bias,
+                                         const float* down_weight, const float* down_bias, float rms_eps,
+                                         float* output_token, float* next_k_cache, float* next_v_cache) {
+  // qwen_decode_layer0_reference_wrapper.cpp:99-101
+  if (!input_token || !output_token || !next_k_cache || !next_v_cache || past_seq_len < 0) return QWEN_ERR_KERNEL;
+  const HostL0 h{input_layernorm_weight, q_weight, q_bias, k_weight, k_bias, v_weight, v_bias, o_weight, o_bias,
+                 post_attention_layernorm_weight, gate_weight, gate_bias, up_weight, up_bias, down_weight, down_bias};
+  if (!h.weights_present() || past_seq_len > QWEN_MAX_SEQ - 1 ||
+      (past_seq_len > 0 && (!past_k_cache || !past_v_cache)))
+    return QWEN_ERR_KERNEL;
+  return guarded([&]() -> int {
+    const int past = past_seq_len;
+    const size_t past_n = (size_t)QWEN_KV_HEADS * past * QWEN_HEAD_DIM;
+    const size_t next_n = (size_t)QWEN_KV_HEADS * (past + 1) * QWEN_HEAD_DIM;
+    CallScope cs(l0_weight_floats() * 4 + 64 * 256 + layer0_workspace_bytes(1, past, true) +
+                 (2 * QWEN_HIDDEN + 128 + 2 * past_n + 2 * next_n) * 4);
+    Arena& A = cs.A();
+    const hipStream_t st = cs.st();
+    const Layer0Weights w = stage_l0(A, h, st);
+    const float* x_d = stage_in(A, input_token, QWEN_HIDDEN, st);
+    const std::vector<float> tab = l0_rope_rows(past, 1, false);
+    const float* tab_d = stage_in(A, tab.data(), tab.size(), st);
+    const float* pk_d = stage_in(A, past_k_cache, past_n, st);
+    const float* pv_d = stage_in(A, past_v_cache, past_n, st);
+    float* out_d = A.alloc_n<float>(QWEN_HIDDEN);
+    float* k_d = A.alloc_n<float>(next_n);
+    float* v_d = A.alloc_n<float>(next_n);
+    void* ws = A.alloc(layer0_workspace_bytes(1, past, true));
+    run_layer0_reference(w, rms_eps, true, x_d, 1, past, tab_d, pk_d, pv_d, out_d, k_d, v_d, ws, st);
+    QWEN_HIP(hipGetLastError());
+    copy_out(output_token, out_d, QWEN_HIDDEN, st);
+    copy_out(next_k_cache, k_d, next_n, st);
+    copy_out(next_v_cache, v_d, next_n, st);
+    cs.sync();
+    return QWEN_OK;
+  });
+}
+
+int qwen_prefill_layer0_reference_forward(const float* input_sequence, int seq_len,
+                                          const float* input_layernorm_weight, const float* q_weight,
+                                          const float* q_bias, const float* k_weight, const float* k_bias,
+                                          const float* v_weight, const float* v_bias, const float* o_weight,
+                                          const float* o_bias, const float* post_attention_layernorm_weight,
+                                          const float* gate_weight, const float* gate_bias, const float* up_weight,
+                                          const float* up_bias, const float* down_weight, const float* down_bias,
+                                          float rms_eps, float* output_sequence) {
+  const HostL0 h{input_layernorm_weight, q_weight, q_bias, k_weight, k_bias, v_weight, v_bias, o_weight, o_bias,
+                 post_attention_layernorm_weight, gate_weight, gate_bias, up_weight, up_bias, down_weight, down_bias};
+  return prefill_layer0(input_sequence, seq_len, h, rms_eps, output_sequence, nullptr, nullptr);
+}
+
+int qwen_prefill_layer0_reference_forward_with_cache(
+    const float* input_sequence, int seq_len, const float* input_layernorm_weight, const float* q_weight,
+    const float* q_bias, const float* k_weight, const float* k_bias, const float* v_weight, const float* v_bias,
+    const float* o_weight, const float* o_bias, const float* post_attention_layernorm_weight, const float* gate_weight,
+    const float* gate_bias, const float* up_weight, const float* up_bias, const float* down_weight,
+    const float* down_bias, float rms_eps, float* output_sequence, float* k_cache, float* v_cache) {
+  const HostL0 h{input_layernorm_weight, q_weight, q_bias, k_weight, k_bias, v_weight, v_bias, o_weight, o_bias,
+                 post_attention_layernorm_weight, gate_weight, gate_bias, up_weight, up_bias, down_weight, down_bias};
+  return prefill_layer0(input_sequence, seq_len, h, rms_eps, output_sequence, k_cache, v_cache);
 }
 
 }  // extern "C"

@@ -122,6 +122,22 @@ void launch_kv_synthetic(float* cache, uint64_t rows, uint64_t stream, hipStream
 void launch_embed(const uint16_t* table, int vocab, const int* ids, int count, float* hidden, hipStream_t st);
 void launch_eval_expf(uint32_t first, uint32_t stride, uint64_t n, float* y, hipStream_t st);
 
+// ---- unquantized layer-0 reference path: kernels_layer0.hip ----
+// fp32 weights [out][in] row-major (biases optional), device pointers.
+struct Layer0Weights {
+  const float *ln, *qw, *qb, *kw, *kb, *vw, *vb, *ow, *ob, *post_ln, *gw, *gb, *uw, *ub, *dw, *db;
+};
+// Tokens whose attention probabilities are held at once (bounded workspace), of T queries over at
+// most nmax keys.
+int layer0_attention_chunk(int T, int nmax);
+size_t layer0_workspace_bytes(int T, int past, bool decode);
+// decode: T = 1 token at position `past`, past_k/past_v head-major [2][past][128], k_out/v_out
+// head-major [2][past+1][128].  prefill: T tokens at positions 0..T-1, k_out/v_out (optional)
+// head-major [2][T][128].  rope_tab: [T][cos 64 | sin 64] from the host libm (prefill: bf16-rounded).
+void run_layer0_reference(const Layer0Weights& W, float eps, bool decode, const float* x, int T, int past,
+                          const float* rope_tab, const float* past_k, const float* past_v, float* out, float* k_out,
+                          float* v_out, void* workspace, hipStream_t st);
+
 // ---- model head: kernels_head.hip ----
 // Final RMSNorm (bf16 weight norm_w[1536]) of `count` hidden rows, tied bf16 lm_head over
 // table[vocab][1536] (vocab a multiple of 128), bf16-rounded logits [count][vocab] (when logits is
