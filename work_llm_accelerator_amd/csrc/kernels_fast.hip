@@ -1154,6 +1154,134 @@ __global__ void __launch_bounds__(256) reduce_norm_quant_kernel(GemmArgs a, int 
                     a.sums_out + 2 * tok, nullptr);
 }
 
+// kFuseNormQuant for 1536-wide rows, one wave per token row: the arithmetic of
+// reduce_norm_quant_kernel with wave reductions in place of block reductions, and every load of the
+// row (split partials, scales, residual or bias, norm weights) issued before the first use, so a
+// row costs one memory round trip.  Lane l owns float4 columns l + 64 j, j < 6.
+// grid = tokens, block = 64 (one wave per row, spread over as many CUs as rows).
+template <int EPI>
+__global__ void __launch_bounds__(64) reduce_norm_quant_wave_kernel(GemmArgs a, int splits) {
+  constexpr int NV = QWEN_HIDDEN / 256;
+  const int lane = threadIdx.x & 63;
+  const int tok = blockIdx.x;
+  const size_t zstride = (size_t)a.tokens * QWEN_HIDDEN;
+  const float4* pt = reinterpret_cast<const float4*>(a.part + (size_t)tok * QWEN_HIDDEN) + lane;
+  const float4* sw4 = reinterpret_cast<const float4*>(a.sw) + lane;
+  const float4* w4 = reinterpret_cast<const float4*>(a.norm_w) + lane;
+  const float4* r4 = EPI == kEpiResidual ? reinterpret_cast<const float4*>(a.resid + (size_t)tok * a.resid_stride) + lane
+                                         : reinterpret_cast<const float4*>(a.bias) + lane;
+  const bool has_add = EPI == kEpiResidual || a.bias != nullptr;
+  const bool has_w = a.norm != kNormNone;
+  float4 acc[NV], sw[NV], ad[NV], wn[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    sw[j] = sw4[64 * j];
+    ad[j] = has_add ? r4[64 * j] : make_float4(0, 0, 0, 0);
+    wn[j] = has_w ? w4[64 * j] : make_float4(0, 0, 0, 0);
+  }
+  // split sums in z order, 4 splits per batch of loads
+#pragma unroll
+  for (int j = 0; j < NV; ++j) acc[j] = make_float4(0, 0, 0, 0);
+  for (int z0 = 0; z0 < splits; z0 += 4) {
+    float4 pz[4][NV];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int j = 0; j < NV; ++j)
+        pz[u][j] = z0 + u < splits ? pt[(size_t)(z0 + u) * (zstride / 4) + 64 * j] : make_float4(0, 0, 0, 0);
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (z0 + u < splits)
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+          acc[j].x += pz[u][j].x;
+          acc[j].y += pz[u][j].y;
+          acc[j].z += pz[u][j].z;
+          acc[j].w += pz[u][j].w;
+        }
+  }
+  const double corr = -8.0 * (256.0 * (double)a.sums[2 * tok] + (double)a.sums[2 * tok + 1]) * (double)a.sx[tok];
+  float4 v[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int row0 = 4 * (lane + 64 * j);
+    const float s4[4] = {sw[j].x, sw[j].y, sw[j].z, sw[j].w};
+    const float p4[4] = {acc[j].x, acc[j].y, acc[j].z, acc[j].w};
+    const float d4[4] = {ad[j].x, ad[j].y, ad[j].z, ad[j].w};
+    float out[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float val = p4[q] + (float)(corr * (double)s4[q]);
+      out[q] = EPI == kEpiResidual ? d4[q] + val : val + d4[q];
+    }
+    if (EPI == kEpiResidual && a.y_raw)
+      *reinterpret_cast<float4*>(a.y_raw + (size_t)tok * a.y_stride + row0) = make_float4(out[0], out[1], out[2], out[3]);
+    if (EPI == kEpiResidual && a.round_bf16)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) out[q] = round_bf16(out[q]);
+    v[j] = make_float4(out[0], out[1], out[2], out[3]);
+    *reinterpret_cast<float4*>(a.y + (size_t)tok * a.y_stride + row0) = v[j];
+  }
+  // RMSNorm (norm_quant_row's arithmetic, wave reductions)
+  if (a.norm == kNormDecode) {
+    double ss = 0.0;
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+      ss += (double)v[j].x * v[j].x + (double)v[j].y * v[j].y + (double)v[j].z * v[j].z + (double)v[j].w * v[j].w;
+    ss = wave_sum_d(ss);
+    const double inv = 1.0 / sqrt(ss / (double)QWEN_HIDDEN + (double)QWEN_RMS_EPS);
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+      v[j] = make_float4((float)((double)v[j].x * inv * wn[j].x), (float)((double)v[j].y * inv * wn[j].y),
+                         (float)((double)v[j].z * inv * wn[j].z), (float)((double)v[j].w * inv * wn[j].w));
+  } else if (a.norm == kNormPrefill) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
+    ss = wave_sum(ss);
+    const float inv = 1.0f / approx_sqrt(ss / (float)QWEN_HIDDEN + QWEN_RMS_EPS);
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+      v[j] = make_float4(v[j].x * inv * wn[j].x, v[j].y * inv * wn[j].y, v[j].z * inv * wn[j].z, v[j].w * inv * wn[j].w);
+  }
+  // two-limb quantization (norm_quant_row's code)
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j)
+    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
+  amax = wave_max(amax);
+  const float qinv = amax > 0.0f ? (float)kQuantMax / amax : 0.0f;
+  int8_t* row = a.xq_out + (size_t)tok * (2 * QWEN_HIDDEN);
+  int sh = 0, sl = 0;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int k = lane + 64 * j;
+    const float e[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+    uint32_t hw = 0, lw = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float xf = fminf(fmaxf(rintf(e[q] * qinv), -(float)kQuantMax), (float)kQuantMax);
+      const int X = (int)xf;
+      const int H = (X + 128) >> 8;
+      const int L = X - (H << 8);
+      hw |= (uint32_t)(H & 0xFF) << (8 * q);
+      lw |= (uint32_t)(L & 0xFF) << (8 * q);
+      sh += H;
+      sl += L;
+    }
+    const int base = ((4 * k) >> 7) * 256 + ((4 * k) & 127);
+    *reinterpret_cast<uint32_t*>(row + base) = hw;
+    *reinterpret_cast<uint32_t*>(row + base + 128) = lw;
+  }
+  sh = wave_sum_i(sh);
+  sl = wave_sum_i(sl);
+  if (lane == 0) {
+    a.sx_out[tok] = amax > 0.0f ? amax / (float)kQuantMax : 1.0f;
+    a.sums_out[2 * tok] = sh;
+    a.sums_out[2 * tok + 1] = sl;
+  }
+}
+
 // ---------------------------------------------------------------------------------------------
 // RoPE of q (in place) and k, plus the K/V cache append, for rows of a fused [q | k | v] buffer
 // (qkv_stride floats per token).  Decode: token b is sequence b at position pos[b].  Prefill:
@@ -1732,7 +1860,10 @@ static void launch_reduce(const GemmArgs& a, int splits, hipStream_t st) {
   if (a.fuse == kFuseQkvRope) {
     hipLaunchKernelGGL(reduce_qkv_rope_kernel, dim3(a.tokens), dim3(256), 0, st, a, splits);
   } else if (a.fuse == kFuseNormQuant) {
-    hipLaunchKernelGGL((reduce_norm_quant_kernel<EPI>), dim3(a.tokens), dim3(256), 0, st, a, splits);
+    if (a.out_dim == QWEN_HIDDEN)
+      hipLaunchKernelGGL((reduce_norm_quant_wave_kernel<EPI>), dim3(a.tokens), dim3(64), 0, st, a, splits);
+    else
+      hipLaunchKernelGGL((reduce_norm_quant_kernel<EPI>), dim3(a.tokens), dim3(256), 0, st, a, splits);
   } else {
     const size_t quads = (size_t)a.tokens * (a.out_dim / 4);
     hipLaunchKernelGGL((gemm_splitk_reduce_kernel<EPI>), dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, st, a,
