@@ -50,9 +50,12 @@ __device__ __forceinline__ float load_agent(const float* p) {
 }
 
 // Prefill SiLU for the FAST GEMM epilogue: v / (1 + approx_exp(-v)) with approx_exp in its
-// division-free Horner form and a fast reciprocal division (a few ulp from silu_prefill, whose
-// reference form spends seven IEEE divisions per element).
-__device__ __forceinline__ float silu_prefill_fast(float v) { return __fdividef(v, 1.0f + approx_exp_fast(-v)); }
+// division-free Horner form and the division as v * rcp(1 + e) with the hardware reciprocal
+// (v_rcp_f32, 1 ulp): a few ulp from silu_prefill, whose reference form spends seven IEEE
+// divisions per element.
+__device__ __forceinline__ float silu_prefill_fast(float v) {
+  return v * __builtin_amdgcn_rcpf(1.0f + approx_exp_fast(-v));
+}
 
 // ---------------------------------------------------------------------------------------------
 // Weight repack.  Reference layout: W[o][i] is the nibble at byte (o*in + i)/2, low nibble for
@@ -565,6 +568,7 @@ __global__ void __launch_bounds__(256 * TW) gemm_i8_pipe_kernel(GemmArgs a) {
   static_assert(NBUF >= 3, "at least two chunks in flight");
   static_assert((RTW * D) % TW == 0, "weight tiles split evenly over the token groups");
   static_assert((NBUF - 2) * OPS < 64, "pipeline depth");
+  static_assert(D * RTW + 8 <= 15, "LDS reads in flight (weight tiles, token tiles n and n+1) fit lgkmcnt");
   // One LDS object per stage and operand: the compiler tracks direct-load writes per object, so
   // reads of one stage do not wait for loads still landing in the others.
   __shared__ __align__(16) uint8_t smem[NBUF * (XB + WB)];  // stage s: [XB activations][WB weights]
@@ -716,56 +720,79 @@ __global__ void __launch_bounds__(256 * TW) gemm_i8_pipe_kernel(GemmArgs a) {
   wait_vmcnt<0>();  // the trailing reloads land before the wave moves on
 
   const bool partial = gridDim.z > 1 || (!DUAL && a.fuse != kFuseNone);  // a reduce kernel finishes
+  // Epilogue operands.  Every load is issued before the first use, so the wave waits for memory
+  // once rather than once per (row tile, token tile); token columns past the last token read the
+  // last token's values and store nothing.
+  int tok[NT];
+  float sxv[NT];
+  int sh8[NT], sl8[NT];
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+    tok[n] = tok0 + tw * 16 * NT + n * 16 + col;
+    const int tc = min(tok[n], a.tokens - 1);
+    sxv[n] = a.sx[tc];
+    const int2 sm = *reinterpret_cast<const int2*>(a.sums + 2 * tc);
+    sh8[n] = 8 * sm.x;
+    sl8[n] = 8 * sm.y;
+  }
+  float sw[RTW][4], sw2[RTW][4], bias[RTW][4];
+#pragma unroll
+  for (int r = 0; r < RTW; ++r) {
+    const int row0 = min(rt0 + r, row_tiles - 1) * 16 + 4 * g;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      sw[r][q] = a.sw[row0 + q];
+      sw2[r][q] = DUAL ? a.sw2[row0 + q] : 0.0f;
+      bias[r][q] = (EPI == kEpiStore && a.bias) ? a.bias[row0 + q] : 0.0f;
+    }
+  }
 #pragma unroll
   for (int r = 0; r < RTW; ++r) {
     if (!rt_ok[r]) continue;
     const int row0 = (rt0 + r) * 16 + 4 * g;
-    float sw[4], sw2[4], bias[4];
+    float4 res[NT];
+    if (EPI == kEpiResidual && !partial) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      sw[q] = a.sw[row0 + q];
-      sw2[q] = DUAL ? a.sw2[row0 + q] : 0.0f;
-      bias[q] = a.bias ? a.bias[row0 + q] : 0.0f;
+      for (int n = 0; n < NT; ++n)
+        res[n] = *reinterpret_cast<const float4*>(a.resid + (size_t)min(tok[n], a.tokens - 1) * a.resid_stride + row0);
     }
 #pragma unroll
     for (int n = 0; n < NT; ++n) {
-      const int tok = tok0 + tw * 16 * NT + n * 16 + col;
-      if (tok >= a.tokens) continue;
-      const float sx = a.sx[tok];
       float out[4];
       if (partial) {
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-          out[q] = ((float)accH[0][r][n][q] * 256.0f + (float)accL[0][r][n][q]) * sx * sw[q];
-        *reinterpret_cast<float4*>(a.part + ((size_t)blockIdx.z * a.tokens + tok) * a.out_dim + row0) =
-            make_float4(out[0], out[1], out[2], out[3]);
+          out[q] = ((float)accH[0][r][n][q] * 256.0f + (float)accL[0][r][n][q]) * sxv[n] * sw[r][q];
+        if (tok[n] < a.tokens)
+          *reinterpret_cast<float4*>(a.part + ((size_t)blockIdx.z * a.tokens + tok[n]) * a.out_dim + row0) =
+              make_float4(out[0], out[1], out[2], out[3]);
         continue;
       }
-      const int sh8 = 8 * a.sums[2 * tok];
-      const int sl8 = 8 * a.sums[2 * tok + 1];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         // fp32 dequantization: the int32 sums are exact; fp32 adds ~2^-24 relative, far inside the
         // FAST tolerance, at a quarter of the cost of the fp64 form
-        const float tot = (float)(accH[0][r][n][q] - sh8) * 256.0f + (float)(accL[0][r][n][q] - sl8);
-        const float v = tot * sx * sw[q];
+        const float tot = (float)(accH[0][r][n][q] - sh8[n]) * 256.0f + (float)(accL[0][r][n][q] - sl8[n]);
+        const float v = tot * sxv[n] * sw[r][q];
         if (EPI == kEpiSiluMul) {
-          const float tot2 = (float)(accH[D - 1][r][n][q] - sh8) * 256.0f + (float)(accL[D - 1][r][n][q] - sl8);
-          const float u = tot2 * sx * sw2[q];
+          const float tot2 = (float)(accH[D - 1][r][n][q] - sh8[n]) * 256.0f + (float)(accL[D - 1][r][n][q] - sl8[n]);
+          const float u = tot2 * sxv[n] * sw2[r][q];
           const float sg = a.prefill_silu ? silu_prefill_fast(v) : silu_decode(v);
           out[q] = sg * u;
         } else if (EPI == kEpiResidual) {
-          out[q] = a.resid[(size_t)tok * a.resid_stride + row0 + q] + v;
+          out[q] = (&res[n].x)[q] + v;
         } else {
-          out[q] = v + bias[q];
+          out[q] = v + bias[r][q];
         }
       }
+      if (tok[n] >= a.tokens) continue;
       if (EPI == kEpiResidual && a.y_raw)
-        *reinterpret_cast<float4*>(a.y_raw + (size_t)tok * a.y_stride + row0) = make_float4(out[0], out[1], out[2], out[3]);
+        *reinterpret_cast<float4*>(a.y_raw + (size_t)tok[n] * a.y_stride + row0) =
+            make_float4(out[0], out[1], out[2], out[3]);
       if (EPI == kEpiResidual && a.round_bf16)
 #pragma unroll
         for (int q = 0; q < 4; ++q) out[q] = round_bf16(out[q]);
-      *reinterpret_cast<float4*>(a.y + (size_t)tok * a.y_stride + row0) = make_float4(out[0], out[1], out[2], out[3]);
+      *reinterpret_cast<float4*>(a.y + (size_t)tok[n] * a.y_stride + row0) = make_float4(out[0], out[1], out[2], out[3]);
     }
   }
 }
@@ -1598,7 +1625,9 @@ __device__ __forceinline__ bf16x4 bf16_lo4(float4 x, bf16x4 h) {
 //   [0, 8K)   K hi: row r (key 32t + r) of 256 bytes; 16-byte segment s (dims 8s..8s+7) stored at
 //             position s ^ (r & 15)
 //   [8K, 16K) K lo, same layout
-//   [16K,24K) V^T hi: row d (dim) of 64 bytes; segment s (keys 8s..8s+7) at position s ^ ((d>>2)&3)
+//   [16K,24K) V^T hi: row d (dim) of 64 bytes; segment s holds keys 4s..4s+3 then 16+4s..16+4s+3
+//             (the 8 keys one lane of the P.V product needs, so it reads them with one 16-byte
+//             read) at position s ^ ((d>>2)&3)
 //   [24K,32K) V^T lo, same layout
 // Keys past S repeat key S-1 (masked by the attention).  The swizzles make the attention's LDS
 // reads of 16 rows at one column fall on distinct bank groups.  grid = (ntile, 2, nseq), block = 256.
@@ -1628,20 +1657,25 @@ __global__ void __launch_bounds__(256) kv_bf16_tiles_kernel(const float* __restr
           bf16x8{l0[0], l0[1], l0[2], l0[3], l1[0], l1[1], l1[2], l1[3]};
     }
   }
-  {  // V^T: thread = (dim d, key half h)
-    const int d = threadIdx.x >> 1, h = threadIdx.x & 1;
+  {  // V^T: thread = (dim d, segment pair sp): segments 2sp and 2sp+1, i.e. keys 8sp..8sp+7 and
+     // 16+8sp..16+8sp+7
+    const int d = threadIdx.x >> 1, sp = threadIdx.x & 1;
     float x[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) x[i] = vb[(size_t)min(t * kPfKeys + 16 * h + i, S - 1) * QWEN_KV_WIDTH + d];
+    for (int i = 0; i < 8; ++i) {
+      x[i] = vb[(size_t)min(t * kPfKeys + 8 * sp + i, S - 1) * QWEN_KV_WIDTH + d];
+      x[8 + i] = vb[(size_t)min(t * kPfKeys + 16 + 8 * sp + i, S - 1) * QWEN_KV_WIDTH + d];
+    }
 #pragma unroll
-    for (int sgi = 0; sgi < 2; ++sgi) {
+    for (int j = 0; j < 2; ++j) {
       bf16x8 vh, vl;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        vh[e] = (__bf16)x[8 * sgi + e];
-        vl[e] = (__bf16)(x[8 * sgi + e] - (float)vh[e]);
+        const float xv = x[(e < 4 ? 0 : 8) + 4 * j + (e & 3)];
+        vh[e] = (__bf16)xv;
+        vl[e] = (__bf16)(xv - (float)vh[e]);
       }
-      const int pos = ((2 * h + sgi) ^ ((d >> 2) & 3)) * 16;
+      const int pos = ((2 * sp + j) ^ ((d >> 2) & 3)) * 16;
       *reinterpret_cast<bf16x8*>(tile + 16384 + d * 64 + pos) = vh;
       *reinterpret_cast<bf16x8*>(tile + 24576 + d * 64 + pos) = vl;
     }
@@ -1793,15 +1827,9 @@ __global__ void __launch_bounds__(896) attn_prefill_tiles_kernel(const float* __
 #pragma unroll
     for (int n = 0; n < 8; ++n) {
       const int d = 16 * n + col;
-      const int sw = (d >> 2) & 3;
-      const int p0 = 16384 + d * 64 + (((g >> 1) ^ sw) << 4) + 8 * (g & 1);        // keys 4g..4g+3
-      const int p1 = 16384 + d * 64 + (((2 + (g >> 1)) ^ sw) << 4) + 8 * (g & 1);  // keys 16+4g..16+4g+3
-      const bf16x4 vh0 = *reinterpret_cast<const bf16x4*>(T + p0);
-      const bf16x4 vh1 = *reinterpret_cast<const bf16x4*>(T + p1);
-      const bf16x4 vl0 = *reinterpret_cast<const bf16x4*>(T + 8192 + p0);
-      const bf16x4 vl1 = *reinterpret_cast<const bf16x4*>(T + 8192 + p1);
-      const bf16x8 vh = bf16x8{vh0[0], vh0[1], vh0[2], vh0[3], vh1[0], vh1[1], vh1[2], vh1[3]};
-      const bf16x8 vl = bf16x8{vl0[0], vl0[1], vl0[2], vl0[3], vl1[0], vl1[1], vl1[2], vl1[3]};
+      const int pv = 16384 + d * 64 + ((g ^ ((d >> 2) & 3)) << 4);  // keys 4g..4g+3, 16+4g..16+4g+3
+      const bf16x8 vh = *reinterpret_cast<const bf16x8*>(T + pv);
+      const bf16x8 vl = *reinterpret_cast<const bf16x8*>(T + 8192 + pv);
       acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph, vh, acc[n], 0, 0, 0);
       acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pl, vh, acc[n], 0, 0, 0);
       acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph, vl, acc[n], 0, 0, 0);
