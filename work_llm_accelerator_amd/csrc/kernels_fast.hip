@@ -1627,10 +1627,13 @@ __device__ __forceinline__ bf16x4 bf16_lo4(float4 x, bf16x4 h) {
 //   [8K, 16K) K lo, same layout
 //   [16K,24K) V^T hi: row d (dim) of 64 bytes; segment s holds keys 4s..4s+3 then 16+4s..16+4s+3
 //             (the 8 keys one lane of the P.V product needs, so it reads them with one 16-byte
-//             read) at position s ^ ((d>>2)&3)
+//             read) at position s ^ ((d>>1)&3)
 //   [24K,32K) V^T lo, same layout
-// Keys past S repeat key S-1 (masked by the attention).  The swizzles make the attention's LDS
-// reads of 16 rows at one column fall on distinct bank groups.  grid = (ntile, 2, nseq), block = 256.
+// Keys past S repeat key S-1 (masked by the attention).  ds_read_b128 serves 8 consecutive lanes
+// at a time from 128 bytes of banks (measured on gfx950: a 2-way conflict in those 8 lanes halves
+// the read rate); the swizzles give the 8 lanes of every such group 8 distinct 16-byte bank groups
+// (K: rows 256 B apart, segment XOR row; V^T: rows 64 B apart, two rows per 128 B, segment XOR
+// (d>>1)&3).  grid = (ntile, 2, nseq), block = 256.
 // ---------------------------------------------------------------------------------------------
 constexpr int kPfTileBytes = 32768;
 
@@ -1675,7 +1678,7 @@ __global__ void __launch_bounds__(256) kv_bf16_tiles_kernel(const float* __restr
         vh[e] = (__bf16)xv;
         vl[e] = (__bf16)(xv - (float)vh[e]);
       }
-      const int pos = ((2 * sp + j) ^ ((d >> 2) & 3)) * 16;
+      const int pos = ((2 * sp + j) ^ ((d >> 1) & 3)) * 16;
       *reinterpret_cast<bf16x8*>(tile + 16384 + d * 64 + pos) = vh;
       *reinterpret_cast<bf16x8*>(tile + 24576 + d * 64 + pos) = vl;
     }
@@ -1827,7 +1830,7 @@ __global__ void __launch_bounds__(896) attn_prefill_tiles_kernel(const float* __
 #pragma unroll
     for (int n = 0; n < 8; ++n) {
       const int d = 16 * n + col;
-      const int pv = 16384 + d * 64 + ((g ^ ((d >> 2) & 3)) << 4);  // keys 4g..4g+3, 16+4g..16+4g+3
+      const int pv = 16384 + d * 64 + ((g ^ ((d >> 1) & 3)) << 4);  // keys 4g..4g+3, 16+4g..16+4g+3
       const bf16x8 vh = *reinterpret_cast<const bf16x8*>(T + pv);
       const bf16x8 vl = *reinterpret_cast<const bf16x8*>(T + 8192 + pv);
       acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph, vh, acc[n], 0, 0, 0);
