@@ -1771,6 +1771,7 @@ __global__ void __launch_bounds__(896) attn_prefill_tiles_kernel(const float* __
     }
   }
   const int qpos = past + q0 + 16 * half + col;  // position of this lane's query column
+  const int qpos0 = past + q0 + 16 * half;       // the wave's first query position
   float m_run = -INFINITY, l_run = 0.0f;
   v4f acc[8];
 #pragma unroll
@@ -1793,15 +1794,21 @@ __global__ void __launch_bounds__(896) attn_prefill_tiles_kernel(const float* __
         sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, ql[m], sc[kt], 0, 0, 0);
       }
     }
+    // Only a tile that reaches past the wave's first query or past the last key needs the mask.
+    if (t * kPfKeys + kPfKeys - 1 > qpos0 || t * kPfKeys + kPfKeys > nkeys) {
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = t * kPfKeys + kt * 16 + 4 * g + r;
+          if (key > qpos || key >= nkeys) sc[kt][r] = -INFINITY;
+        }
+    }
     float mt = -INFINITY;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = t * kPfKeys + kt * 16 + 4 * g + r;
-        if (key > qpos || key >= nkeys) sc[kt][r] = -INFINITY;
-        mt = fmaxf(mt, sc[kt][r]);
-      }
+      for (int r = 0; r < 4; ++r) mt = fmaxf(mt, sc[kt][r]);
     mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
     // Tile 0 holds key 0 <= qpos, so m_run is finite from tile 0 on; a later tile with every key
     // past qpos gives mt = -inf, corr = 1 and p = 0, leaving the column's state unchanged.
@@ -1821,11 +1828,15 @@ __global__ void __launch_bounds__(896) attn_prefill_tiles_kernel(const float* __
       ph[e] = (__bf16)p[e];
       pl[e] = (__bf16)(p[e] - (float)ph[e]);
     }
+    // The running max of most columns is unchanged by most tiles: corr is then exactly 1 and the
+    // rescale is skipped unless some column of the wave needs it.
+    if (__ballot(corr != 1.0f) != 0) {
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const float cr = __shfl(corr, 4 * g + rr, 64);  // lane 4g + rr holds query column 4g + rr
+      for (int rr = 0; rr < 4; ++rr) {
+        const float cr = __shfl(corr, 4 * g + rr, 64);  // lane 4g + rr holds query column 4g + rr
 #pragma unroll
-      for (int n = 0; n < 8; ++n) acc[n][rr] *= cr;
+        for (int n = 0; n < 8; ++n) acc[n][rr] *= cr;
+      }
     }
 #pragma unroll
     for (int n = 0; n < 8; ++n) {
