@@ -519,7 +519,9 @@ __global__ void __launch_bounds__(256) gemm_i8_kernel(GemmArgs a) {
 // Pipelined many-token GEMM.  Both operands of every K chunk reach LDS through direct
 // global->LDS loads (global_load_lds_dwordx4, 16 bytes per lane, no VGPR round trip), NBUF
 // chunks deep, so one wave keeps NBUF-1 chunks in flight while the matrix cores consume the
-// oldest.  Per chunk and wave: NT loads of activation rows (the block's TOK rows are split over
+// oldest.  With NBUF = 2 a block's next chunk lands during its current one, and two blocks share
+// the CU (WPE = 2 caps a wave at 256 VGPRs, two waves per SIMD): each block's epilogue and load
+// waits then run beside the other block's MFMAs.  Per chunk and wave: NT loads of activation rows (the block's TOK rows are split over
 // the 4 waves, 4 rows of 256 bytes per load) and RTW*D loads of the wave's own weight tiles.
 // Activation rows are XOR-swizzled by 16-byte segment (LDS segment s holds global segment
 // s ^ (row & 15)), so the 16 lanes of a lane group read 16 token rows on 16 distinct bank groups.
@@ -558,14 +560,14 @@ __device__ __forceinline__ void reg_tie(v4i& r) { asm volatile("" : "+v"(r)); }
 
 constexpr int kRasterGroup = 8;  // token tiles per raster group of the pipelined GEMM
 
-template <int NT, int RTW, int NBUF, int EPI, bool DUAL, int TW>
-__global__ void __launch_bounds__(256 * TW) gemm_i8_pipe_kernel(GemmArgs a) {
+template <int NT, int RTW, int NBUF, int EPI, bool DUAL, int TW, int WPE = 1>
+__global__ void __launch_bounds__(256 * TW) __attribute__((amdgpu_waves_per_eu(WPE))) gemm_i8_pipe_kernel(GemmArgs a) {
   constexpr int D = DUAL ? 2 : 1;
   constexpr int TOK = 16 * NT * TW;        // tokens per block (TW token groups of 16*NT)
   constexpr int XB = TOK * 256;                 // activation bytes per stage
   constexpr int WB = 4 * RTW * D * 1024;        // weight bytes per stage (4 waves)
   constexpr int OPS = NT + RTW * D / TW;        // direct loads per chunk per wave
-  static_assert(NBUF >= 3, "at least two chunks in flight");
+  static_assert(NBUF >= 2, "at least one chunk in flight");
   static_assert((RTW * D) % TW == 0, "weight tiles split evenly over the token groups");
   static_assert((NBUF - 2) * OPS < 64, "pipeline depth");
   static_assert(D * RTW + 8 <= 15, "LDS reads in flight (weight tiles, token tiles n and n+1) fit lgkmcnt");
@@ -1913,12 +1915,12 @@ static void launch_reduce(const GemmArgs& a, int splits, hipStream_t st) {
   }
 }
 
-template <int NT, int RTW, int NBUF, int EPI, bool DUAL, int TW = 1>
+template <int NT, int RTW, int NBUF, int EPI, bool DUAL, int TW = 1, int WPE = 1>
 static void launch_gemm_pipe_t(const GemmArgs& a, int splits, hipStream_t st) {
   const int row_tiles = a.out_dim / 16;
   const int nblk = ((a.tokens + 16 * NT * TW - 1) / (16 * NT * TW)) * ((row_tiles + 4 * RTW - 1) / (4 * RTW));
   const dim3 grid(8 * ((nblk + 7) / 8), 1, splits);
-  hipLaunchKernelGGL((gemm_i8_pipe_kernel<NT, RTW, NBUF, EPI, DUAL, TW>), grid, dim3(256 * TW), 0, st, a);
+  hipLaunchKernelGGL((gemm_i8_pipe_kernel<NT, RTW, NBUF, EPI, DUAL, TW, WPE>), grid, dim3(256 * TW), 0, st, a);
   if (!DUAL && (splits > 1 || a.fuse != kFuseNone)) launch_reduce<EPI>(a, splits, st);
 }
 
@@ -1981,12 +1983,14 @@ static void launch_gemm_epi(const GemmArgs& a, hipStream_t st) {
     if (!DUAL && a.fuse != kFuseNone) launch_reduce<EPI>(a, 1, st);
     return;
   }
-  // Many tokens (prefill): 8-wave blocks of 128 tokens, two waves per SIMD, three LDS stages.
+  // Many tokens (prefill): 4-wave blocks of 64 tokens with two LDS stages (64 KiB), two blocks per
+  // CU.  Measured against one 8-wave block of 128 tokens with three stages (144 KiB) per CU at 16,384
+  // tokens: gate/up 0.94-0.98 -> 0.79 ms, down 0.38-0.40 -> 0.34 ms, QKV 111-118 -> 97-100 us.
   if (a.tokens > kSplitTokens && a.fuse == kFuseNone) {
     if constexpr (DUAL)
-      launch_gemm_pipe_t<4, 2, 3, EPI, DUAL, 2>(a, 1, st);
+      launch_gemm_pipe_t<4, 2, 2, EPI, DUAL, 1, 2>(a, 1, st);
     else
-      launch_gemm_pipe_t<4, 4, 3, EPI, DUAL, 2>(a, 1, st);
+      launch_gemm_pipe_t<4, 4, 2, EPI, DUAL, 1, 2>(a, 1, st);
     return;
   }
   if constexpr (DUAL) {
