@@ -296,7 +296,8 @@ def test_model_decode_fast_batched(torch, layers2, batch):
 def test_model_prefill_fast_mid(torch, layers2, S):
     """40 tokens: the 17..64-token GEMM path on prefill shapes; 150 tokens: the 65..256-token GEMM
     path and five causal 32-key tiles of the prefill attention (partial last tile); 300 tokens: the
-    8-wave many-token GEMM (two full 128-token tiles and a partial one) and ten key tiles."""
+    many-token GEMM (4-wave blocks: four full 64-token tiles and a partial one), ten key tiles and a
+    partial last 16-query attention block."""
     from work_llm_accelerator_amd.model import FLAG_NO_BF16_ROUND, MODE_FAST, DeviceModel, KvCache
 
     print(f"model prefill fast S={S}", flush=True)
@@ -311,5 +312,31 @@ def test_model_prefill_fast_mid(torch, layers2, S):
         ref, ks, vs = oracle_prefill(layers2[:1], x, S, rounding=False)
         assert rel_err(got, ref) <= FAST_TOL
         assert rel_err(cache.k[0, 0].cpu().numpy().reshape(-1), ks[0]) <= FAST_TOL
+    finally:
+        m1.close()
+
+
+def test_model_prefill_fast_many_seqs(torch, layers2):
+    """Three sequences of 200 tokens: 600 tokens per projection (the many-token GEMM, a partial last
+    64-token tile), three sequences in the attention grid, each with a partial last 16-query block
+    and a partial last key tile."""
+    from work_llm_accelerator_amd.model import FLAG_NO_BF16_ROUND, MODE_FAST, DeviceModel, KvCache
+
+    B, S = 3, 200
+    print(f"model prefill fast B={B} S={S}", flush=True)
+    xs = [round_bfloat16_array(random_hidden(777 + b, S)) for b in range(B)]
+    m1 = DeviceModel(1, layers2[0].weight_ddr, layers2[0].scale_ddr)
+    try:
+        cache = KvCache.allocate(1, B, S)
+        hidden = torch.from_numpy(np.stack(xs).reshape(B, S, HIDDEN)).cuda()
+        m1.prefill(MODE_FAST | FLAG_NO_BF16_ROUND, hidden, cache)
+        m1.synchronize()
+        got = hidden.cpu().numpy().reshape(B, -1)
+        for b in range(B):
+            ref, ks, vs = oracle_prefill(layers2[:1], xs[b], S, rounding=False)
+            assert rel_err(got[b], ref) <= FAST_TOL, (b, rel_err(got[b], ref))
+            gk = cache.k[0, b, :S].cpu().numpy().reshape(-1)
+            gv = cache.v[0, b, :S].cpu().numpy().reshape(-1)
+            assert rel_err(gk, ks[0]) <= FAST_TOL and rel_err(gv, vs[0]) <= FAST_TOL
     finally:
         m1.close()
