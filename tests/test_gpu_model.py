@@ -340,3 +340,25 @@ def test_model_prefill_fast_many_seqs(torch, layers2):
             assert rel_err(gk, ks[0]) <= FAST_TOL and rel_err(gv, vs[0]) <= FAST_TOL
     finally:
         m1.close()
+
+
+@pytest.mark.parametrize("past", [0, 37])
+def test_model_decode_o_reduce_in_gate_up(torch, layers2, model2, past):
+    """One sequence: the O projection's reduce step (residual, RMSNorm, quantization) runs in every
+    block of the gate/up projection instead of its own launch; both forms must give exactly the same
+    hidden row and K/V cache, over both layers with the driver's bf16 rounding, for two calls in a
+    row."""
+    from work_llm_accelerator_amd.model import FLAG_SEPARATE_REDUCE, MODE_FAST
+
+    print(f"model decode fast O reduce in gate/up past={past}", flush=True)
+    outs = []
+    for flag in (0, FLAG_SEPARATE_REDUCE):
+        cache, _, x = decode_setup(torch, 2, [past], 48, seed=61)
+        hidden = torch.from_numpy(x).cuda()
+        pos = torch.tensor([past], dtype=torch.int32, device="cuda")
+        for _ in range(2):
+            model2.decode(MODE_FAST | flag, hidden, pos, past + 1, cache)
+        model2.synchronize()
+        outs.append((hidden.cpu().numpy(), cache.k.cpu().numpy(), cache.v.cpu().numpy()))
+    for a, b in zip(outs[0], outs[1]):
+        assert bits_equal(a.reshape(-1), b.reshape(-1)), first_mismatch(a.reshape(-1), b.reshape(-1))

@@ -813,10 +813,19 @@ __global__ void __launch_bounds__(256 * TW) __attribute__((amdgpu_waves_per_eu(W
 // wave w holds rows p and p + 64 of head rg, p = 16w + 4g + q).
 // grid = 8 * tt_count * ceil(groups / 8) blocks of 256, groups = row groups x splits.
 // ---------------------------------------------------------------------------------------------
-template <int RTW, bool DUAL, int EPI, int NKC, bool ROPE, int KSW>
-__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(3)))
-gemm_skinny_kernel(GemmArgs a, int tt_count, int rg_count, int splits) {
+template <int EPI>
+__device__ __forceinline__ void reduce_norm_quant_row(const GemmArgs& a, int splits, int tok, int8_t* xq_row,
+                                                      int chunk_stride, float* sx_out, int* sums_out, bool write_y);
+
+// PRE (one token, KSW = 1): the activation slice is not loaded but made by the block: wave 0 redoes
+// the reduce step of the previous projection (`pre`, pre_splits K splits, kFuseNormQuant on a
+// 1536-wide row) for token 0 straight into the slice, once the block's weight loads are in flight;
+// block 0 alone writes the finished row (pre.y).  K chunk c of the slice is the token's row c.
+template <int RTW, bool DUAL, int EPI, int NKC, bool ROPE, int KSW, bool PRE>
+__device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count, int rg_count, int splits,
+                                                 const GemmArgs& pre, int pre_splits) {
   constexpr int D = DUAL ? 2 : 1;
+  static_assert(!PRE || (KSW == 1 && NKC * kKChunk == QWEN_HIDDEN), "PRE: one K group over a 1536-wide row");
   constexpr int KC = NKC / KSW;  // K chunks per wave group
   static_assert(NKC % KSW == 0, "K chunks split evenly over the wave groups");
   static_assert(RTW * D * 8 * 1024 <= NKC * 16 * 256 || KSW == 1, "K-group reduction fits the slice buffer");
@@ -840,7 +849,7 @@ gemm_skinny_kernel(GemmArgs a, int tt_count, int rg_count, int splits) {
   const size_t row_stride_x = (size_t)a.in_dim * 2u;
 
   // activation slice -> LDS: chunk c, rows 4q..4q+3 per load (1 KiB), wave w takes chunks w, w+4KSW, ..
-  for (int c = threadIdx.x >> 6; c < NKC; c += 4 * KSW) {
+  for (int c = threadIdx.x >> 6; c < (PRE ? 0 : NKC); c += 4 * KSW) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int row = 4 * q + (lane >> 4);
@@ -871,6 +880,14 @@ gemm_skinny_kernel(GemmArgs a, int tt_count, int rg_count, int splits) {
     }
   }
   __builtin_amdgcn_sched_barrier(0);  // every load above is in flight before any use (one round trip)
+  __shared__ float pre_sx;
+  __shared__ int pre_sums[2];
+  if constexpr (PRE) {
+    // token 0's row of the slice: K chunk c at xs + c * 16 * 256 (row 0 of the chunk, unswizzled)
+    if (threadIdx.x < 64)
+      reduce_norm_quant_row<kEpiStore>(pre, pre_splits, 0, reinterpret_cast<int8_t*>(xs), 16 * 256, &pre_sx, pre_sums,
+                                       blockIdx.x == 0);
+  }
   wait_vmcnt<0>();
   __syncthreads();
 
@@ -938,7 +955,7 @@ gemm_skinny_kernel(GemmArgs a, int tt_count, int rg_count, int splits) {
   // epilogue: lane holds rows 16*rt + 4g + q (q < 4) of token tok0 + col
   const int tok = tok0 + col;
   if (tok >= a.tokens) return;
-  const double sx = (double)a.sx[tok];
+  const double sx = (double)(PRE ? pre_sx : a.sx[tok]);
   const bool partial = splits > 1 || (!DUAL && !ROPE && a.fuse != kFuseNone);
   if (partial) {
 #pragma unroll
@@ -954,8 +971,8 @@ gemm_skinny_kernel(GemmArgs a, int tt_count, int rg_count, int splits) {
     }
     return;
   }
-  const int sh8 = 8 * a.sums[2 * tok];
-  const int sl8 = 8 * a.sums[2 * tok + 1];
+  const int sh8 = 8 * (PRE ? pre_sums[0] : a.sums[2 * tok]);
+  const int sl8 = 8 * (PRE ? pre_sums[1] : a.sums[2 * tok + 1]);
   float y[RTW][4];
 #pragma unroll
   for (int r = 0; r < RTW; ++r) {
@@ -1021,6 +1038,18 @@ gemm_skinny_kernel(GemmArgs a, int tt_count, int rg_count, int splits) {
       *reinterpret_cast<float4*>(a.y + (size_t)tok * a.y_stride + row0) = make_float4(o[0], o[1], o[2], o[3]);
     }
   }
+}
+
+template <int RTW, bool DUAL, int EPI, int NKC, bool ROPE, int KSW>
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(3)))
+gemm_skinny_kernel(GemmArgs a, int tt_count, int rg_count, int splits) {
+  gemm_skinny_body<RTW, DUAL, EPI, NKC, ROPE, KSW, false>(a, tt_count, rg_count, splits, a, 0);
+}
+
+// One token, with the previous projection's reduce step redone by every block (see PRE above).
+template <int RTW, bool DUAL, int EPI, int NKC, bool ROPE>
+__global__ void __launch_bounds__(256) gemm_skinny_pre_kernel(GemmArgs a, int rg_count, GemmArgs pre, int pre_splits) {
+  gemm_skinny_body<RTW, DUAL, EPI, NKC, ROPE, 1, true>(a, 1, rg_count, 1, pre, pre_splits);
 }
 
 // Sum over z < splits of part[z * zstride + off .. + 3] in z order.  The loads of 8 splits are all
@@ -1186,13 +1215,15 @@ __global__ void __launch_bounds__(256) reduce_norm_quant_kernel(GemmArgs a, int 
 // kFuseNormQuant for 1536-wide rows, one wave per token row: the arithmetic of
 // reduce_norm_quant_kernel with wave reductions in place of block reductions, and every load of the
 // row (split partials, scales, residual or bias, norm weights) issued before the first use, so a
-// row costs one memory round trip.  Lane l owns float4 columns l + 64 j, j < 6.
-// grid = tokens, block = 64 (one wave per row, spread over as many CUs as rows).
+// row costs one memory round trip.  Lane l owns float4 columns l + 64 j, j < 6.  The two-limb code
+// goes to xq_row ([K chunk][limb][128 bytes], K chunk c at byte c * chunk_stride: a row of a.xq_out,
+// or a token row of a GEMM's LDS activation slice), the scale and limb sums to sx_out / sums_out;
+// the finished row goes to a.y (and a.y_raw) when write_y.
 template <int EPI>
-__global__ void __launch_bounds__(64) reduce_norm_quant_wave_kernel(GemmArgs a, int splits) {
+__device__ __forceinline__ void reduce_norm_quant_row(const GemmArgs& a, int splits, int tok, int8_t* xq_row,
+                                                      int chunk_stride, float* sx_out, int* sums_out, bool write_y) {
   constexpr int NV = QWEN_HIDDEN / 256;
   const int lane = threadIdx.x & 63;
-  const int tok = blockIdx.x;
   const size_t zstride = (size_t)a.tokens * QWEN_HIDDEN;
   const float4* pt = reinterpret_cast<const float4*>(a.part + (size_t)tok * QWEN_HIDDEN) + lane;
   const float4* sw4 = reinterpret_cast<const float4*>(a.sw) + lane;
@@ -1243,13 +1274,13 @@ __global__ void __launch_bounds__(64) reduce_norm_quant_wave_kernel(GemmArgs a, 
       const float val = p4[q] + (float)(corr * (double)s4[q]);
       out[q] = EPI == kEpiResidual ? d4[q] + val : val + d4[q];
     }
-    if (EPI == kEpiResidual && a.y_raw)
+    if (EPI == kEpiResidual && a.y_raw && write_y)
       *reinterpret_cast<float4*>(a.y_raw + (size_t)tok * a.y_stride + row0) = make_float4(out[0], out[1], out[2], out[3]);
     if (EPI == kEpiResidual && a.round_bf16)
 #pragma unroll
       for (int q = 0; q < 4; ++q) out[q] = round_bf16(out[q]);
     v[j] = make_float4(out[0], out[1], out[2], out[3]);
-    *reinterpret_cast<float4*>(a.y + (size_t)tok * a.y_stride + row0) = v[j];
+    if (write_y) *reinterpret_cast<float4*>(a.y + (size_t)tok * a.y_stride + row0) = v[j];
   }
   // RMSNorm (norm_quant_row's arithmetic, wave reductions)
   if (a.norm == kNormDecode) {
@@ -1280,7 +1311,7 @@ __global__ void __launch_bounds__(64) reduce_norm_quant_wave_kernel(GemmArgs a, 
     amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
   amax = wave_max(amax);
   const float qinv = amax > 0.0f ? (float)kQuantMax / amax : 0.0f;
-  int8_t* row = a.xq_out + (size_t)tok * (2 * QWEN_HIDDEN);
+  int8_t* row = xq_row;
   int sh = 0, sl = 0;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
@@ -1298,17 +1329,25 @@ __global__ void __launch_bounds__(64) reduce_norm_quant_wave_kernel(GemmArgs a, 
       sh += H;
       sl += L;
     }
-    const int base = ((4 * k) >> 7) * 256 + ((4 * k) & 127);
+    const int base = ((4 * k) >> 7) * chunk_stride + ((4 * k) & 127);
     *reinterpret_cast<uint32_t*>(row + base) = hw;
     *reinterpret_cast<uint32_t*>(row + base + 128) = lw;
   }
   sh = wave_sum_i(sh);
   sl = wave_sum_i(sl);
   if (lane == 0) {
-    a.sx_out[tok] = amax > 0.0f ? amax / (float)kQuantMax : 1.0f;
-    a.sums_out[2 * tok] = sh;
-    a.sums_out[2 * tok + 1] = sl;
+    *sx_out = amax > 0.0f ? amax / (float)kQuantMax : 1.0f;
+    sums_out[0] = sh;
+    sums_out[1] = sl;
   }
+}
+
+// grid = tokens, block = 64 (one wave per row, spread over as many CUs as rows).
+template <int EPI>
+__global__ void __launch_bounds__(64) reduce_norm_quant_wave_kernel(GemmArgs a, int splits) {
+  const int tok = blockIdx.x;
+  reduce_norm_quant_row<EPI>(a, splits, tok, a.xq_out + (size_t)tok * (2 * QWEN_HIDDEN), 256, a.sx_out + tok,
+                             a.sums_out + 2 * tok, true);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1946,7 +1985,8 @@ static bool launch_skinny(const GemmArgs& a, hipStream_t st) {
     }
     if (!DUAL && a.fuse != kFuseNone && !a.part) return false;
     launch_skinny_t<1, DUAL, EPI, 12, false>(a, row_tiles / 4, 1, st);
-    if (!DUAL && a.fuse != kFuseNone) launch_reduce<EPI>(a, 1, st);
+    if (!DUAL && a.fuse != kFuseNone && !(a.defer_reduce && a.tokens == 1 && a.fuse == kFuseNormQuant))
+      launch_reduce<EPI>(a, 1, st);
     return true;
   }
   if constexpr (!DUAL) {
@@ -2008,6 +2048,16 @@ static void launch_gemm_epi(const GemmArgs& a, hipStream_t st) {
       launch_gemm_pipe_t<4, 4, 4, EPI, DUAL>(a, splits, st);
     }
   }
+}
+
+bool launch_gemm_i8_pre(const GemmArgs& a, const GemmArgs& pre, int pre_splits, hipStream_t st) {
+  if (a.tokens != 1 || a.in_dim != QWEN_HIDDEN || !a.wp2 || a.out_dim % 64 != 0 || pre.out_dim != QWEN_HIDDEN ||
+      pre.fuse != kFuseNormQuant || pre.tokens != 1 || pre_splits < 1)
+    return false;
+  const int rg_count = a.out_dim / 64;
+  hipLaunchKernelGGL((gemm_skinny_pre_kernel<1, true, kEpiSiluMul, 12, false>), dim3(8 * ((rg_count + 7) / 8)),
+                     dim3(256), 0, st, a, rg_count, pre, pre_splits);
+  return true;
 }
 
 void launch_gemm_i8(const GemmArgs& a, int epi, hipStream_t st) {

@@ -224,6 +224,13 @@ struct qwen_hip_model {
   void gemm(const Ws& w, int tokens, int in, int out, const uint8_t* wpm, const float* sw, const float* bias,
             float* y, size_t ys, int epi, const uint8_t* wp2 = nullptr, const float* sw2 = nullptr,
             const float* resid = nullptr, int round = 0, int prefill_silu = 0, const GemmArgs* fuse = nullptr) {
+    launch_gemm_i8(args(w, tokens, in, out, wpm, sw, bias, y, ys, wp2, sw2, resid, round, prefill_silu, fuse), epi,
+                   stream);
+  }
+  GemmArgs args(const Ws& w, int tokens, int in, int out, const uint8_t* wpm, const float* sw, const float* bias,
+                float* y, size_t ys, const uint8_t* wp2 = nullptr, const float* sw2 = nullptr,
+                const float* resid = nullptr, int round = 0, int prefill_silu = 0,
+                const GemmArgs* fuse = nullptr) const {
     GemmArgs g = fuse ? *fuse : GemmArgs{};
     g.wp = wpm;
     g.wp2 = wp2;
@@ -244,11 +251,11 @@ struct qwen_hip_model {
     g.round_bf16 = round;
     g.prefill_silu = prefill_silu;
     g.part = wp2 ? nullptr : w.splitk;
-    launch_gemm_i8(g, epi, stream);
+    return g;
   }
 
   void decode_fast(int B, float* hidden, const int* pos, int max_keys, float* kc0, float* vc0, uint64_t ss,
-                   uint64_t ls, int round) {
+                   uint64_t ls, int round, bool pre_reduce = true) {
     const AttnDecodePlan plan = plan_attn_decode(B, max_keys);
     const Ws w = carve(B, B, plan.nsplit);
     const bool fused = B <= kSplitTokens;
@@ -284,17 +291,32 @@ struct qwen_hip_model {
       fn.xq_out = w.xq;
       fn.sx_out = w.sx;
       fn.sums_out = w.sums;
-      if (fused) {
+      if (fused && B == 1 && pre_reduce) {
+        // one sequence: the O projection leaves its fp32 partials, and every block of the gate/up
+        // projection finishes that row (residual, RMSNorm, quantization) into its own activation
+        // slice: one launch fewer per layer
         fn.norm_w = f.post_ln;
-        gemm(w, B, QWEN_HIDDEN, QWEN_HIDDEN, f.o, f.sw_o, nullptr, w.att, QWEN_HIDDEN, kEpiStore, nullptr, nullptr,
-             nullptr, 0, 0, &fn);
+        fn.defer_reduce = 1;
+        const GemmArgs oa = args(w, B, QWEN_HIDDEN, QWEN_HIDDEN, f.o, f.sw_o, nullptr, w.att, QWEN_HIDDEN, nullptr,
+                                 nullptr, nullptr, 0, 0, &fn);
+        fn.defer_reduce = 0;
+        launch_gemm_i8(oa, kEpiStore, stream);
+        const GemmArgs ga = args(w, B, QWEN_HIDDEN, QWEN_INTERMEDIATE, f.gate, f.sw_gate, nullptr, w.s,
+                                 QWEN_INTERMEDIATE, f.up, f.sw_up);
+        if (!launch_gemm_i8_pre(ga, oa, 1, stream)) throw std::runtime_error("gate/up with the O reduce: bad shape");
       } else {
-        gemm(w, B, QWEN_HIDDEN, QWEN_HIDDEN, f.o, f.sw_o, nullptr, w.att, QWEN_HIDDEN, kEpiStore);
-        launch_norm_quant(w.att, QWEN_HIDDEN, B, QWEN_HIDDEN, f.post_ln, kNormDecode, w.xq, w.sx, w.sums, nullptr,
-                          stream);
+        if (fused) {
+          fn.norm_w = f.post_ln;
+          gemm(w, B, QWEN_HIDDEN, QWEN_HIDDEN, f.o, f.sw_o, nullptr, w.att, QWEN_HIDDEN, kEpiStore, nullptr, nullptr,
+               nullptr, 0, 0, &fn);
+        } else {
+          gemm(w, B, QWEN_HIDDEN, QWEN_HIDDEN, f.o, f.sw_o, nullptr, w.att, QWEN_HIDDEN, kEpiStore);
+          launch_norm_quant(w.att, QWEN_HIDDEN, B, QWEN_HIDDEN, f.post_ln, kNormDecode, w.xq, w.sx, w.sums, nullptr,
+                            stream);
+        }
+        gemm(w, B, QWEN_HIDDEN, QWEN_INTERMEDIATE, f.gate, f.sw_gate, nullptr, w.s, QWEN_INTERMEDIATE, kEpiSiluMul,
+             f.up, f.sw_up, nullptr, 0, 0);
       }
-      gemm(w, B, QWEN_HIDDEN, QWEN_INTERMEDIATE, f.gate, f.sw_gate, nullptr, w.s, QWEN_INTERMEDIATE, kEpiSiluMul,
-           f.up, f.sw_up, nullptr, 0, 0);
       launch_norm_quant(w.s, QWEN_INTERMEDIATE, B, QWEN_INTERMEDIATE, nullptr, kNormNone, w.xq, w.sx, w.sums,
                         nullptr, stream);
       const bool fuse_next = fused && l + 1 < layers;  // the next layer's input RMSNorm + quantize
@@ -494,7 +516,8 @@ int qwen_hip_model_decode(qwen_hip_model* m, int mode, int batch, float* hidden,
                           float* k_cache, float* v_cache, uint64_t seq_stride, uint64_t layer_stride) {
   if (!m || !hidden || !positions || !k_cache || !v_cache) return invalid("null argument");
   const int round = (mode & QWEN_FLAG_NO_BF16_ROUND) ? 0 : 1;
-  mode &= ~QWEN_FLAG_NO_BF16_ROUND;
+  const bool pre_reduce = (mode & QWEN_FLAG_SEPARATE_REDUCE) == 0;
+  mode &= ~(QWEN_FLAG_NO_BF16_ROUND | QWEN_FLAG_SEPARATE_REDUCE);
   if (batch <= 0 || max_keys <= 0 || max_keys > QWEN_MAX_SEQ || (mode != QWEN_MODE_ORDERED && mode != QWEN_MODE_FAST))
     return invalid("invalid decode shape or mode");
   if (mode == QWEN_MODE_FAST && (size_t)batch > kMaxArrivals) return invalid("FAST decode batch above 4096 sequences");
@@ -504,7 +527,8 @@ int qwen_hip_model_decode(qwen_hip_model* m, int mode, int batch, float* hidden,
   std::lock_guard<std::mutex> lock(m->mu);
   return guarded_model([&]() -> int {
     if (mode == QWEN_MODE_FAST)
-      m->decode_fast(batch, hidden, positions, max_keys, k_cache, v_cache, seq_stride, layer_stride, round);
+      m->decode_fast(batch, hidden, positions, max_keys, k_cache, v_cache, seq_stride, layer_stride, round,
+                     pre_reduce);
     else
       m->decode_ordered(batch, hidden, positions, max_keys, k_cache, v_cache, seq_stride, layer_stride, round);
     m->last = LastCall{1, mode, batch, 1, max_keys, 0, positions, k_cache, v_cache, seq_stride, layer_stride};
