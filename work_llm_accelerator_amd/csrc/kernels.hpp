@@ -84,11 +84,12 @@ void launch_repack_int4(const uint8_t* W, int out_dim, int in_dim, uint8_t* WP, 
 void launch_norm_quant(const float* x, size_t x_stride, int rows, int n, const float* w, int norm, int8_t* xq,
                        float* sx, int* sums, float* xn, hipStream_t st);
 void launch_gemm_i8(const GemmArgs& a, int epi, hipStream_t st);
-// Gate/up + SiLU·up of one token whose activation row is `pre`'s unfinished reduce step (pre_splits
-// K splits of fp32 partials, kFuseNormQuant on a 1536-wide row): every block finishes that row into
-// its own activation slice, block 0 writes it to pre.y.  Returns false (nothing launched) for other
-// shapes.
-bool launch_gemm_i8_pre(const GemmArgs& a, const GemmArgs& pre, int pre_splits, hipStream_t st);
+// A projection of one token whose activation row is `pre`'s unfinished reduce step (epilogue
+// pre_epi, pre_splits K splits of fp32 partials, kFuseNormQuant on a 1536-wide row): every block
+// finishes that row into its own activation slice, block 0 writes it to pre.y.  Shapes: gate/up +
+// SiLU·up after the O projection (pre_epi kEpiStore), the fused Q/K/V + RoPE after the down
+// projection (pre_epi kEpiResidual).  Returns false (nothing launched) for other shapes.
+bool launch_gemm_i8_pre(const GemmArgs& a, const GemmArgs& pre, int pre_epi, int pre_splits, hipStream_t st);
 // Decode (pos given): token t is sequence t at position pos[t].  Prefill (pos null): token t is
 // sequence t / seq_len at position past + t % seq_len.  Positions outside [0, limit) are skipped.
 void launch_rope_qkv(float* qkv, int qkv_stride, const int* pos, int seq_len, int past, int limit, int tokens,

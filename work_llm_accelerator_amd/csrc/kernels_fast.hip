@@ -818,10 +818,11 @@ __device__ __forceinline__ void reduce_norm_quant_row(const GemmArgs& a, int spl
                                                       int chunk_stride, float* sx_out, int* sums_out, bool write_y);
 
 // PRE (one token, KSW = 1): the activation slice is not loaded but made by the block: wave 0 redoes
-// the reduce step of the previous projection (`pre`, pre_splits K splits, kFuseNormQuant on a
-// 1536-wide row) for token 0 straight into the slice, once the block's weight loads are in flight;
-// block 0 alone writes the finished row (pre.y).  K chunk c of the slice is the token's row c.
-template <int RTW, bool DUAL, int EPI, int NKC, bool ROPE, int KSW, bool PRE>
+// the reduce step of the previous projection (`pre` with epilogue PRE_EPI, pre_splits K splits,
+// kFuseNormQuant on a 1536-wide row) for token 0 straight into the slice, once the block's weight
+// loads are in flight; block 0 alone writes the finished row (pre.y, pre.y_raw).  K chunk c of the
+// slice is the token's row c.
+template <int RTW, bool DUAL, int EPI, int NKC, bool ROPE, int KSW, bool PRE, int PRE_EPI = kEpiStore>
 __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count, int rg_count, int splits,
                                                  const GemmArgs& pre, int pre_splits) {
   constexpr int D = DUAL ? 2 : 1;
@@ -885,8 +886,8 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   if constexpr (PRE) {
     // token 0's row of the slice: K chunk c at xs + c * 16 * 256 (row 0 of the chunk, unswizzled)
     if (threadIdx.x < 64)
-      reduce_norm_quant_row<kEpiStore>(pre, pre_splits, 0, reinterpret_cast<int8_t*>(xs), 16 * 256, &pre_sx, pre_sums,
-                                       blockIdx.x == 0);
+      reduce_norm_quant_row<PRE_EPI>(pre, pre_splits, 0, reinterpret_cast<int8_t*>(xs), 16 * 256, &pre_sx, pre_sums,
+                                     blockIdx.x == 0);
   }
   wait_vmcnt<0>();
   __syncthreads();
@@ -1047,9 +1048,9 @@ gemm_skinny_kernel(GemmArgs a, int tt_count, int rg_count, int splits) {
 }
 
 // One token, with the previous projection's reduce step redone by every block (see PRE above).
-template <int RTW, bool DUAL, int EPI, int NKC, bool ROPE>
+template <int RTW, bool DUAL, int EPI, int NKC, bool ROPE, int PRE_EPI>
 __global__ void __launch_bounds__(256) gemm_skinny_pre_kernel(GemmArgs a, int rg_count, GemmArgs pre, int pre_splits) {
-  gemm_skinny_body<RTW, DUAL, EPI, NKC, ROPE, 1, true>(a, 1, rg_count, 1, pre, pre_splits);
+  gemm_skinny_body<RTW, DUAL, EPI, NKC, ROPE, 1, true, PRE_EPI>(a, 1, rg_count, 1, pre, pre_splits);
 }
 
 // Sum over z < splits of part[z * zstride + off .. + 3] in z order.  The loads of 8 splits are all
@@ -1992,7 +1993,7 @@ static bool launch_skinny(const GemmArgs& a, hipStream_t st) {
   if constexpr (!DUAL) {
     if (a.in_dim == QWEN_INTERMEDIATE && a.part && a.fuse != kFuseQkvRope) {
       launch_skinny_t<1, false, EPI, 14, false>(a, row_tiles / 4, 5, st);
-      launch_reduce<EPI>(a, 5, st);
+      if (!(a.defer_reduce && a.tokens == 1 && a.fuse == kFuseNormQuant)) launch_reduce<EPI>(a, 5, st);
       return true;
     }
   }
@@ -2050,14 +2051,24 @@ static void launch_gemm_epi(const GemmArgs& a, hipStream_t st) {
   }
 }
 
-bool launch_gemm_i8_pre(const GemmArgs& a, const GemmArgs& pre, int pre_splits, hipStream_t st) {
-  if (a.tokens != 1 || a.in_dim != QWEN_HIDDEN || !a.wp2 || a.out_dim % 64 != 0 || pre.out_dim != QWEN_HIDDEN ||
-      pre.fuse != kFuseNormQuant || pre.tokens != 1 || pre_splits < 1)
+bool launch_gemm_i8_pre(const GemmArgs& a, const GemmArgs& pre, int pre_epi, int pre_splits, hipStream_t st) {
+  if (a.tokens != 1 || a.in_dim != QWEN_HIDDEN || pre.out_dim != QWEN_HIDDEN || pre.fuse != kFuseNormQuant ||
+      pre.tokens != 1 || pre_splits < 1 || pre_splits > kMaxSplits)
     return false;
-  const int rg_count = a.out_dim / 64;
-  hipLaunchKernelGGL((gemm_skinny_pre_kernel<1, true, kEpiSiluMul, 12, false>), dim3(8 * ((rg_count + 7) / 8)),
-                     dim3(256), 0, st, a, rg_count, pre, pre_splits);
-  return true;
+  if (a.wp2 && a.out_dim % 64 == 0 && pre_epi == kEpiStore) {  // gate/up after the O projection
+    const int rg_count = a.out_dim / 64;
+    hipLaunchKernelGGL((gemm_skinny_pre_kernel<1, true, kEpiSiluMul, 12, false, kEpiStore>),
+                       dim3(8 * ((rg_count + 7) / 8)), dim3(256), 0, st, a, rg_count, pre, pre_splits);
+    return true;
+  }
+  if (!a.wp2 && a.fuse == kFuseQkvRope && a.out_dim == QWEN_QKV_ROWS && pre_epi == kEpiResidual) {
+    // Q/K/V + RoPE + KV append after the previous layer's down projection
+    const int rg_count = a.out_dim / 128;
+    hipLaunchKernelGGL((gemm_skinny_pre_kernel<2, false, kEpiStore, 12, true, kEpiResidual>),
+                       dim3(8 * ((rg_count + 7) / 8)), dim3(256), 0, st, a, rg_count, pre, pre_splits);
+    return true;
+  }
+  return false;
 }
 
 void launch_gemm_i8(const GemmArgs& a, int epi, hipStream_t st) {

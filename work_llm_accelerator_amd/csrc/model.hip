@@ -259,6 +259,8 @@ struct qwen_hip_model {
     const AttnDecodePlan plan = plan_attn_decode(B, max_keys);
     const Ws w = carve(B, B, plan.nsplit);
     const bool fused = B <= kSplitTokens;
+    const bool one = fused && B == 1 && pre_reduce;  // one sequence: reduce steps in the next projection
+    GemmArgs down_pending{};                         // the previous layer's deferred down projection
     for (int l = 0; l < layers; ++l) {
       const FastLayer& f = fast[l];
       float* kc = kc0 + (size_t)l * ls;
@@ -277,8 +279,17 @@ struct qwen_hip_model {
         fq.v_cache = vc;
         fq.seq_stride = ss;
         fq.limit = max_keys;
-        gemm(w, B, QWEN_HIDDEN, (int)kQkvRows, f.qkv, f.sw_qkv, f.b_qkv, w.qkv, kQkvRows, kEpiStore, nullptr, nullptr,
-             nullptr, 0, 0, &fq);
+        if (one && l > 0) {
+          // the previous layer's down projection left its K-split partials: every block of this
+          // projection finishes that row (residual, bf16 rounding, this layer's RMSNorm, quantization)
+          const GemmArgs qa = args(w, B, QWEN_HIDDEN, (int)kQkvRows, f.qkv, f.sw_qkv, f.b_qkv, w.qkv, kQkvRows,
+                                   nullptr, nullptr, nullptr, 0, 0, &fq);
+          if (!launch_gemm_i8_pre(qa, down_pending, kEpiResidual, 5, stream))
+            throw std::runtime_error("Q/K/V with the down reduce: bad shape");
+        } else {
+          gemm(w, B, QWEN_HIDDEN, (int)kQkvRows, f.qkv, f.sw_qkv, f.b_qkv, w.qkv, kQkvRows, kEpiStore, nullptr,
+               nullptr, nullptr, 0, 0, &fq);
+        }
       } else {
         gemm(w, B, QWEN_HIDDEN, (int)kQkvRows, f.qkv, f.sw_qkv, f.b_qkv, w.qkv, kQkvRows, kEpiStore);
         launch_rope_qkv(w.qkv, (int)kQkvRows, pos, 1, 0, max_keys, B, rope_decode, kc, vc, ss, stream);
@@ -291,7 +302,7 @@ struct qwen_hip_model {
       fn.xq_out = w.xq;
       fn.sx_out = w.sx;
       fn.sums_out = w.sums;
-      if (fused && B == 1 && pre_reduce) {
+      if (one) {
         // one sequence: the O projection leaves its fp32 partials, and every block of the gate/up
         // projection finishes that row (residual, RMSNorm, quantization) into its own activation
         // slice: one launch fewer per layer
@@ -303,7 +314,8 @@ struct qwen_hip_model {
         launch_gemm_i8(oa, kEpiStore, stream);
         const GemmArgs ga = args(w, B, QWEN_HIDDEN, QWEN_INTERMEDIATE, f.gate, f.sw_gate, nullptr, w.s,
                                  QWEN_INTERMEDIATE, f.up, f.sw_up);
-        if (!launch_gemm_i8_pre(ga, oa, 1, stream)) throw std::runtime_error("gate/up with the O reduce: bad shape");
+        if (!launch_gemm_i8_pre(ga, oa, kEpiStore, 1, stream))
+          throw std::runtime_error("gate/up with the O reduce: bad shape");
       } else {
         if (fused) {
           fn.norm_w = f.post_ln;
@@ -321,8 +333,16 @@ struct qwen_hip_model {
                         nullptr, stream);
       const bool fuse_next = fused && l + 1 < layers;  // the next layer's input RMSNorm + quantize
       fn.norm_w = fuse_next ? fast[l + 1].ln : nullptr;
-      gemm(w, B, QWEN_INTERMEDIATE, QWEN_HIDDEN, f.down, f.sw_down, nullptr, hidden, QWEN_HIDDEN, kEpiResidual,
-           nullptr, nullptr, w.att, round, 0, fuse_next ? &fn : nullptr);
+      if (one && fuse_next) {
+        fn.defer_reduce = 1;
+        down_pending = args(w, B, QWEN_INTERMEDIATE, QWEN_HIDDEN, f.down, f.sw_down, nullptr, hidden, QWEN_HIDDEN,
+                            nullptr, nullptr, w.att, round, 0, &fn);
+        fn.defer_reduce = 0;
+        launch_gemm_i8(down_pending, kEpiResidual, stream);
+      } else {
+        gemm(w, B, QWEN_INTERMEDIATE, QWEN_HIDDEN, f.down, f.sw_down, nullptr, hidden, QWEN_HIDDEN, kEpiResidual,
+             nullptr, nullptr, w.att, round, 0, fuse_next ? &fn : nullptr);
+      }
     }
     QWEN_HIP(hipGetLastError());
   }
