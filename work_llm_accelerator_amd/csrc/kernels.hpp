@@ -90,6 +90,11 @@ void launch_gemm_i8(const GemmArgs& a, int epi, hipStream_t st);
 // SiLU·up after the O projection (pre_epi kEpiStore), the fused Q/K/V + RoPE after the down
 // projection (pre_epi kEpiResidual).  Returns false (nothing launched) for other shapes.
 bool launch_gemm_i8_pre(const GemmArgs& a, const GemmArgs& pre, int pre_epi, int pre_splits, hipStream_t st);
+// The down projection (+ residual) of one token whose activation row is the fp32 row pre.y
+// (pre.in_dim = 8960 wide): every block quantizes that row for its own K chunks (as norm_quant_kernel
+// without a norm), block 0 writes its scale and limb sums to pre.sx_out / pre.sums_out (= a.sx,
+// a.sums), followed by the reduce step unless a.defer_reduce.  Returns false for other shapes.
+bool launch_gemm_i8_preq(const GemmArgs& a, const GemmArgs& pre, hipStream_t st);
 // Decode (pos given): token t is sequence t at position pos[t].  Prefill (pos null): token t is
 // sequence t / seq_len at position past + t % seq_len.  Positions outside [0, limit) are skipped.
 void launch_rope_qkv(float* qkv, int qkv_stride, const int* pos, int seq_len, int past, int limit, int tokens,

@@ -817,16 +817,85 @@ template <int EPI>
 __device__ __forceinline__ void reduce_norm_quant_row(const GemmArgs& a, int splits, int tok, int8_t* xq_row,
                                                       int chunk_stride, float* sx_out, int* sums_out, bool write_y);
 
+// Two-limb quantization of one fp32 row x[0, n) (n % 4 == 0, n <= NV * 1024) by a 256-thread block
+// with norm_quant_row's arithmetic and thread mapping (float4 k = t + 256 j): the code of K chunks
+// kc0 .. kc0 + nkc - 1 goes to xs (chunk kc0 + i at byte i * chunk_stride), the scale and limb sums of
+// the whole row to sx_lds / sums_lds and, when sx_g is given, to sx_g / sums_g.
+template <int NV>
+__device__ __forceinline__ void quant_row_slice(const float* __restrict__ x, int n, int kc0, int nkc, uint8_t* xs,
+                                                int chunk_stride, float* sx_lds, int* sums_lds, float* sx_g,
+                                                int* sums_g) {
+  __shared__ float red_f[4];
+  __shared__ int red_i[4];
+  const int n4 = n >> 2;
+  const float4* x4 = reinterpret_cast<const float4*>(x);
+  float4 v[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int k = threadIdx.x + 256 * j;
+    v[j] = k < n4 ? x4[k] : make_float4(0, 0, 0, 0);
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j)
+    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
+  amax = block_max4(amax, red_f);
+  const float inv = amax > 0.0f ? (float)kQuantMax / amax : 0.0f;
+  int sh = 0, sl = 0;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int k = threadIdx.x + 256 * j;
+    if (k < n4) {
+      const float e[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+      uint32_t hw = 0, lw = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float xf = fminf(fmaxf(rintf(e[q] * inv), -(float)kQuantMax), (float)kQuantMax);
+        const int X = (int)xf;
+        const int H = (X + 128) >> 8;
+        const int L = X - (H << 8);
+        hw |= (uint32_t)(H & 0xFF) << (8 * q);
+        lw |= (uint32_t)(L & 0xFF) << (8 * q);
+        sh += H;
+        sl += L;
+      }
+      const int chunk = (4 * k) >> 7;
+      if (chunk >= kc0 && chunk < kc0 + nkc) {
+        uint8_t* dst = xs + (chunk - kc0) * chunk_stride + ((4 * k) & 127);
+        *reinterpret_cast<uint32_t*>(dst) = hw;
+        *reinterpret_cast<uint32_t*>(dst + 128) = lw;
+      }
+    }
+  }
+  sh = block_sum4_i(sh, red_i);
+  sl = block_sum4_i(sl, red_i);
+  if (threadIdx.x == 0) {
+    const float sx = amax > 0.0f ? amax / (float)kQuantMax : 1.0f;
+    *sx_lds = sx;
+    sums_lds[0] = sh;
+    sums_lds[1] = sl;
+    if (sx_g) {
+      *sx_g = sx;
+      sums_g[0] = sh;
+      sums_g[1] = sl;
+    }
+  }
+}
+
 // PRE (one token, KSW = 1): the activation slice is not loaded but made by the block: wave 0 redoes
 // the reduce step of the previous projection (`pre` with epilogue PRE_EPI, pre_splits K splits,
 // kFuseNormQuant on a 1536-wide row) for token 0 straight into the slice, once the block's weight
 // loads are in flight; block 0 alone writes the finished row (pre.y, pre.y_raw).  K chunk c of the
-// slice is the token's row c.
-template <int RTW, bool DUAL, int EPI, int NKC, bool ROPE, int KSW, bool PRE, int PRE_EPI = kEpiStore>
+// slice is the token's row c.  PRE_QUANT (one token, KSW = 1): the slice is the two-limb code of the
+// fp32 row pre.y (pre.in_dim wide, as norm_quant_kernel without a norm), made by every block for its
+// own K chunks; block 0 writes the row's scale and limb sums to pre.sx_out / pre.sums_out.
+template <int RTW, bool DUAL, int EPI, int NKC, bool ROPE, int KSW, bool PRE, int PRE_EPI = kEpiStore,
+          bool PRE_QUANT = false>
 __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count, int rg_count, int splits,
                                                  const GemmArgs& pre, int pre_splits) {
   constexpr int D = DUAL ? 2 : 1;
   static_assert(!PRE || (KSW == 1 && NKC * kKChunk == QWEN_HIDDEN), "PRE: one K group over a 1536-wide row");
+  static_assert(!PRE_QUANT || (KSW == 1 && !PRE), "PRE_QUANT: one K group");
   constexpr int KC = NKC / KSW;  // K chunks per wave group
   static_assert(NKC % KSW == 0, "K chunks split evenly over the wave groups");
   static_assert(RTW * D * 8 * 1024 <= NKC * 16 * 256 || KSW == 1, "K-group reduction fits the slice buffer");
@@ -850,7 +919,7 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   const size_t row_stride_x = (size_t)a.in_dim * 2u;
 
   // activation slice -> LDS: chunk c, rows 4q..4q+3 per load (1 KiB), wave w takes chunks w, w+4KSW, ..
-  for (int c = threadIdx.x >> 6; c < (PRE ? 0 : NKC); c += 4 * KSW) {
+  for (int c = threadIdx.x >> 6; c < (PRE || PRE_QUANT ? 0 : NKC); c += 4 * KSW) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int row = 4 * q + (lane >> 4);
@@ -883,6 +952,11 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   __builtin_amdgcn_sched_barrier(0);  // every load above is in flight before any use (one round trip)
   __shared__ float pre_sx;
   __shared__ int pre_sums[2];
+  if constexpr (PRE_QUANT) {
+    // token 0's row of the slice: K chunks kc0 .. kc0 + NKC - 1 (row 0 of each chunk, unswizzled)
+    quant_row_slice<kQuantVecs>(pre.y, pre.in_dim, kc0, NKC, xs, 16 * 256, &pre_sx, pre_sums,
+                                blockIdx.x == 0 ? pre.sx_out : nullptr, pre.sums_out);
+  }
   if constexpr (PRE) {
     // token 0's row of the slice: K chunk c at xs + c * 16 * 256 (row 0 of the chunk, unswizzled)
     if (threadIdx.x < 64)
@@ -956,7 +1030,7 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   // epilogue: lane holds rows 16*rt + 4g + q (q < 4) of token tok0 + col
   const int tok = tok0 + col;
   if (tok >= a.tokens) return;
-  const double sx = (double)(PRE ? pre_sx : a.sx[tok]);
+  const double sx = (double)(PRE || PRE_QUANT ? pre_sx : a.sx[tok]);
   const bool partial = splits > 1 || (!DUAL && !ROPE && a.fuse != kFuseNone);
   if (partial) {
 #pragma unroll
@@ -972,8 +1046,8 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
     }
     return;
   }
-  const int sh8 = 8 * (PRE ? pre_sums[0] : a.sums[2 * tok]);
-  const int sl8 = 8 * (PRE ? pre_sums[1] : a.sums[2 * tok + 1]);
+  const int sh8 = 8 * (PRE || PRE_QUANT ? pre_sums[0] : a.sums[2 * tok]);
+  const int sl8 = 8 * (PRE || PRE_QUANT ? pre_sums[1] : a.sums[2 * tok + 1]);
   float y[RTW][4];
 #pragma unroll
   for (int r = 0; r < RTW; ++r) {
@@ -1045,6 +1119,12 @@ template <int RTW, bool DUAL, int EPI, int NKC, bool ROPE, int KSW>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(3)))
 gemm_skinny_kernel(GemmArgs a, int tt_count, int rg_count, int splits) {
   gemm_skinny_body<RTW, DUAL, EPI, NKC, ROPE, KSW, false>(a, tt_count, rg_count, splits, a, 0);
+}
+
+// One token, the activation row quantized by every block for its own K chunks (see PRE_QUANT above).
+template <int RTW, int EPI, int NKC>
+__global__ void __launch_bounds__(256) gemm_skinny_preq_kernel(GemmArgs a, int rg_count, int splits, GemmArgs pre) {
+  gemm_skinny_body<RTW, false, EPI, NKC, false, 1, false, kEpiStore, true>(a, 1, rg_count, splits, pre, 0);
 }
 
 // One token, with the previous projection's reduce step redone by every block (see PRE above).
@@ -2069,6 +2149,18 @@ bool launch_gemm_i8_pre(const GemmArgs& a, const GemmArgs& pre, int pre_epi, int
     return true;
   }
   return false;
+}
+
+bool launch_gemm_i8_preq(const GemmArgs& a, const GemmArgs& pre, hipStream_t st) {
+  if (a.tokens != 1 || a.in_dim != QWEN_INTERMEDIATE || a.out_dim != QWEN_HIDDEN || a.wp2 || !a.part ||
+      pre.in_dim != a.in_dim || !pre.y || !pre.sx_out || !pre.sums_out)
+    return false;
+  constexpr int kSplits = 5;  // 14 K chunks each, as the separate-quantization path
+  const int rg_count = a.out_dim / 64;
+  hipLaunchKernelGGL((gemm_skinny_preq_kernel<1, kEpiResidual, 14>), dim3(8 * ((rg_count * kSplits + 7) / 8)),
+                     dim3(256), 0, st, a, rg_count, kSplits, pre);
+  if (!(a.defer_reduce && a.fuse == kFuseNormQuant)) launch_reduce<kEpiResidual>(a, kSplits, st);
+  return true;
 }
 
 void launch_gemm_i8(const GemmArgs& a, int epi, hipStream_t st) {

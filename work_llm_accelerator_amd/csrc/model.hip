@@ -329,17 +329,25 @@ struct qwen_hip_model {
         gemm(w, B, QWEN_HIDDEN, QWEN_INTERMEDIATE, f.gate, f.sw_gate, nullptr, w.s, QWEN_INTERMEDIATE, kEpiSiluMul,
              f.up, f.sw_up, nullptr, 0, 0);
       }
-      launch_norm_quant(w.s, QWEN_INTERMEDIATE, B, QWEN_INTERMEDIATE, nullptr, kNormNone, w.xq, w.sx, w.sums,
-                        nullptr, stream);
       const bool fuse_next = fused && l + 1 < layers;  // the next layer's input RMSNorm + quantize
       fn.norm_w = fuse_next ? fast[l + 1].ln : nullptr;
-      if (one && fuse_next) {
-        fn.defer_reduce = 1;
-        down_pending = args(w, B, QWEN_INTERMEDIATE, QWEN_HIDDEN, f.down, f.sw_down, nullptr, hidden, QWEN_HIDDEN,
-                            nullptr, nullptr, w.att, round, 0, &fn);
+      if (one) {
+        // the SiLU·up row is quantized by every block of the down projection for its own K chunks;
+        // the reduce step runs in the next layer's Q/K/V blocks (its own launch after the last layer)
+        GemmArgs sq{};
+        sq.y = w.s;
+        sq.in_dim = QWEN_INTERMEDIATE;
+        sq.sx_out = w.sx;
+        sq.sums_out = w.sums;
+        fn.defer_reduce = fuse_next ? 1 : 0;
+        const GemmArgs da = args(w, B, QWEN_INTERMEDIATE, QWEN_HIDDEN, f.down, f.sw_down, nullptr, hidden,
+                                 QWEN_HIDDEN, nullptr, nullptr, w.att, round, 0, fuse_next ? &fn : nullptr);
         fn.defer_reduce = 0;
-        launch_gemm_i8(down_pending, kEpiResidual, stream);
+        if (!launch_gemm_i8_preq(da, sq, stream)) throw std::runtime_error("down with the quantization: bad shape");
+        if (fuse_next) down_pending = da;
       } else {
+        launch_norm_quant(w.s, QWEN_INTERMEDIATE, B, QWEN_INTERMEDIATE, nullptr, kNormNone, w.xq, w.sx, w.sums,
+                          nullptr, stream);
         gemm(w, B, QWEN_INTERMEDIATE, QWEN_HIDDEN, f.down, f.sw_down, nullptr, hidden, QWEN_HIDDEN, kEpiResidual,
              nullptr, nullptr, w.att, round, 0, fuse_next ? &fn : nullptr);
       }

@@ -20,7 +20,7 @@ from .layout import HIDDEN, KV_WIDTH, LAYOUT
 MODE_ORDERED = 0
 MODE_FAST = 1
 FLAG_NO_BF16_ROUND = 0x100  # skip the driver's bf16 rounding between layers
-FLAG_SEPARATE_REDUCE = 0x200  # FAST decode of one sequence: the O projection's reduce as its own launch
+FLAG_SEPARATE_REDUCE = 0x200  # FAST decode of one sequence: the row steps fused into projections as own launches
 
 KERNEL_ATTN_DECODE = 1
 KERNEL_GEMM_GATE_UP = 2
