@@ -292,6 +292,38 @@ def test_model_decode_fast_batched(torch, layers2, batch):
         m1.close()
 
 
+@pytest.mark.skip(reason="split decode on CU-masked streams switched off: on MI355X both cases passed, then "
+                  "the process hung while the model and its CU-masked streams were torn down (cause not found)")
+@pytest.mark.parametrize("pcus", [4, 8])
+def test_model_decode_fast_split(torch, layers2, model2, monkeypatch, pcus):
+    """A batch decoded as two concurrent halves on CU-masked streams (projections on `pcus` CUs of
+    every XCD, attention on the rest): every sequence of both halves stays within the per-layer
+    tolerance of the oracle over two layers (the second layer's input RMSNorm + quantization fused
+    into the first layer's down projection), and so do the appended K/V rows."""
+    from work_llm_accelerator_amd.model import FLAG_NO_BF16_ROUND, MODE_FAST
+
+    batch = 32
+    rng = np.random.default_rng(900 + pcus)
+    pasts = [int(p) for p in rng.integers(0, 60, batch)]
+    print(f"model decode fast split batch={batch} pcus={pcus}", flush=True)
+    monkeypatch.setenv("QWEN_SPLIT_CUS", str(pcus))
+    cache, hist, x = decode_setup(torch, 2, pasts, 64, seed=53)
+    hidden = torch.from_numpy(x).cuda()
+    pos = torch.tensor(pasts, dtype=torch.int32, device="cuda")
+    model2.decode(MODE_FAST | FLAG_NO_BF16_ROUND, hidden, pos, max(pasts) + 1, cache)
+    model2.synchronize()
+    got = hidden.cpu().numpy()
+    for b, past in enumerate(pasts):
+        kl = [hist[(l, b)][0].copy() for l in range(2)]
+        vl = [hist[(l, b)][1].copy() for l in range(2)]
+        ref = oracle_decode(layers2, x[b], past, kl, vl, rounding=False)
+        assert rel_err(got[b], ref) <= FAST_TOL, (b, rel_err(got[b], ref))
+        for l in range(2):
+            gk = cache.k[l, b, past].cpu().numpy().reshape(-1)
+            rk = kl[l].reshape(-1, KV_WIDTH)[past]
+            assert rel_err(gk, rk) <= FAST_TOL, (b, l, rel_err(gk, rk))
+
+
 @pytest.mark.parametrize("S", [40, 150, 300])
 def test_model_prefill_fast_mid(torch, layers2, S):
     """40 tokens: the 17..64-token GEMM path on prefill shapes; 150 tokens: the 65..256-token GEMM

@@ -106,7 +106,8 @@ void launch_rope_qkv(float* qkv, int qkv_stride, const int* pos, int seq_len, in
 struct AttnDecodePlan {
   int nsplit, chunk;
 };
-AttnDecodePlan plan_attn_decode(int batch, int max_keys);
+// `cus`: the CUs the launch may use (a CU-masked stream), 0 for all of them.
+AttnDecodePlan plan_attn_decode(int batch, int max_keys, int cus = 0);
 void launch_zero_u32(unsigned* p, int n, hipStream_t st);
 void launch_attn_decode(const float* qkv, int qkv_stride, const float* k_cache, const float* v_cache,
                         size_t seq_stride, const int* pos, int batch, int max_keys, const AttnDecodePlan& plan,

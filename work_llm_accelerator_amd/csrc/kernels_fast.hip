@@ -2181,16 +2181,17 @@ void launch_rope_qkv(float* qkv, int qkv_stride, const int* pos, int seq_len, in
 constexpr int kAttnMinChunk = 64;
 constexpr int kAttnSoftSplits = 24;
 
-AttnDecodePlan plan_attn_decode(int batch, int max_keys) {
+AttnDecodePlan plan_attn_decode(int batch, int max_keys, int cus) {
   // co-resident blocks of attn_decode_kernel on the current device (CUs x blocks per CU)
-  static const int slots = [] {
+  static const int2 dev_slots = [] {
     int dev = 0, per_cu = 0;
     hipDeviceProp_t prop;
-    if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess) return 1024;
+    if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess) return int2{256, 4};
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, attn_decode_kernel, 256, 0) != hipSuccess || per_cu < 1)
       per_cu = 1;
-    return prop.multiProcessorCount * per_cu;
+    return int2{prop.multiProcessorCount, per_cu};
   }();
+  const int slots = (cus > 0 && cus < dev_slots.x ? cus : dev_slots.x) * dev_slots.y;
   // 3 of every 4 co-resident slots: the KV stream runs faster at 12 than at 16 waves per CU.
   int nsplit = (3 * slots / 4) / (QWEN_KV_HEADS * (batch > 0 ? batch : 1));
   nsplit = nsplit < 1 ? 1 : (nsplit > kAttnMaxSplits ? kAttnMaxSplits : nsplit);
