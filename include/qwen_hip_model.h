@@ -44,7 +44,8 @@ typedef struct qwen_hip_model qwen_hip_model;
 /* OR-ed into `mode`: skip the bf16 rounding between layers (the layer outputs stay fp32). */
 #define QWEN_FLAG_NO_BF16_ROUND 0x100
 /* OR-ed into `mode` (FAST decode of one sequence): run the small row steps as launches of their own
- * rather than in the prologue of every block of the projection that follows them: the O projection's
+ * rather than in the prologue of every block of the projection that follows them: the decode
+ * attention's split merge + context quantization (fused into O), the O projection's
  * reduce (fused into gate/up), the SiLU·up quantization (fused into down) and the down projection's
  * reduce + next RMSNorm + quantization (fused into the next layer's Q/K/V).  Same arithmetic, same
  * results; it exists to check the fused forms. */

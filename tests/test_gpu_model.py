@@ -376,8 +376,9 @@ def test_model_prefill_fast_many_seqs(torch, layers2):
 
 @pytest.mark.parametrize("past", [0, 37])
 def test_model_decode_o_reduce_in_gate_up(torch, layers2, model2, past):
-    """One sequence: the O projection's reduce step (RMSNorm, quantization) runs in every block of
-    the gate/up projection, the SiLU·up row's quantization in every block of the down projection,
+    """One sequence: the decode attention's split merge and the context row's quantization run in
+    every block of the O projection, the O projection's reduce step (RMSNorm, quantization) in every
+    block of the gate/up projection, the SiLU·up row's quantization in every block of the down projection,
     and layer 0's down-projection reduce step (residual, bf16 rounding, layer 1's RMSNorm,
     quantization) in every block of layer 1's Q/K/V projection, instead of their own launches; both
     forms must give exactly the same hidden row and K/V cache, over both layers with the driver's

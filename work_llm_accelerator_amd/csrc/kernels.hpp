@@ -38,6 +38,17 @@ constexpr int kFuseNone = 0, kFuseQkvRope = 1, kFuseNormQuant = 2;
 // Bytes of the two-limb code of `rows` activation rows of width n.
 inline size_t xq_bytes(size_t rows, size_t n) { return rows * n * 2u; }
 
+// The split-KV decode-attention partials of one sequence (attn_decode_kernel without its merge):
+// part[head][split][128] and pml[head][split] = (m, l), merged by the blocks of the O projection.
+struct AttnMergeArgs {
+  const float* part;
+  const float2* pml;
+  const int* pos;  // position of the sequence's new token
+  int nsplit, chunk, max_keys;
+  float* sx_out;  // scale and limb sums of the quantized context row (block 0 writes them)
+  int* sums_out;
+};
+
 struct GemmArgs {
   const uint8_t* wp;    // repacked weights (tile layout)
   const uint8_t* wp2;   // second matrix (gate/up pair) or null
@@ -95,6 +106,11 @@ bool launch_gemm_i8_pre(const GemmArgs& a, const GemmArgs& pre, int pre_epi, int
 // without a norm), block 0 writes its scale and limb sums to pre.sx_out / pre.sums_out (= a.sx,
 // a.sums), followed by the reduce step unless a.defer_reduce.  Returns false for other shapes.
 bool launch_gemm_i8_preq(const GemmArgs& a, const GemmArgs& pre, hipStream_t st);
+// The O projection of one token whose input row is the attention context of `am`: every block merges
+// the attention's split partials (the arithmetic of attn_decode_kernel's merge) and quantizes the row
+// into its own slice; block 0 writes the row's scale and limb sums to am.sx_out / am.sums_out (= a.sx,
+// a.sums), followed by the reduce step unless a.defer_reduce.  Returns false for other shapes.
+bool launch_gemm_i8_prea(const GemmArgs& a, const AttnMergeArgs& am, hipStream_t st);
 // Decode (pos given): token t is sequence t at position pos[t].  Prefill (pos null): token t is
 // sequence t / seq_len at position past + t % seq_len.  Positions outside [0, limit) are skipped.
 void launch_rope_qkv(float* qkv, int qkv_stride, const int* pos, int seq_len, int past, int limit, int tokens,

@@ -159,7 +159,8 @@ __device__ __forceinline__ int block_sum4_i(int v, int* s4) {
 // the token scale and the two limb sums.
 // ---------------------------------------------------------------------------------------------
 __device__ void quantize_row_lds(const float* __restrict__ v, int n, int8_t* __restrict__ xq_row,
-                                 float* __restrict__ sx_out, int* __restrict__ sums_out, float* red_f, int* red_i) {
+                                 float* __restrict__ sx_out, int* __restrict__ sums_out, float* red_f, int* red_i,
+                                 int chunk_stride = 256) {
   float amax = 0.0f;
   for (int k = threadIdx.x; k < n; k += 256) amax = fmaxf(amax, fabsf(v[k]));
   amax = block_max4(amax, red_f);
@@ -174,8 +175,8 @@ __device__ void quantize_row_lds(const float* __restrict__ v, int n, int8_t* __r
     const int L = X - (H << 8);
     const int chunk = k >> 7;
     const int within = k & 127;
-    xq_row[chunk * 256 + within] = (int8_t)H;
-    xq_row[chunk * 256 + 128 + within] = (int8_t)L;
+    xq_row[chunk * chunk_stride + within] = (int8_t)H;
+    xq_row[chunk * chunk_stride + 128 + within] = (int8_t)L;
     sh += H;
     sl += L;
   }
@@ -882,20 +883,95 @@ __device__ __forceinline__ void quant_row_slice(const float* __restrict__ x, int
   }
 }
 
+// The merge of one sequence's split-KV decode-attention partials, in the arithmetic and order of
+// attn_decode_kernel's merge (per head: max of the split maxima, exp-weights normalised by the
+// weighted sum, then the weighted sum of the split partial rows), followed by quantize_row_lds of the
+// context row into token 0's row of a skinny-GEMM slice (K chunk c at xs + c * chunk_stride).  The
+// partials come from the previous launch, so plain loads see them.  256 threads.
+__device__ __forceinline__ void attn_merge_quant_slice(const AttnMergeArgs& am, uint8_t* xs, int chunk_stride,
+                                                       float* sx_lds, int* sums_lds, bool write_global) {
+  __shared__ float ml[QWEN_Q_HEADS * kAttnMaxSplits * 2];  // (m, l) per head and split, then merge weights
+  __shared__ float row[QWEN_HIDDEN];
+  __shared__ float red_f[4];
+  __shared__ int red_i[4];
+  const int n = min(max(am.pos[0], 0) + 1, am.max_keys);
+  const int nc = (n + am.chunk - 1) / am.chunk;  // splits that hold keys
+  const int nsplit = am.nsplit;
+  const int d = threadIdx.x & 127;
+  const int h0 = threadIdx.x >> 7;
+  const float* pa = am.part + d;
+  const float* pb = reinterpret_cast<const float*>(am.pml);
+  float pv[6][8];
+  auto load_part = [&](int s0) {
+#pragma unroll
+    for (int k = 0; k < 6; ++k)
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        pv[k][j] = s0 + j < nc ? pa[((size_t)(h0 + 2 * k) * nsplit + s0 + j) * QWEN_HEAD_DIM] : 0.0f;
+  };
+  load_part(0);
+  for (int i = threadIdx.x; i < QWEN_Q_HEADS * nc; i += 256) {
+    const int h = i / nc, sp = i % nc;
+    ml[(h * kAttnMaxSplits + sp) * 2] = pb[2 * (h * nsplit + sp)];
+    ml[(h * kAttnMaxSplits + sp) * 2 + 1] = pb[2 * (h * nsplit + sp) + 1];
+  }
+  __syncthreads();
+  if (threadIdx.x < QWEN_Q_HEADS) {
+    float* mh = ml + threadIdx.x * kAttnMaxSplits * 2;
+    float M = -INFINITY;
+    for (int sp = 0; sp < nc; ++sp) M = fmaxf(M, mh[2 * sp]);
+    float L = 0.0f;
+    for (int sp = 0; sp < nc; ++sp) {
+      const float f = __expf(mh[2 * sp] - M);
+      mh[2 * sp] = f;
+      L += mh[2 * sp + 1] * f;
+    }
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    for (int sp = 0; sp < nc; ++sp) mh[2 * sp] *= inv;  // merge weight of split sp
+  }
+  __syncthreads();
+  float out[6];
+#pragma unroll
+  for (int k = 0; k < 6; ++k) out[k] = 0.0f;
+  for (int s0 = 0; s0 < nc; s0 += 8) {
+    if (s0 > 0) load_part(s0);
+#pragma unroll
+    for (int k = 0; k < 6; ++k)
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (s0 + j < nc) out[k] += pv[k][j] * ml[((h0 + 2 * k) * kAttnMaxSplits + s0 + j) * 2];
+  }
+#pragma unroll
+  for (int k = 0; k < 6; ++k) row[(h0 + 2 * k) * QWEN_HEAD_DIM + d] = out[k];
+  __syncthreads();
+  quantize_row_lds(row, QWEN_HIDDEN, reinterpret_cast<int8_t*>(xs), sx_lds, sums_lds, red_f, red_i, chunk_stride);
+  if (write_global && threadIdx.x == 0) {
+    *am.sx_out = *sx_lds;
+    am.sums_out[0] = sums_lds[0];
+    am.sums_out[1] = sums_lds[1];
+  }
+}
+
 // PRE (one token, KSW = 1): the activation slice is not loaded but made by the block: wave 0 redoes
 // the reduce step of the previous projection (`pre` with epilogue PRE_EPI, pre_splits K splits,
 // kFuseNormQuant on a 1536-wide row) for token 0 straight into the slice, once the block's weight
 // loads are in flight; block 0 alone writes the finished row (pre.y, pre.y_raw).  K chunk c of the
 // slice is the token's row c.  PRE_QUANT (one token, KSW = 1): the slice is the two-limb code of the
 // fp32 row pre.y (pre.in_dim wide, as norm_quant_kernel without a norm), made by every block for its
-// own K chunks; block 0 writes the row's scale and limb sums to pre.sx_out / pre.sums_out.
+// own K chunks; block 0 writes the row's scale and limb sums to pre.sx_out / pre.sums_out.  PRE_ATTN
+// (one token, KSW = 1, the 1536-wide context row): every block merges the decode attention's split
+// partials (am) and quantizes the row into the slice; block 0 writes its scale and limb sums.
 template <int RTW, bool DUAL, int EPI, int NKC, bool ROPE, int KSW, bool PRE, int PRE_EPI = kEpiStore,
-          bool PRE_QUANT = false>
+          bool PRE_QUANT = false, bool PRE_ATTN = false>
 __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count, int rg_count, int splits,
-                                                 const GemmArgs& pre, int pre_splits) {
+                                                 const GemmArgs& pre, int pre_splits,
+                                                 const AttnMergeArgs& am = AttnMergeArgs{}) {
   constexpr int D = DUAL ? 2 : 1;
   static_assert(!PRE || (KSW == 1 && NKC * kKChunk == QWEN_HIDDEN), "PRE: one K group over a 1536-wide row");
   static_assert(!PRE_QUANT || (KSW == 1 && !PRE), "PRE_QUANT: one K group");
+  static_assert(!PRE_ATTN || (KSW == 1 && !PRE && !PRE_QUANT && NKC * kKChunk == QWEN_HIDDEN),
+                "PRE_ATTN: one K group over the 1536-wide context row");
+  constexpr bool kMade = PRE || PRE_QUANT || PRE_ATTN;  // the slice is made by the block
   constexpr int KC = NKC / KSW;  // K chunks per wave group
   static_assert(NKC % KSW == 0, "K chunks split evenly over the wave groups");
   static_assert(RTW * D * 8 * 1024 <= NKC * 16 * 256 || KSW == 1, "K-group reduction fits the slice buffer");
@@ -919,7 +995,7 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   const size_t row_stride_x = (size_t)a.in_dim * 2u;
 
   // activation slice -> LDS: chunk c, rows 4q..4q+3 per load (1 KiB), wave w takes chunks w, w+4KSW, ..
-  for (int c = threadIdx.x >> 6; c < (PRE || PRE_QUANT ? 0 : NKC); c += 4 * KSW) {
+  for (int c = threadIdx.x >> 6; c < (kMade ? 0 : NKC); c += 4 * KSW) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int row = 4 * q + (lane >> 4);
@@ -952,6 +1028,7 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   __builtin_amdgcn_sched_barrier(0);  // every load above is in flight before any use (one round trip)
   __shared__ float pre_sx;
   __shared__ int pre_sums[2];
+  if constexpr (PRE_ATTN) attn_merge_quant_slice(am, xs, 16 * 256, &pre_sx, pre_sums, blockIdx.x == 0);
   if constexpr (PRE_QUANT) {
     // token 0's row of the slice: K chunks kc0 .. kc0 + NKC - 1 (row 0 of each chunk, unswizzled)
     quant_row_slice<kQuantVecs>(pre.y, pre.in_dim, kc0, NKC, xs, 16 * 256, &pre_sx, pre_sums,
@@ -1030,7 +1107,7 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   // epilogue: lane holds rows 16*rt + 4g + q (q < 4) of token tok0 + col
   const int tok = tok0 + col;
   if (tok >= a.tokens) return;
-  const double sx = (double)(PRE || PRE_QUANT ? pre_sx : a.sx[tok]);
+  const double sx = (double)(kMade ? pre_sx : a.sx[tok]);
   const bool partial = splits > 1 || (!DUAL && !ROPE && a.fuse != kFuseNone);
   if (partial) {
 #pragma unroll
@@ -1046,8 +1123,8 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
     }
     return;
   }
-  const int sh8 = 8 * (PRE || PRE_QUANT ? pre_sums[0] : a.sums[2 * tok]);
-  const int sl8 = 8 * (PRE || PRE_QUANT ? pre_sums[1] : a.sums[2 * tok + 1]);
+  const int sh8 = 8 * (kMade ? pre_sums[0] : a.sums[2 * tok]);
+  const int sl8 = 8 * (kMade ? pre_sums[1] : a.sums[2 * tok + 1]);
   float y[RTW][4];
 #pragma unroll
   for (int r = 0; r < RTW; ++r) {
@@ -1125,6 +1202,13 @@ gemm_skinny_kernel(GemmArgs a, int tt_count, int rg_count, int splits) {
 template <int RTW, int EPI, int NKC>
 __global__ void __launch_bounds__(256) gemm_skinny_preq_kernel(GemmArgs a, int rg_count, int splits, GemmArgs pre) {
   gemm_skinny_body<RTW, false, EPI, NKC, false, 1, false, kEpiStore, true>(a, 1, rg_count, splits, pre, 0);
+}
+
+// One token whose activation row is the decode attention's context: every block merges the split
+// partials and quantizes the row (see PRE_ATTN above).
+template <int RTW, int EPI, int NKC>
+__global__ void __launch_bounds__(256) gemm_skinny_prea_kernel(GemmArgs a, int rg_count, AttnMergeArgs am) {
+  gemm_skinny_body<RTW, false, EPI, NKC, false, 1, false, kEpiStore, false, true>(a, 1, rg_count, 1, a, 0, am);
 }
 
 // One token, with the previous projection's reduce step redone by every block (see PRE above).
@@ -1491,7 +1575,8 @@ __global__ void __launch_bounds__(64) rope_qkv_kernel(float* __restrict__ qkv, i
 // part[b][head][c][128] and pml[b][head][c] with device-coherent stores and counts itself in
 // arrivals[b]; the last of the sequence's 2*nsplit blocks to arrive merges the sequence's splits
 // into ctx[b] (optional), quantizes that row for the O projection (xq, sx, sums) and re-arms
-// arrivals[b] to 0 for the next launch.
+// arrivals[b] to 0 for the next launch.  With xq == nullptr the launch ends after the partials (the
+// O projection of a one-sequence decode merges them in every block: attn_merge_quant_slice).
 // ---------------------------------------------------------------------------------------------
 typedef float v4f __attribute__((ext_vector_type(4)));
 constexpr int kQRow = QWEN_HEAD_DIM + 4;  // LDS floats per query row (16-byte pad: no bank aliasing)
@@ -1696,6 +1781,8 @@ attn_decode_kernel(const float* __restrict__ qkv, int qkv_stride, const float* _
       }
     }
   }
+
+  if (xq == nullptr) return;  // partials only: the next launch merges them
 
   // Arrival.  The partials were written with device-coherent (agent-scope) stores; once every wave
   // has waited for its stores to complete, they are visible to every XCD, and one thread counts the
@@ -2204,6 +2291,18 @@ bool launch_gemm_i8_pre(const GemmArgs& a, const GemmArgs& pre, int pre_epi, int
     return true;
   }
   return false;
+}
+
+bool launch_gemm_i8_prea(const GemmArgs& a, const AttnMergeArgs& am, hipStream_t st) {
+  if (a.tokens != 1 || a.in_dim != QWEN_HIDDEN || a.out_dim != QWEN_HIDDEN || a.wp2 || !a.part ||
+      a.fuse != kFuseNormQuant || !am.part || !am.pml || !am.pos || !am.sx_out || !am.sums_out || am.nsplit < 1 ||
+      am.nsplit > kAttnMaxSplits || am.chunk < 1)
+    return false;
+  const int rg_count = a.out_dim / 64;
+  hipLaunchKernelGGL((gemm_skinny_prea_kernel<1, kEpiStore, 12>), dim3(8 * ((rg_count + 7) / 8)), dim3(256), 0, st, a,
+                     rg_count, am);
+  if (!a.defer_reduce) launch_reduce<kEpiStore>(a, 1, st);
+  return true;
 }
 
 bool launch_gemm_i8_preq(const GemmArgs& a, const GemmArgs& pre, hipStream_t st) {

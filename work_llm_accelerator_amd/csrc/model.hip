@@ -301,8 +301,9 @@ struct qwen_hip_model {
         gemm(w, B, QWEN_HIDDEN, (int)kQkvRows, f.qkv, f.sw_qkv, f.b_qkv, w.qkv, kQkvRows, kEpiStore);
         launch_rope_qkv(w.qkv, (int)kQkvRows, pos, 1, 0, max_keys, B, rope_decode, kc, vc, ss, stream);
       }
+      // one sequence: the attention leaves its split partials, merged by every block of the O projection
       launch_attn_decode(w.qkv, (int)kQkvRows, kc, vc, ss, pos, B, max_keys, plan, w.part, w.pml, w.arrivals,
-                         nullptr, w.xq, w.sx, w.sums, stream);
+                         nullptr, one ? nullptr : w.xq, w.sx, w.sums, stream);
       GemmArgs fn{};
       fn.fuse = kFuseNormQuant;
       fn.norm = kNormDecode;
@@ -318,7 +319,8 @@ struct qwen_hip_model {
         const GemmArgs oa = args(w, B, QWEN_HIDDEN, QWEN_HIDDEN, f.o, f.sw_o, nullptr, w.att, QWEN_HIDDEN, nullptr,
                                  nullptr, nullptr, 0, 0, &fn);
         fn.defer_reduce = 0;
-        launch_gemm_i8(oa, kEpiStore, stream);
+        const AttnMergeArgs am{w.part, w.pml, pos, plan.nsplit, plan.chunk, max_keys, w.sx, w.sums};
+        if (!launch_gemm_i8_prea(oa, am, stream)) throw std::runtime_error("O with the attention merge: bad shape");
         const GemmArgs ga = args(w, B, QWEN_HIDDEN, QWEN_INTERMEDIATE, f.gate, f.sw_gate, nullptr, w.s,
                                  QWEN_INTERMEDIATE, f.up, f.sw_up);
         if (!launch_gemm_i8_pre(ga, oa, kEpiStore, 1, stream))
