@@ -1025,6 +1025,27 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
       for (int c = 0; c < KC; ++c) wv[r][d][c] = wp[(size_t)c * 64u];  // cached: reused by the XCD's other token tiles
     }
   }
+  // the epilogue's per-row scales (and bias) and per-token scale and limb sums, in flight with the
+  // weights: none depends on the MFMAs, and loaded after them they would cost one more round trip
+  float swv[RTW][4], sw2v[RTW][4], biasv[RTW][4];
+#pragma unroll
+  for (int r = 0; r < RTW; ++r) {
+    const int row0 = (ok[r] ? rg * 4 * RTW + wave + 4 * r : 0) * 16 + 4 * g;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      swv[r][q] = a.sw[row0 + q];
+      sw2v[r][q] = DUAL ? a.sw2[row0 + q] : 0.0f;
+      biasv[r][q] = (EPI == kEpiStore && !DUAL && a.bias) ? a.bias[row0 + q] : 0.0f;
+    }
+  }
+  const int tok_l = min(tok0 + col, a.tokens - 1);
+  float sx_l = 0.0f;
+  int sh_l = 0, sl_l = 0;
+  if constexpr (!(PRE || PRE_QUANT || PRE_ATTN)) {
+    sx_l = a.sx[tok_l];
+    sh_l = a.sums[2 * tok_l];
+    sl_l = a.sums[2 * tok_l + 1];
+  }
   __builtin_amdgcn_sched_barrier(0);  // every load above is in flight before any use (one round trip)
   __shared__ float pre_sx;
   __shared__ int pre_sums[2];
@@ -1107,7 +1128,7 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   // epilogue: lane holds rows 16*rt + 4g + q (q < 4) of token tok0 + col
   const int tok = tok0 + col;
   if (tok >= a.tokens) return;
-  const double sx = (double)(kMade ? pre_sx : a.sx[tok]);
+  const double sx = (double)(kMade ? pre_sx : sx_l);
   const bool partial = splits > 1 || (!DUAL && !ROPE && a.fuse != kFuseNone);
   if (partial) {
 #pragma unroll
@@ -1117,14 +1138,14 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
       float out[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q)
-        out[q] = (float)(((double)accH[r][0][q] * 256.0 + (double)accL[r][0][q]) * sx) * a.sw[row0 + q];
+        out[q] = (float)(((double)accH[r][0][q] * 256.0 + (double)accL[r][0][q]) * sx) * swv[r][q];
       *reinterpret_cast<float4*>(a.part + ((size_t)z * a.tokens + tok) * a.out_dim + row0) =
           make_float4(out[0], out[1], out[2], out[3]);
     }
     return;
   }
-  const int sh8 = 8 * (kMade ? pre_sums[0] : a.sums[2 * tok]);
-  const int sl8 = 8 * (kMade ? pre_sums[1] : a.sums[2 * tok + 1]);
+  const int sh8 = 8 * (kMade ? pre_sums[0] : sh_l);
+  const int sl8 = 8 * (kMade ? pre_sums[1] : sl_l);
   float y[RTW][4];
 #pragma unroll
   for (int r = 0; r < RTW; ++r) {
@@ -1136,16 +1157,16 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
         continue;
       }
       const double tot = (double)(accH[r][0][q] - sh8) * 256.0 + (double)(accL[r][0][q] - sl8);
-      const float v = (float)(tot * sx) * a.sw[row0 + q];
+      const float v = (float)(tot * sx) * swv[r][q];
       if (EPI == kEpiSiluMul) {
         const double tot2 = (double)(accH[r][D - 1][q] - sh8) * 256.0 + (double)(accL[r][D - 1][q] - sl8);
-        const float u = (float)(tot2 * sx) * a.sw2[row0 + q];
+        const float u = (float)(tot2 * sx) * sw2v[r][q];
         const float sg = a.prefill_silu ? silu_prefill(v) : silu_decode(v);
         y[r][q] = sg * u;
       } else if (EPI == kEpiResidual) {
         y[r][q] = a.resid[(size_t)tok * a.resid_stride + row0 + q] + v;
       } else {
-        y[r][q] = v + (a.bias ? a.bias[row0 + q] : 0.0f);
+        y[r][q] = v + biasv[r][q];
       }
     }
   }
