@@ -98,10 +98,22 @@ __global__ void __launch_bounds__(64) repack_int4_kernel(const uint8_t* __restri
 // ---------------------------------------------------------------------------------------------
 // Block reductions (256 threads = 4 waves of 64).
 // ---------------------------------------------------------------------------------------------
+// Max and integer sum do not depend on the order of the operations, so they reduce each row of 16
+// lanes with DPP moves (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_ror:4, row_ror:8: every lane
+// ends with its row's result) and combine the four rows from v_readlane, instead of six LDS
+// permutes.  Float and double sums keep the xor butterfly (their rounding depends on the order).
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  v = fmaxf(v, __int_as_float(dpp_i<0xB1>(__float_as_int(v))));
+  v = fmaxf(v, __int_as_float(dpp_i<0x4E>(__float_as_int(v))));
+  v = fmaxf(v, __int_as_float(dpp_i<0x124>(__float_as_int(v))));
+  v = fmaxf(v, __int_as_float(dpp_i<0x128>(__float_as_int(v))));
+  const int b = __float_as_int(v);
+  return fmaxf(fmaxf(__int_as_float(__builtin_amdgcn_readlane(b, 0)), __int_as_float(__builtin_amdgcn_readlane(b, 16))),
+               fmaxf(__int_as_float(__builtin_amdgcn_readlane(b, 32)), __int_as_float(__builtin_amdgcn_readlane(b, 48))));
 }
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -114,9 +126,12 @@ __device__ __forceinline__ double wave_sum_d(double v) {
   return v;
 }
 __device__ __forceinline__ int wave_sum_i(int v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  v += dpp_i<0xB1>(v);
+  v += dpp_i<0x4E>(v);
+  v += dpp_i<0x124>(v);
+  v += dpp_i<0x128>(v);
+  return (__builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16)) +
+         (__builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48));
 }
 
 // Reductions over the 4 waves of a 256-thread block; every thread receives the result.
@@ -814,18 +829,22 @@ __global__ void __launch_bounds__(256 * TW) __attribute__((amdgpu_waves_per_eu(W
 // wave w holds rows p and p + 64 of head rg, p = 16w + 4g + q).
 // grid = 8 * tt_count * ceil(groups / 8) blocks of 256, groups = row groups x splits.
 // ---------------------------------------------------------------------------------------------
-template <int EPI>
+struct NoIssue {
+  __device__ void operator()() const {}
+};
+template <int EPI, class Issue = NoIssue>
 __device__ __forceinline__ void reduce_norm_quant_row(const GemmArgs& a, int splits, int tok, int8_t* xq_row,
-                                                      int chunk_stride, float* sx_out, int* sums_out, bool write_y);
+                                                      int chunk_stride, float* sx_out, int* sums_out, bool write_y,
+                                                      Issue&& issue = Issue{});
 
 // Two-limb quantization of one fp32 row x[0, n) (n % 4 == 0, n <= NV * 1024) by a 256-thread block
 // with norm_quant_row's arithmetic and thread mapping (float4 k = t + 256 j): the code of K chunks
 // kc0 .. kc0 + nkc - 1 goes to xs (chunk kc0 + i at byte i * chunk_stride), the scale and limb sums of
 // the whole row to sx_lds / sums_lds and, when sx_g is given, to sx_g / sums_g.
-template <int NV>
+template <int NV, class Issue>
 __device__ __forceinline__ void quant_row_slice(const float* __restrict__ x, int n, int kc0, int nkc, uint8_t* xs,
                                                 int chunk_stride, float* sx_lds, int* sums_lds, float* sx_g,
-                                                int* sums_g) {
+                                                int* sums_g, Issue&& issue) {
   __shared__ float red_f[4];
   __shared__ int red_i[4];
   const int n4 = n >> 2;
@@ -836,6 +855,9 @@ __device__ __forceinline__ void quant_row_slice(const float* __restrict__ x, int
     const int k = threadIdx.x + 256 * j;
     v[j] = k < n4 ? x4[k] : make_float4(0, 0, 0, 0);
   }
+  __builtin_amdgcn_sched_barrier(0);
+  issue();  // the caller's loads queue behind the row's
+  __builtin_amdgcn_sched_barrier(0);
   float amax = 0.0f;
 #pragma unroll
   for (int j = 0; j < NV; ++j)
@@ -885,36 +907,58 @@ __device__ __forceinline__ void quant_row_slice(const float* __restrict__ x, int
 
 // The merge of one sequence's split-KV decode-attention partials, in the arithmetic and order of
 // attn_decode_kernel's merge (per head: max of the split maxima, exp-weights normalised by the
-// weighted sum, then the weighted sum of the split partial rows), followed by quantize_row_lds of the
-// context row into token 0's row of a skinny-GEMM slice (K chunk c at xs + c * chunk_stride).  The
+// weighted sum, then the weighted sum of the split partial rows), followed by quantize_row_lds's
+// quantization of the context row (from registers) into token 0's row of a skinny-GEMM slice (K chunk c at xs + c * chunk_stride).  The
 // partials come from the previous launch, so plain loads see them.  256 threads.
+template <class Issue>
 __device__ __forceinline__ void attn_merge_quant_slice(const AttnMergeArgs& am, uint8_t* xs, int chunk_stride,
-                                                       float* sx_lds, int* sums_lds, bool write_global) {
+                                                       float* sx_lds, int* sums_lds, bool write_global,
+                                                       Issue&& issue) {
   __shared__ float ml[QWEN_Q_HEADS * kAttnMaxSplits * 2];  // (m, l) per head and split, then merge weights
-  __shared__ float row[QWEN_HIDDEN];
   __shared__ float red_f[4];
   __shared__ int red_i[4];
-  const int n = min(max(am.pos[0], 0) + 1, am.max_keys);
-  const int nc = (n + am.chunk - 1) / am.chunk;  // splits that hold keys
+  // The loads do not wait for the position: the first kFirst splits' partials and every (m, l) pair
+  // are loaded whatever the key count; the merge below reads only the splits that hold keys.  Thread
+  // t owns float4 f = t and t + 256 (f < 384) of the context row: head f >> 5, dims 4 (f & 31) .. + 3;
+  // 16-byte loads keep a wave's outstanding loads (with the caller's weights) under the counter's 63.
+  constexpr int kFirst = 16;  // one-sequence plans use at most 24 splits
   const int nsplit = am.nsplit;
-  const int d = threadIdx.x & 127;
-  const int h0 = threadIdx.x >> 7;
-  const float* pa = am.part + d;
-  const float* pb = reinterpret_cast<const float*>(am.pml);
-  float pv[6][8];
+  float4 pv[2][kFirst];
   auto load_part = [&](int s0) {
 #pragma unroll
-    for (int k = 0; k < 6; ++k)
+    for (int u = 0; u < 2; ++u) {
+      const int f = threadIdx.x + 256 * u;
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        pv[k][j] = s0 + j < nc ? pa[((size_t)(h0 + 2 * k) * nsplit + s0 + j) * QWEN_HEAD_DIM] : 0.0f;
+      for (int j = 0; j < kFirst; ++j)
+        pv[u][j] = (f < QWEN_HIDDEN / 4 && s0 + j < nsplit)
+                       ? *reinterpret_cast<const float4*>(am.part + ((size_t)(f >> 5) * nsplit + s0 + j) * QWEN_HEAD_DIM +
+                                                          4 * (f & 31))
+                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
   };
+  const int p0 = am.pos[0];
   load_part(0);
-  for (int i = threadIdx.x; i < QWEN_Q_HEADS * nc; i += 256) {
-    const int h = i / nc, sp = i % nc;
-    ml[(h * kAttnMaxSplits + sp) * 2] = pb[2 * (h * nsplit + sp)];
-    ml[(h * kAttnMaxSplits + sp) * 2 + 1] = pb[2 * (h * nsplit + sp) + 1];
+  constexpr int kMlPer = (QWEN_Q_HEADS * kAttnMaxSplits + 255) / 256;  // (m, l) pairs per thread, at most
+  float2 mlv[kMlPer];
+#pragma unroll
+  for (int u = 0; u < kMlPer; ++u) {
+    const int i = threadIdx.x + 256 * u;
+    mlv[u] = i < QWEN_Q_HEADS * nsplit ? am.pml[i] : make_float2(0.0f, 0.0f);  // pml[h][sp] at h * nsplit + sp
   }
+  __builtin_amdgcn_sched_barrier(0);
+  issue();  // the caller's loads queue behind the partials
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int u = 0; u < kMlPer; ++u) {
+    const int i = threadIdx.x + 256 * u;
+    if (i < QWEN_Q_HEADS * nsplit) {
+      const int h = i / nsplit, sp = i % nsplit;
+      ml[(h * kAttnMaxSplits + sp) * 2] = mlv[u].x;
+      ml[(h * kAttnMaxSplits + sp) * 2 + 1] = mlv[u].y;
+    }
+  }
+  const int n = min(max(p0, 0) + 1, am.max_keys);
+  const int nc = (n + am.chunk - 1) / am.chunk;  // splits that hold keys (the rest hold stale values)
   __syncthreads();
   if (threadIdx.x < QWEN_Q_HEADS) {
     float* mh = ml + threadIdx.x * kAttnMaxSplits * 2;
@@ -930,25 +974,68 @@ __device__ __forceinline__ void attn_merge_quant_slice(const AttnMergeArgs& am, 
     for (int sp = 0; sp < nc; ++sp) mh[2 * sp] *= inv;  // merge weight of split sp
   }
   __syncthreads();
-  float out[6];
-#pragma unroll
-  for (int k = 0; k < 6; ++k) out[k] = 0.0f;
-  for (int s0 = 0; s0 < nc; s0 += 8) {
+  float4 out[2] = {make_float4(0.0f, 0.0f, 0.0f, 0.0f), make_float4(0.0f, 0.0f, 0.0f, 0.0f)};
+  for (int s0 = 0; s0 < nc; s0 += kFirst) {
     if (s0 > 0) load_part(s0);
 #pragma unroll
-    for (int k = 0; k < 6; ++k)
+    for (int u = 0; u < 2; ++u) {
+      const int f = threadIdx.x + 256 * u;
+      if (f < QWEN_HIDDEN / 4) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        if (s0 + j < nc) out[k] += pv[k][j] * ml[((h0 + 2 * k) * kAttnMaxSplits + s0 + j) * 2];
+        for (int j = 0; j < kFirst; ++j)
+          if (s0 + j < nc) {
+            const float w = ml[((f >> 5) * kAttnMaxSplits + s0 + j) * 2];
+            out[u].x += pv[u][j].x * w;
+            out[u].y += pv[u][j].y * w;
+            out[u].z += pv[u][j].z * w;
+            out[u].w += pv[u][j].w * w;
+          }
+      }
+    }
   }
+  // quantize_row_lds's arithmetic on the thread's own float4s, straight from registers
+  float amax = 0.0f;
 #pragma unroll
-  for (int k = 0; k < 6; ++k) row[(h0 + 2 * k) * QWEN_HEAD_DIM + d] = out[k];
-  __syncthreads();
-  quantize_row_lds(row, QWEN_HIDDEN, reinterpret_cast<int8_t*>(xs), sx_lds, sums_lds, red_f, red_i, chunk_stride);
-  if (write_global && threadIdx.x == 0) {
-    *am.sx_out = *sx_lds;
-    am.sums_out[0] = sums_lds[0];
-    am.sums_out[1] = sums_lds[1];
+  for (int u = 0; u < 2; ++u)
+    if (threadIdx.x + 256 * u < QWEN_HIDDEN / 4)
+      amax = fmaxf(amax, fmaxf(fmaxf(fabsf(out[u].x), fabsf(out[u].y)), fmaxf(fabsf(out[u].z), fabsf(out[u].w))));
+  amax = block_max4(amax, red_f);
+  const float inv = amax > 0.0f ? (float)kQuantMax / amax : 0.0f;
+  int sh = 0, sl = 0;
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int f = threadIdx.x + 256 * u;
+    if (f < QWEN_HIDDEN / 4) {
+      const float e[4] = {out[u].x, out[u].y, out[u].z, out[u].w};
+      uint32_t hw = 0, lw = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float xf = fminf(fmaxf(rintf(e[q] * inv), -(float)kQuantMax), (float)kQuantMax);
+        const int X = (int)xf;
+        const int H = (X + 128) >> 8;
+        const int L = X - (H << 8);
+        hw |= (uint32_t)(H & 0xFF) << (8 * q);
+        lw |= (uint32_t)(L & 0xFF) << (8 * q);
+        sh += H;
+        sl += L;
+      }
+      uint8_t* dst = xs + ((4 * f) >> 7) * chunk_stride + ((4 * f) & 127);
+      *reinterpret_cast<uint32_t*>(dst) = hw;
+      *reinterpret_cast<uint32_t*>(dst + 128) = lw;
+    }
+  }
+  sh = block_sum4_i(sh, red_i);
+  sl = block_sum4_i(sl, red_i);
+  if (threadIdx.x == 0) {
+    const float sx = amax > 0.0f ? amax / (float)kQuantMax : 1.0f;
+    *sx_lds = sx;
+    sums_lds[0] = sh;
+    sums_lds[1] = sl;
+    if (write_global) {
+      *am.sx_out = sx;
+      am.sums_out[0] = sh;
+      am.sums_out[1] = sl;
+    }
   }
 }
 
@@ -1010,57 +1097,63 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   }
   // decode position of this lane's token (RoPE epilogue), loaded with the weights
   const int P = ROPE ? a.pos[min(tok0 + col, a.tokens - 1)] : 0;
-  // weight tiles -> registers
   uint4 wv[RTW][D][KC];
   bool ok[RTW];
-#pragma unroll
-  for (int r = 0; r < RTW; ++r) {
-    const int rt = rg * 4 * RTW + wave + 4 * r;
-    ok[r] = rt < row_tiles;
-    const size_t base = ((size_t)(ok[r] ? rt : 0) * nkc_all + kc0 + kg * KC) * 64u + lane;
-#pragma unroll
-    for (int d = 0; d < D; ++d) {
-      const uint4* wp = reinterpret_cast<const uint4*>(d ? a.wp2 : a.wp) + base;
-#pragma unroll
-      for (int c = 0; c < KC; ++c) wv[r][d][c] = wp[(size_t)c * 64u];  // cached: reused by the XCD's other token tiles
-    }
-  }
-  // the epilogue's per-row scales (and bias) and per-token scale and limb sums, in flight with the
-  // weights: none depends on the MFMAs, and loaded after them they would cost one more round trip
   float swv[RTW][4], sw2v[RTW][4], biasv[RTW][4];
-#pragma unroll
-  for (int r = 0; r < RTW; ++r) {
-    const int row0 = (ok[r] ? rg * 4 * RTW + wave + 4 * r : 0) * 16 + 4 * g;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      swv[r][q] = a.sw[row0 + q];
-      sw2v[r][q] = DUAL ? a.sw2[row0 + q] : 0.0f;
-      biasv[r][q] = (EPI == kEpiStore && !DUAL && a.bias) ? a.bias[row0 + q] : 0.0f;
-    }
-  }
   const int tok_l = min(tok0 + col, a.tokens - 1);
   float sx_l = 0.0f;
   int sh_l = 0, sl_l = 0;
-  if constexpr (!(PRE || PRE_QUANT || PRE_ATTN)) {
-    sx_l = a.sx[tok_l];
-    sh_l = a.sums[2 * tok_l];
-    sl_l = a.sums[2 * tok_l + 1];
-  }
-  __builtin_amdgcn_sched_barrier(0);  // every load above is in flight before any use (one round trip)
+  // Weight tiles -> registers, then the epilogue's per-row scales (and bias) and per-token scale and
+  // limb sums: none depends on the MFMAs, and loaded after them they would cost one more round trip.
+  // With a made slice (kMade) this runs inside the prologue, after the prologue's own loads: a wave's
+  // loads return in order, so the prologue's few loads must not queue behind the weights.
+  auto issue_loads = [&]() {
+#pragma unroll
+    for (int r = 0; r < RTW; ++r) {
+      const int rt = rg * 4 * RTW + wave + 4 * r;
+      ok[r] = rt < row_tiles;
+      const size_t base = ((size_t)(ok[r] ? rt : 0) * nkc_all + kc0 + kg * KC) * 64u + lane;
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+        const uint4* wp = reinterpret_cast<const uint4*>(d ? a.wp2 : a.wp) + base;
+#pragma unroll
+        for (int c = 0; c < KC; ++c) wv[r][d][c] = wp[(size_t)c * 64u];  // cached: reused by the XCD's other token tiles
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < RTW; ++r) {
+      const int row0 = (ok[r] ? rg * 4 * RTW + wave + 4 * r : 0) * 16 + 4 * g;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        swv[r][q] = a.sw[row0 + q];
+        sw2v[r][q] = DUAL ? a.sw2[row0 + q] : 0.0f;
+        biasv[r][q] = (EPI == kEpiStore && !DUAL && a.bias) ? a.bias[row0 + q] : 0.0f;
+      }
+    }
+    if constexpr (!kMade) {
+      sx_l = a.sx[tok_l];
+      sh_l = a.sums[2 * tok_l];
+      sl_l = a.sums[2 * tok_l + 1];
+    }
+  };
   __shared__ float pre_sx;
   __shared__ int pre_sums[2];
-  if constexpr (PRE_ATTN) attn_merge_quant_slice(am, xs, 16 * 256, &pre_sx, pre_sums, blockIdx.x == 0);
+  if constexpr (PRE_ATTN) attn_merge_quant_slice(am, xs, 16 * 256, &pre_sx, pre_sums, blockIdx.x == 0, issue_loads);
   if constexpr (PRE_QUANT) {
     // token 0's row of the slice: K chunks kc0 .. kc0 + NKC - 1 (row 0 of each chunk, unswizzled)
     quant_row_slice<kQuantVecs>(pre.y, pre.in_dim, kc0, NKC, xs, 16 * 256, &pre_sx, pre_sums,
-                                blockIdx.x == 0 ? pre.sx_out : nullptr, pre.sums_out);
+                                blockIdx.x == 0 ? pre.sx_out : nullptr, pre.sums_out, issue_loads);
   }
   if constexpr (PRE) {
     // token 0's row of the slice: K chunk c at xs + c * 16 * 256 (row 0 of the chunk, unswizzled)
     if (threadIdx.x < 64)
       reduce_norm_quant_row<PRE_EPI>(pre, pre_splits, 0, reinterpret_cast<int8_t*>(xs), 16 * 256, &pre_sx, pre_sums,
-                                     blockIdx.x == 0);
+                                     blockIdx.x == 0, issue_loads);
+    else
+      issue_loads();
   }
+  if constexpr (!kMade) issue_loads();
+  __builtin_amdgcn_sched_barrier(0);  // every load above is in flight before any use
   wait_vmcnt<0>();
   __syncthreads();
 
@@ -1405,9 +1498,11 @@ __global__ void __launch_bounds__(256) reduce_norm_quant_kernel(GemmArgs a, int 
 // goes to xq_row ([K chunk][limb][128 bytes], K chunk c at byte c * chunk_stride: a row of a.xq_out,
 // or a token row of a GEMM's LDS activation slice), the scale and limb sums to sx_out / sums_out;
 // the finished row goes to a.y (and a.y_raw) when write_y.
-template <int EPI>
+// `issue` runs right after the row's loads are issued (a caller's own loads then queue behind them).
+template <int EPI, class Issue>
 __device__ __forceinline__ void reduce_norm_quant_row(const GemmArgs& a, int splits, int tok, int8_t* xq_row,
-                                                      int chunk_stride, float* sx_out, int* sums_out, bool write_y) {
+                                                      int chunk_stride, float* sx_out, int* sums_out, bool write_y,
+                                                      Issue&& issue) {
   constexpr int NV = QWEN_HIDDEN / 256;
   const int lane = threadIdx.x & 63;
   const size_t zstride = (size_t)a.tokens * QWEN_HIDDEN;
@@ -1418,6 +1513,11 @@ __device__ __forceinline__ void reduce_norm_quant_row(const GemmArgs& a, int spl
                                          : reinterpret_cast<const float4*>(a.bias) + lane;
   const bool has_add = EPI == kEpiResidual || a.bias != nullptr;
   const bool has_w = a.norm != kNormNone;
+  // Every load in one batch (a single memory round trip for up to kZB splits): the token's limb sums
+  // and scale, the per-row operands, then the split partials.
+  constexpr int kZB = 5;
+  const int sum_h = a.sums[2 * tok], sum_l = a.sums[2 * tok + 1];
+  const float sx_tok = a.sx[tok];
   float4 acc[NV], sw[NV], ad[NV], wn[NV];
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
@@ -1425,18 +1525,23 @@ __device__ __forceinline__ void reduce_norm_quant_row(const GemmArgs& a, int spl
     ad[j] = has_add ? r4[64 * j] : make_float4(0, 0, 0, 0);
     wn[j] = has_w ? w4[64 * j] : make_float4(0, 0, 0, 0);
   }
-  // split sums in z order, 4 splits per batch of loads
+  // split sums in z order
 #pragma unroll
   for (int j = 0; j < NV; ++j) acc[j] = make_float4(0, 0, 0, 0);
-  for (int z0 = 0; z0 < splits; z0 += 4) {
-    float4 pz[4][NV];
+  for (int z0 = 0; z0 < splits; z0 += kZB) {
+    float4 pz[kZB][NV];
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
+    for (int u = 0; u < kZB; ++u)
 #pragma unroll
       for (int j = 0; j < NV; ++j)
         pz[u][j] = z0 + u < splits ? pt[(size_t)(z0 + u) * (zstride / 4) + 64 * j] : make_float4(0, 0, 0, 0);
+    if (z0 == 0) {
+      __builtin_amdgcn_sched_barrier(0);
+      issue();
+      __builtin_amdgcn_sched_barrier(0);
+    }
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
+    for (int u = 0; u < kZB; ++u)
       if (z0 + u < splits)
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
@@ -1446,7 +1551,7 @@ __device__ __forceinline__ void reduce_norm_quant_row(const GemmArgs& a, int spl
           acc[j].w += pz[u][j].w;
         }
   }
-  const double corr = -8.0 * (256.0 * (double)a.sums[2 * tok] + (double)a.sums[2 * tok + 1]) * (double)a.sx[tok];
+  const double corr = -8.0 * (256.0 * (double)sum_h + (double)sum_l) * (double)sx_tok;
   float4 v[NV];
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
