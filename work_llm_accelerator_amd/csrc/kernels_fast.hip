@@ -832,6 +832,38 @@ __global__ void __launch_bounds__(256 * TW) __attribute__((amdgpu_waves_per_eu(W
 struct NoIssue {
   __device__ void operator()() const {}
 };
+
+// Elementwise pieces of the reduce step: the split sum plus zero-point correction, residual or bias,
+// optional y_raw / y stores and bf16 rounding of elements row0 .. row0 + 3; the sum of squares of
+// four elements in double; the RMSNorm scaling.
+template <int EPI>
+__device__ __forceinline__ float4 rnq_combine(const GemmArgs& a, int tok, int row0, float4 acc, float4 sw, float4 ad,
+                                              double corr, bool write_y) {
+  const float s4[4] = {sw.x, sw.y, sw.z, sw.w};
+  const float p4[4] = {acc.x, acc.y, acc.z, acc.w};
+  const float d4[4] = {ad.x, ad.y, ad.z, ad.w};
+  float out[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float val = p4[q] + (float)(corr * (double)s4[q]);
+    out[q] = EPI == kEpiResidual ? d4[q] + val : val + d4[q];
+  }
+  if (EPI == kEpiResidual && a.y_raw && write_y)
+    *reinterpret_cast<float4*>(a.y_raw + (size_t)tok * a.y_stride + row0) = make_float4(out[0], out[1], out[2], out[3]);
+  if (EPI == kEpiResidual && a.round_bf16)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) out[q] = round_bf16(out[q]);
+  const float4 v = make_float4(out[0], out[1], out[2], out[3]);
+  if (write_y) *reinterpret_cast<float4*>(a.y + (size_t)tok * a.y_stride + row0) = v;
+  return v;
+}
+__device__ __forceinline__ double rnq_sq4(float4 v) {
+  return (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
+}
+__device__ __forceinline__ float4 rnq_norm4(float4 v, double inv, float4 w) {
+  return make_float4((float)((double)v.x * inv * w.x), (float)((double)v.y * inv * w.y),
+                     (float)((double)v.z * inv * w.z), (float)((double)v.w * inv * w.w));
+}
 template <int EPI, class Issue = NoIssue>
 __device__ __forceinline__ void reduce_norm_quant_row(const GemmArgs& a, int splits, int tok, int8_t* xq_row,
                                                       int chunk_stride, float* sx_out, int* sums_out, bool write_y,
@@ -1554,37 +1586,17 @@ __device__ __forceinline__ void reduce_norm_quant_row(const GemmArgs& a, int spl
   const double corr = -8.0 * (256.0 * (double)sum_h + (double)sum_l) * (double)sx_tok;
   float4 v[NV];
 #pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    const int row0 = 4 * (lane + 64 * j);
-    const float s4[4] = {sw[j].x, sw[j].y, sw[j].z, sw[j].w};
-    const float p4[4] = {acc[j].x, acc[j].y, acc[j].z, acc[j].w};
-    const float d4[4] = {ad[j].x, ad[j].y, ad[j].z, ad[j].w};
-    float out[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float val = p4[q] + (float)(corr * (double)s4[q]);
-      out[q] = EPI == kEpiResidual ? d4[q] + val : val + d4[q];
-    }
-    if (EPI == kEpiResidual && a.y_raw && write_y)
-      *reinterpret_cast<float4*>(a.y_raw + (size_t)tok * a.y_stride + row0) = make_float4(out[0], out[1], out[2], out[3]);
-    if (EPI == kEpiResidual && a.round_bf16)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) out[q] = round_bf16(out[q]);
-    v[j] = make_float4(out[0], out[1], out[2], out[3]);
-    if (write_y) *reinterpret_cast<float4*>(a.y + (size_t)tok * a.y_stride + row0) = v[j];
-  }
+  for (int j = 0; j < NV; ++j)
+    v[j] = rnq_combine<EPI>(a, tok, 4 * (lane + 64 * j), acc[j], sw[j], ad[j], corr, write_y);
   // RMSNorm (norm_quant_row's arithmetic, wave reductions)
   if (a.norm == kNormDecode) {
     double ss = 0.0;
 #pragma unroll
-    for (int j = 0; j < NV; ++j)
-      ss += (double)v[j].x * v[j].x + (double)v[j].y * v[j].y + (double)v[j].z * v[j].z + (double)v[j].w * v[j].w;
+    for (int j = 0; j < NV; ++j) ss += rnq_sq4(v[j]);
     ss = wave_sum_d(ss);
     const double inv = 1.0 / sqrt(ss / (double)QWEN_HIDDEN + (double)QWEN_RMS_EPS);
 #pragma unroll
-    for (int j = 0; j < NV; ++j)
-      v[j] = make_float4((float)((double)v[j].x * inv * wn[j].x), (float)((double)v[j].y * inv * wn[j].y),
-                         (float)((double)v[j].z * inv * wn[j].z), (float)((double)v[j].w * inv * wn[j].w));
+    for (int j = 0; j < NV; ++j) v[j] = rnq_norm4(v[j], inv, wn[j]);
   } else if (a.norm == kNormPrefill) {
     float ss = 0.0f;
 #pragma unroll
