@@ -374,7 +374,7 @@ def test_model_prefill_fast_many_seqs(torch, layers2):
         m1.close()
 
 
-@pytest.mark.parametrize("past", [0, 37])
+@pytest.mark.parametrize("past", [0, 37, 1500])
 def test_model_decode_o_reduce_in_gate_up(torch, layers2, model2, past):
     """One sequence: the decode attention's split merge and the context row's quantization run in
     every block of the O projection, the O projection's reduce step (RMSNorm, quantization) in every
@@ -382,13 +382,24 @@ def test_model_decode_o_reduce_in_gate_up(torch, layers2, model2, past):
     and layer 0's down-projection reduce step (residual, bf16 rounding, layer 1's RMSNorm,
     quantization) in every block of layer 1's Q/K/V projection, instead of their own launches; both
     forms must give exactly the same hidden row and K/V cache, over both layers with the driver's
-    bf16 rounding, for two calls in a row."""
+    bf16 rounding, for two calls in a row.  1500 keys: 24 attention splits, so the O blocks' merge
+    loads its partials in two batches (16 + 8); its first call is also checked against the oracle."""
     from work_llm_accelerator_amd.model import FLAG_SEPARATE_REDUCE, MODE_FAST
 
     print(f"model decode fast O reduce in gate/up past={past}", flush=True)
+    if past > 1000:
+        cache, hist, x = decode_setup(torch, 2, [past], past + 1, seed=61)
+        hidden = torch.from_numpy(x).cuda()
+        pos = torch.tensor([past], dtype=torch.int32, device="cuda")
+        model2.decode(MODE_FAST, hidden, pos, past + 1, cache)
+        model2.synchronize()
+        kl = [hist[(l, 0)][0].copy() for l in range(2)]
+        vl = [hist[(l, 0)][1].copy() for l in range(2)]
+        ref = oracle_decode(layers2, x[0], past, kl, vl)
+        assert rel_err(hidden.cpu().numpy()[0], ref) <= FAST_TOL_ROUNDED
     outs = []
     for flag in (0, FLAG_SEPARATE_REDUCE):
-        cache, _, x = decode_setup(torch, 2, [past], 48, seed=61)
+        cache, _, x = decode_setup(torch, 2, [past], max(48, past + 1), seed=61)
         hidden = torch.from_numpy(x).cuda()
         pos = torch.tensor([past], dtype=torch.int32, device="cuda")
         for _ in range(2):
