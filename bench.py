@@ -277,7 +277,7 @@ def bench_greedy(args, torch, prompt: int, seed: int) -> dict:
     model.synchronize()
     head_ms = e0.elapsed_time(e1) / reps
     head_bytes = table_bytes + 1536 * 4 + 1536 * 2
-    res["roofline"] = {"bound": "hbm", "kernel": "lm_head_kernel (with head_norm_kernel and argmax_finalize_kernel)",
+    res["roofline"] = {"bound": "hbm", "kernel": "lm_head_row_kernel (with head_norm_kernel and argmax_finalize_kernel)",
                        "achieved": head_bytes / (head_ms * 1e-3) / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                        "frac": head_bytes / (head_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "traffic": None,
                        "avg_launch_us": head_ms * 1e3, "algorithmic_bytes_per_launch": head_bytes}

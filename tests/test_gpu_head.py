@@ -91,7 +91,9 @@ def test_head_small_vocab(torch, count):
         m.close()
 
 
-def test_head_full_vocab(torch):
+@pytest.mark.parametrize("count", [1, 2])
+def test_head_full_vocab(torch, count):
+    """count 1: the one-token row-streaming kernel; 2: the MFMA kernel."""
     from work_llm_accelerator_amd.model import DeviceModel
 
     rng = np.random.default_rng(151936)
@@ -101,7 +103,7 @@ def test_head_full_vocab(torch):
     m = DeviceModel(1, synthetic_seed=9)
     try:
         m.set_head(table, norm)
-        check_head(torch, m, vocab, table, norm, 2, seed=77)
+        check_head(torch, m, vocab, table, norm, count, seed=77)
     finally:
         m.close()
 

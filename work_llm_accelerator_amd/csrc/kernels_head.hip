@@ -187,6 +187,88 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) l
   }
 }
 
+// One token (greedy decode): each logit as a dot product on the VALU, so that every load reads 1 KiB of
+// one table row (lm_head_kernel's MFMA A operand reads 64 B of 16 rows per load: 5.0 TB/s).  grid =
+// vocab / 128, block = 256; wave w of block vb takes rows vb*128 + 32w .. + 31, two at a time with the
+// next two rows' loads in flight.  Lane l holds x[8l + 512j .. + 7] (j < 3) in fp32 and forms its 24
+// products of a row in (j, e) order; the 64 lane sums are added by DPP row steps, then the four rows in
+// lane order.  Logits are rounded to bf16 and keyed as in lm_head_kernel (best[0][vb]).
+template <bool LOGITS>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5)))
+lm_head_row_kernel(const uint16_t* __restrict__ table, int vocab, const uint16_t* __restrict__ xn,
+                   float* __restrict__ logits, unsigned long long* __restrict__ best) {
+  __shared__ unsigned long long red[4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row0 = blockIdx.x * (2 * kHeadBlockRows) + wave * 32;
+  constexpr int kRowU4 = QWEN_HIDDEN / 8;  // uint4 per table row
+  float x[3][8];
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    const uint4 q = *reinterpret_cast<const uint4*>(xn + 8 * lane + 512 * j);
+    const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[j][2 * e] = bits_f32(w4[e] << 16);
+      x[j][2 * e + 1] = bits_f32(w4[e] & 0xFFFF0000u);
+    }
+  }
+  const uint4* tp = reinterpret_cast<const uint4*>(table) + (size_t)row0 * kRowU4 + lane;
+  auto load2 = [&](int r, uint4 (&d)[2][3]) {
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr)
+#pragma unroll
+      for (int j = 0; j < 3; ++j) {
+        const hf32x4 v = __builtin_nontemporal_load(reinterpret_cast<const hf32x4*>(tp + (size_t)(r + rr) * kRowU4 + 64 * j));
+        d[rr][j] = make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3]));
+      }
+  };
+  uint4 cur[2][3], nxt[2][3];
+  load2(0, cur);
+  unsigned long long bk = 0ull;
+#pragma unroll 1
+  for (int r = 0; r < 32; r += 2) {
+    if (r + 2 < 32) load2(r + 2, nxt);
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 3; ++j) {
+        const uint32_t w4[4] = {cur[rr][j].x, cur[rr][j].y, cur[rr][j].z, cur[rr][j].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          acc = fmaf(bits_f32(w4[e] << 16), x[j][2 * e], acc);
+          acc = fmaf(bits_f32(w4[e] & 0xFFFF0000u), x[j][2 * e + 1], acc);
+        }
+      }
+      // row sums of 16 lanes (quad_perm [1,0,3,2], [2,3,0,1], row_ror:4, row_ror:8), then the 4 rows
+      acc += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc), 0xB1, 0xF, 0xF, false));
+      acc += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc), 0x4E, 0xF, 0xF, false));
+      acc += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc), 0x124, 0xF, 0xF, false));
+      acc += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc), 0x128, 0xF, 0xF, false));
+      const int ab = __float_as_int(acc);
+      const float tot = (__int_as_float(__builtin_amdgcn_readlane(ab, 0)) + __int_as_float(__builtin_amdgcn_readlane(ab, 16))) +
+                        (__int_as_float(__builtin_amdgcn_readlane(ab, 32)) + __int_as_float(__builtin_amdgcn_readlane(ab, 48)));
+      const float lf = to_bf16(tot);
+      const uint32_t v = (uint32_t)(row0 + r + rr);
+      const unsigned long long key = ((unsigned long long)order_key(lf) << 32) | (unsigned long long)(~v);
+      bk = key > bk ? key : bk;
+      if (LOGITS && lane == 0) logits[row0 + r + rr] = lf;
+    }
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr)
+#pragma unroll
+      for (int j = 0; j < 3; ++j) cur[rr][j] = nxt[rr][j];
+  }
+  if (lane == 0) red[wave] = bk;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned long long m = red[0];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) m = red[w] > m ? red[w] : m;
+    best[blockIdx.x] = m;
+  }
+}
+
 // ids[t] = the row of the largest key in best[t][0 .. nblk).  grid = count, block = 256.
 __global__ void __launch_bounds__(256) argmax_finalize_kernel(const unsigned long long* __restrict__ best, int nblk,
                                                               int* __restrict__ ids) {
@@ -223,7 +305,11 @@ void launch_head(const float* hidden, int count, const uint16_t* norm_w, const u
   const int nblk = vocab / (2 * kHeadBlockRows);
   const size_t lds = (size_t)(count < 16 ? count : 16) * kHeadRow * 2u;  // live token rows of a tile
   hipLaunchKernelGGL(head_norm_kernel, dim3(tiles * 16), dim3(256), 0, st, hidden, count, norm_w, xn);
-  if (logits)
+  if (count == 1 && logits)
+    hipLaunchKernelGGL(lm_head_row_kernel<true>, dim3(nblk), dim3(256), 0, st, table, vocab, xn, logits, best);
+  else if (count == 1)
+    hipLaunchKernelGGL(lm_head_row_kernel<false>, dim3(nblk), dim3(256), 0, st, table, vocab, xn, logits, best);
+  else if (logits)
     hipLaunchKernelGGL(lm_head_kernel<true>, dim3(nblk, tiles), dim3(256), lds, st, table, vocab, xn, count, logits,
                        best);
   else
