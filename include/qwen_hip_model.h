@@ -73,6 +73,15 @@ int qwen_hip_model_create_synthetic(int layers, uint64_t seed, qwen_hip_model** 
 
 int qwen_hip_model_destroy(qwen_hip_model* m);
 int qwen_hip_model_layers(const qwen_hip_model* m);
+
+/* Copies layer `layer`'s DDR images back to host memory: weight_ddr receives QWEN_LAYER_BYTES bytes
+ * and scale_ddr QWEN_LAYER_BYTES/4 words (the per-layer block of llm_memory_layout.h:84-128), e.g. to
+ * run a synthetic model's layers through the reference host library.  Synchronizes the model. */
+int qwen_hip_model_layer_images(qwen_hip_model* m, int layer, uint8_t* weight_ddr, float* scale_ddr);
+
+/* Copies the tied bf16 embedding / lm_head table [vocab][1536] and the bf16 final RMSNorm weight
+ * [1536] back to host memory (raw bf16 bit patterns).  Synchronizes the model. */
+int qwen_hip_model_head_tables(qwen_hip_model* m, uint16_t* embed_bf16, uint16_t* norm_bf16);
 /* The model's hipStream_t. */
 void* qwen_hip_model_stream(qwen_hip_model* m);
 int qwen_hip_model_synchronize(qwen_hip_model* m);
@@ -130,7 +139,9 @@ int qwen_hip_model_greedy(qwen_hip_model* m, const float* hidden, int count, int
 
 /* Re-runs one kernel of the most recent decode/prefill call `reps` times in isolation, on the
  * model's stream between two HIP events, with that call's shapes and the weights of `layer`;
- * *avg_ms receives the mean duration of one launch. */
+ * *avg_ms receives the mean duration of one launch.  The re-run reads that call's positions and K/V
+ * caches through the pointers it was given, so the caller must keep those buffers allocated until
+ * time_kernel returns (their contents may have changed: only the timing is reported). */
 int qwen_hip_model_time_kernel(qwen_hip_model* m, int kernel, int layer, int reps, float* avg_ms);
 
 /* Device INT4 quantizer (verification/real_host_top_backend.py:31-41): per row

@@ -79,6 +79,16 @@ EXTRA_SIGNATURES: dict[str, tuple[list, object]] = {
     "qwen_hip_quantize_int4": ([P, c_int, c_int, P, P, P], c_int),
     "qwen_hip_fill_kv_synthetic": ([P, c_u64, c_u64, P], c_int),
     "qwen_hip_eval_expf": ([ctypes.c_uint32, ctypes.c_uint32, c_u64, P, P], c_int),
+    "qwen_hip_model_layer_images": ([P, c_int, U8P, F32P], c_int),
+    "qwen_hip_model_head_tables": ([P, np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS"),
+                                    np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")], c_int),
+    # FAST operators (include/qwen_hip_ops.h)
+    "qwen_hip_fast_quantize_rows": ([P, c_int, c_int, P, P, P, P], c_int),
+    "qwen_hip_fast_project": ([P, P, P, c_int, c_int, P, c_int, c_int, P, P], c_int),
+    # device-resident descriptor dispatch (include/qwen_hip_dispatch.h): descriptors on the host,
+    # DDR images on the device
+    "qwen_hip_decode_dispatch_layers": ([c_void_p, c_int, P, P, P, P, P, c_void_p], c_int),
+    "qwen_hip_prefill_dispatch_layers": ([c_void_p, c_int, P, P, P, P, P, c_void_p], c_int),
 }
 
 _LIB: ctypes.CDLL | None = None

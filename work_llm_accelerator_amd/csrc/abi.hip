@@ -19,6 +19,7 @@
 #include "qwen_device_math.hpp"
 #include "qwen_prefill_host_wrapper.h"
 #include "runtime.hpp"
+#include "tops.hpp"
 
 using namespace qwen;
 
@@ -190,7 +191,7 @@ int qwen_decode_stub_forward(const float* x, int past, float* out) {
 static int decode_top(const qwen_decode_descriptor& dsc, const uint8_t* wd, const float* sd, float* kv, float* act,
                       const void* s0, const void* s1, const void* s2, const void* s3, const void* s4) {
   // qwen_decode_top_wrapper.cpp:31-38
-  if (!qwen_valid_layer_id(dsc.layer_id) || dsc.past_seq_len < 0) return QWEN_ERR_DECODE_DESC;
+  if (const int st = decode_descriptor_status(dsc)) return st;
   if (any_null({wd, sd, kv, act, s0, s1, s2, s3, s4})) return QWEN_ERR_DECODE_PORT;
   const HostLayer h = resolve_host_layer(wd, sd, dsc.layer_weights_base_addr, dsc.layer_scales_base_addr);
   const float* x = act + dsc.input_token_addr / 4;
@@ -238,27 +239,6 @@ qwen_prefill_attention_tiles atiles(int a_seq, int a_query, int a_key, int a_hp,
   return qwen_prefill_attention_tiles{a_seq, a_query, a_key, a_hp, a_kvp, a_hd, a_qhp, a_kvhp};
 }
 
-// qwen_prefill_attention_kernel.cpp:2252-2268 (pointer checks done by the caller).
-int check_prefill_attention_tiles(int S, const qwen_prefill_attention_tiles& t) {
-  if (S <= 0 || t.seq <= 0 || t.query <= 0 || t.key <= 0 || t.hidden_proj <= 0 || t.kv_proj <= 0 ||
-      t.head_dim != QWEN_HEAD_DIM || t.query_heads_parallel <= 0 || t.kv_heads_parallel <= 0)
-    return QWEN_ERR_KERNEL;
-  if (S > QWEN_PREFILL_CAPACITY || t.seq > QWEN_PREFILL_CAPACITY || t.query > QWEN_PREFILL_QUERY_CAPACITY ||
-      t.key > QWEN_PREFILL_KEY_CAPACITY || t.hidden_proj > QWEN_PREFILL_PROJ_CAPACITY ||
-      t.kv_proj > QWEN_PREFILL_PROJ_CAPACITY || t.query_heads_parallel > QWEN_Q_HEADS ||
-      t.kv_heads_parallel > QWEN_KV_HEADS)
-    return QWEN_ERR_CAPACITY;
-  return QWEN_OK;
-}
-
-// qwen_prefill_mlp_kernel.cpp:277-283 (pointer checks done by the caller).
-int check_prefill_mlp_tiles(int S, const qwen_prefill_mlp_tiles& t) {
-  if (S <= 0 || t.seq <= 0 || t.hidden <= 0 || t.ff <= 0 || t.hidden > QWEN_PREFILL_MLP_HIDDEN_CAPACITY ||
-      t.ff > QWEN_PREFILL_MLP_FF_CAPACITY)
-    return QWEN_ERR_KERNEL;
-  return QWEN_OK;
-}
-
 size_t prefill_call_bytes(int S) {
   return staged_layer_bytes() + prefill_workspace_bytes(S) + 2 * kv_bytes(S) + 4 * act_bytes(S) + 64 * 256;
 }
@@ -293,49 +273,14 @@ int prefill_layer_host(const HostLayer& h, const float* x, int S, float* k_cache
   });
 }
 
-// valid_memory_windows: qwen_prefill_top_core.cpp:42-80.
-bool range_fits(uint64_t off, uint64_t count, uint64_t cap) { return off <= cap && count <= cap - off; }
-bool ranges_overlap(uint64_t a, uint64_t as, uint64_t b, uint64_t bs) { return a < b + bs && b < a + as; }
-
-bool prefill_windows_ok(const qwen_prefill_descriptor& d) {
-  if (d.seq_len <= 0 || d.seq_len > QWEN_PREFILL_CAPACITY) return false;
-  const uint64_t seq_bytes = (uint64_t)d.seq_len * QWEN_HIDDEN * 4u;
-  const uint64_t kvb = (uint64_t)d.seq_len * QWEN_KV_WIDTH * 4u;
-  const uint64_t packed = QWEN_OFF_DOWN_W + QWEN_DOWN_WEIGHT_BYTES - QWEN_OFF_Q_W;
-  const uint64_t scale_bytes = QWEN_OFF_DOWN_S + 4ull * QWEN_HIDDEN;
-  if (d.input_sequence_addr % 4 || d.output_sequence_addr % 4 || d.k_cache_base_addr % 4 || d.v_cache_base_addr % 4 ||
-      d.scratch_base_addr % 4 || d.layer_scales_base_addr % 4)
-    return false;
-  if (!range_fits(d.input_sequence_addr, seq_bytes, QWEN_PREFILL_ACT_WINDOW_BYTES) ||
-      !range_fits(d.output_sequence_addr, seq_bytes, QWEN_PREFILL_ACT_WINDOW_BYTES) ||
-      !range_fits(d.scratch_base_addr, seq_bytes, QWEN_PREFILL_ACT_WINDOW_BYTES) ||
-      !range_fits(d.k_cache_base_addr, kvb, QWEN_PREFILL_KV_WINDOW_BYTES) ||
-      !range_fits(d.v_cache_base_addr, kvb, QWEN_PREFILL_KV_WINDOW_BYTES) ||
-      !range_fits(d.layer_weights_base_addr + QWEN_OFF_Q_W, packed, QWEN_PREFILL_WEIGHT_WINDOW) ||
-      !range_fits(d.layer_scales_base_addr, scale_bytes, QWEN_PREFILL_SCALE_WINDOW_BYTES))
-    return false;
-  if (ranges_overlap(d.input_sequence_addr, seq_bytes, d.output_sequence_addr, seq_bytes) ||
-      ranges_overlap(d.input_sequence_addr, seq_bytes, d.scratch_base_addr, seq_bytes) ||
-      ranges_overlap(d.output_sequence_addr, seq_bytes, d.scratch_base_addr, seq_bytes) ||
-      ranges_overlap(d.k_cache_base_addr, kvb, d.v_cache_base_addr, kvb))
-    return false;
-  return true;
-}
-
 // qwen_prefill_top_wrapper (qwen_prefill_top_wrapper.cpp:7-18) + qwen_prefill_top_core (:84-183).
 int prefill_top(const qwen_prefill_descriptor& d, const uint8_t* wd, const float* sd, float* kv, float* act,
                 const void* s0, const void* s1, const void* s2, const void* s3, const void* s4) {
-  if (d.seq_len <= 0 || d.seq_len > QWEN_MAX_SEQ) return QWEN_ERR_PREFILL_DESC;
-  if (d.seq_len > QWEN_PREFILL_CAPACITY) return QWEN_ERR_PREFILL_DESC;
-  if (!qwen_valid_layer_id(d.layer_id) || d.seq_len <= 0 || !qwen_valid_prefill_tiles(&d.tiles))
-    return QWEN_ERR_PREFILL_DESC;
-  if (any_null({wd, sd, kv, act, s0, s1, s2, s3, s4})) return QWEN_ERR_PREFILL_PORT;
-  if (!prefill_windows_ok(d)) return QWEN_ERR_PREFILL_WINDOW;
+  int mst = QWEN_OK;
+  const int st = prefill_top_status(d, any_null({wd, sd, kv, act, s0, s1, s2, s3, s4}), &mst);
+  if (st) return st;
   const HostLayer h = resolve_host_layer(wd, sd, d.layer_weights_base_addr, d.layer_scales_base_addr);
   const int S = d.seq_len;
-  const int ast = check_prefill_attention_tiles(S, d.tiles.attention);
-  if (ast) return ast;
-  const int mst = check_prefill_mlp_tiles(S, d.tiles.mlp);
   return prefill_layer_host(h, act + d.input_sequence_addr / 4, S, kv + d.k_cache_base_addr / 4,
                             kv + d.v_cache_base_addr / 4, act + d.scratch_base_addr / 4,
                             act + d.output_sequence_addr / 4, mst, true);

@@ -1,0 +1,132 @@
+// Device-resident layer dispatch over the global DDR map (include/qwen_hip_dispatch.h): the
+// reference's descriptor loops (qwen_decode_top_wrapper.cpp:115-130, qwen_prefill_top_wrapper.cpp:
+// 20-35) with every DDR port a device pointer, so no layer image crosses PCIe.  Each layer runs the
+// ORDERED executors (bit-exact with the reference host library) on the caller's stream.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstdlib>
+#include <exception>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "kernels.hpp"
+#include "qwen_hip_dispatch.h"
+#include "runtime.hpp"
+#include "tops.hpp"
+
+using namespace qwen;
+
+namespace {
+
+template <class Fn>
+int guarded_dispatch(Fn&& fn) {
+  try {
+    return fn();
+  } catch (const HipError& e) {
+    set_last_error(std::string(e.what) + ": " + hipGetErrorString(e.code));
+  } catch (const std::exception& e) {
+    set_last_error(e.what());
+  }
+  if (std::getenv("QWEN_HIP_VERBOSE")) std::fprintf(stderr, "qwen-mi355x: %s\n", last_error_cstr());
+  return QWEN_ERR_DEVICE;
+}
+
+// Device pointers of one layer at (w_base, s_base) of the global images (the pointer resolution of
+// qwen_decode_top_wrapper.cpp:40-72 / qwen_prefill_top_core.cpp:100-135).
+DevLayer device_layer(const uint8_t* wd, const float* sd, uint64_t w_base, uint64_t s_base) {
+  const HostLayer h = resolve_host_layer(wd, sd, w_base, s_base);
+  return DevLayer{h.qw, h.kw, h.vw, h.ow, h.gw, h.uw, h.dw, h.ln, h.post_ln, h.qb, h.kb,
+                  h.vb, h.qs, h.ks, h.vs, h.os, h.gs, h.us, h.ds};
+}
+
+void set_completed(int* completed, int n) {
+  if (completed) *completed = n;
+}
+
+}  // namespace
+
+extern "C" {
+
+int qwen_hip_decode_dispatch_layers(const qwen_decode_descriptor* dsc, int n, const uint8_t* wd, const float* sd,
+                                    float* kv, float* act, void* stream, int* completed) {
+  set_completed(completed, 0);
+  if (!dsc || n <= 0) return QWEN_ERR_DECODE_DESC;  // qwen_decode_top_wrapper.cpp:118-120
+  Runtime& rt = Runtime::get();
+  std::lock_guard<std::mutex> lock(rt.mu);
+  return guarded_dispatch([&]() -> int {
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    // RoPE rows and arena sized once, before the first launch (growing either frees memory that
+    // queued layers still read)
+    int max_past = 0;
+    for (int i = 0; i < n && decode_descriptor_status(dsc[i]) == QWEN_OK; ++i)
+      max_past = dsc[i].past_seq_len > max_past ? dsc[i].past_seq_len : max_past;
+    if (max_past >= QWEN_MAX_SEQ) throw std::runtime_error("past_seq_len beyond the 32768-position RoPE table");
+    const float* rope = rt.decode_rope(max_past + 1);
+    rt.arena.reset();
+    rt.arena.reserve(decode_workspace_bytes(1) + 4u * QWEN_HIDDEN + 4u * (size_t)n + 8192u);
+    // every descriptor's position staged before the first launch; the layers' intermediates then
+    // reuse one workspace in stream order
+    std::vector<int> pasts((size_t)n);
+    for (int i = 0; i < n; ++i) pasts[i] = dsc[i].past_seq_len;
+    const int* pos_all = stage_in(rt.arena, pasts.data(), (size_t)n, st);
+    float* att = rt.arena.alloc_n<float>(QWEN_HIDDEN);
+    const size_t layer_mark = rt.arena.mark();
+    int status = QWEN_OK, done = 0;
+    for (; done < n; ++done) {
+      const qwen_decode_descriptor& d = dsc[done];
+      if ((status = decode_descriptor_status(d)) != QWEN_OK) break;
+      if (!wd || !sd || !kv || !act) {
+        status = QWEN_ERR_DECODE_PORT;
+        break;
+      }
+      const int past = d.past_seq_len;
+      rt.arena.rewind(layer_mark);
+      const int* pos_d = pos_all + done;
+      const DevLayer L = device_layer(wd, sd, d.layer_weights_base_addr, d.layer_scales_base_addr);
+      DecodeBatch b{1, pos_d, rope, false, kv + d.k_cache_base_addr / 4, kv + d.v_cache_base_addr / 4, 0, past + 1};
+      run_decode_attention(L, act + d.input_token_addr / 4, b, att, rt.arena, st);
+      run_decode_mlp(L, att, 1, act + d.output_token_addr / 4, rt.arena, st);
+    }
+    QWEN_HIP(hipStreamSynchronize(st));
+    rt.arena.reset();
+    set_completed(completed, done);
+    return status;
+  });
+}
+
+int qwen_hip_prefill_dispatch_layers(const qwen_prefill_descriptor* dsc, int n, const uint8_t* wd, const float* sd,
+                                     float* kv, float* act, void* stream, int* completed) {
+  set_completed(completed, 0);
+  if (!dsc || n <= 0) return QWEN_ERR_PREFILL_DESC;  // qwen_prefill_top_wrapper.cpp:23-25
+  Runtime& rt = Runtime::get();
+  std::lock_guard<std::mutex> lock(rt.mu);
+  return guarded_dispatch([&]() -> int {
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    // a valid descriptor has at most QWEN_PREFILL_CAPACITY tokens: RoPE rows and arena sized once
+    const float* rope = rt.prefill_rope(QWEN_PREFILL_CAPACITY);
+    rt.arena.reset();
+    rt.arena.reserve(prefill_workspace_bytes(QWEN_PREFILL_CAPACITY) + 4096u);
+    int status = QWEN_OK, done = 0;
+    for (; done < n; ++done) {
+      const qwen_prefill_descriptor& d = dsc[done];
+      int mlp_status = QWEN_OK;
+      if ((status = prefill_top_status(d, !wd || !sd || !kv || !act, &mlp_status)) != QWEN_OK) break;
+      const int S = d.seq_len;
+      rt.arena.reset();  // reused in stream order by every layer
+      const DevLayer L = device_layer(wd, sd, d.layer_weights_base_addr, d.layer_scales_base_addr);
+      float* scratch = act + d.scratch_base_addr / 4;  // attention output (qwen_prefill_top_core.cpp:103,155)
+      run_prefill_attention(L, act + d.input_sequence_addr / 4, S, 0, rope, kv + d.k_cache_base_addr / 4,
+                            kv + d.v_cache_base_addr / 4, scratch, rt.arena, st);
+      if ((status = mlp_status) != QWEN_OK) break;  // the attention side effects stay, as in the reference
+      run_prefill_mlp(L, scratch, S, act + d.output_sequence_addr / 4, rt.arena, st);
+    }
+    QWEN_HIP(hipStreamSynchronize(st));
+    rt.arena.reset();
+    set_completed(completed, done);
+    return status;
+  });
+}
+
+}  // extern "C"

@@ -1928,7 +1928,7 @@ attn_decode_kernel(const float* __restrict__ qkv, int qkv_stride, const float* _
   // invalidation is needed on either side.
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (threadIdx.x == 0) s_last = atomicAdd(&arrivals[b], 1u) == 2u * (unsigned)nsplit - 1u;
+  if (threadIdx.x == 0) s_last = atomicAdd(&arrivals[b], 1u) == gridDim.x * gridDim.y - 1u;  // splits x KV heads
   __syncthreads();
   if (!s_last) return;
 

@@ -93,9 +93,7 @@ struct qwen_hip_model {
     float* splitk;  // K-split partials of the non-dual projections (out <= 2048)
     uint8_t* kvt;   // prefill attention: bf16 hi/lo K/V tiles of one layer
   };
-  // `slot` s > 0 places a second, disjoint set of the same parts after slot s - 1's, with the arrival
-  // counters of sequences s*batch.. (two halves of a batch decoded concurrently).
-  Ws carve(size_t tokens, size_t batch, size_t nsplit, size_t kvt_bytes = 0, int slot = 0) {
+  Ws carve(size_t tokens, size_t batch, size_t nsplit, size_t kvt_bytes = 0) {
     size_t off = 0;
     auto take = [&](size_t bytes) {
       const size_t o = off;
@@ -103,7 +101,6 @@ struct qwen_hip_model {
       return o;
     };
     const size_t o_arr = take(kMaxArrivals * 4u);  // fixed offset: never overlaps the parts below
-    const size_t first = off;
     const size_t o_xq = take(xq_bytes(tokens, QWEN_INTERMEDIATE));
     const size_t o_sx = take(tokens * 4u);
     const size_t o_sums = take(tokens * 8u);
@@ -116,15 +113,12 @@ struct qwen_hip_model {
     const size_t o_pml = take(batch * QWEN_Q_HEADS * nsplit * 8u);
     const size_t o_splitk = take(splitk_bytes(kQkvRows));
     const size_t o_kvt = take(kvt_bytes);
-    const size_t shift = (size_t)slot * (off - first);
-    char* b = static_cast<char*>(ws.get(off + shift));
+    char* b = static_cast<char*>(ws.get(off));
     unsigned* arr = reinterpret_cast<unsigned*>(b + o_arr);
     if (ws.generation != arrivals_ready) {  // fresh buffer: arm the counters once
       launch_zero_u32(arr, kMaxArrivals, stream);
       arrivals_ready = ws.generation;
     }
-    b += shift;
-    arr += (size_t)slot * batch;
     return Ws{reinterpret_cast<int8_t*>(b + o_xq), reinterpret_cast<float*>(b + o_sx),
               reinterpret_cast<int*>(b + o_sums), reinterpret_cast<float*>(b + o_qkv),
               reinterpret_cast<float*>(b + o_ctx), reinterpret_cast<float*>(b + o_att),
@@ -216,7 +210,6 @@ struct qwen_hip_model {
 
   ~qwen_hip_model() {
     if (stream) (void)hipStreamSynchronize(stream);
-    split_release();
     for (void* p : {static_cast<void*>(raw_w), static_cast<void*>(raw_s), static_cast<void*>(wp),
                     static_cast<void*>(rope_decode), static_cast<void*>(rope_prefill), static_cast<void*>(embed),
                     static_cast<void*>(head_norm), head_ws.p,
@@ -361,147 +354,6 @@ struct qwen_hip_model {
              nullptr, nullptr, w.att, round, 0, fuse_next ? &fn : nullptr);
       }
     }
-    QWEN_HIP(hipGetLastError());
-  }
-
-  // ---- batched decode as two concurrent halves on CU-masked streams -------------------------
-  // The projections of a decode batch are latency-bound (a few µs per launch whatever the batch)
-  // and its attention is HBM-bound.  Two halves of the batch run as two independent decodes whose
-  // projections queue on one stream confined to `pcus` CUs of every XCD and whose attention queues
-  // on a second stream confined to the other CUs, so one half's projections run under the other
-  // half's attention.  Both halves' kernels are the ones decode_fast launches at half the batch.
-  hipStream_t s_proj = nullptr, s_attn = nullptr;
-  int split_pcus = 0, split_layers = 0;
-  std::vector<hipEvent_t> split_ev;  // [0] start, [1] end, then per (half, layer): Q/K/V done, attention done
-
-  void split_release() {
-    for (hipEvent_t e : split_ev) (void)hipEventDestroy(e);
-    split_ev.clear();
-    if (s_proj) (void)hipStreamDestroy(s_proj);
-    if (s_attn) (void)hipStreamDestroy(s_attn);
-    s_proj = s_attn = nullptr;
-    split_pcus = split_layers = 0;
-  }
-
-  void split_setup(int pcus) {
-    if (split_pcus == pcus && split_layers == layers) return;
-    split_release();
-    int dev = 0;
-    hipDeviceProp_t prop;
-    QWEN_HIP(hipGetDevice(&dev));
-    QWEN_HIP(hipGetDeviceProperties(&prop, dev));
-    const int ncu = prop.multiProcessorCount;
-    if (ncu % 8 != 0 || ncu > 1024 || pcus <= 0 || 8 * pcus >= ncu) throw std::runtime_error("split decode: CU count");
-    // CU mask bit i: the runtime spreads mask bits over the XCDs; choosing bits so that every XCD gets
-    // pcus of them whether bit i belongs to XCD i % 8 or to XCD i / (ncu / 8).
-    const int per_xcd = ncu / 8, words = ncu / 32;
-    std::vector<uint32_t> mp(words, 0u), ma(words, 0u);
-    std::vector<char> on(ncu, 0);
-    for (int x = 0; x < 8; ++x)
-      for (int j = 0; j < pcus; ++j) on[x * per_xcd + ((x + j) % 8) + 8 * (j / 8)] = 1;
-    for (int i = 0; i < ncu; ++i) (on[i] ? mp : ma)[i / 32] |= 1u << (i % 32);
-    QWEN_HIP(hipExtStreamCreateWithCUMask(&s_proj, (uint32_t)words, mp.data()));
-    QWEN_HIP(hipExtStreamCreateWithCUMask(&s_attn, (uint32_t)words, ma.data()));
-    split_ev.resize(2 + 4 * (size_t)layers);
-    for (hipEvent_t& e : split_ev) QWEN_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
-    split_pcus = pcus;
-    split_layers = layers;
-  }
-
-  void decode_fast_split(int B, float* hidden, const int* pos, int max_keys, float* kc0, float* vc0, uint64_t ss,
-                         uint64_t ls, int round, int pcus) {
-    split_setup(pcus);
-    int dev = 0;
-    hipDeviceProp_t prop;
-    QWEN_HIP(hipGetDevice(&dev));
-    QWEN_HIP(hipGetDeviceProperties(&prop, dev));
-    const int H = B / 2;
-    const AttnDecodePlan plan = plan_attn_decode(H, max_keys, prop.multiProcessorCount - 8 * pcus);
-    const Ws w1 = carve(H, H, plan.nsplit, 0, 1);  // the larger extent first: no reallocation after it
-    const Ws w0 = carve(H, H, plan.nsplit, 0, 0);
-    const Ws wh[2] = {w0, w1};
-    hipStream_t const caller = stream;
-    hipEvent_t* ev = split_ev.data();
-    QWEN_HIP(hipEventRecord(ev[0], caller));
-    QWEN_HIP(hipStreamWaitEvent(s_proj, ev[0], 0));
-    QWEN_HIP(hipStreamWaitEvent(s_attn, ev[0], 0));
-    auto evq = [&](int h, int l) { return ev[2 + 4 * l + 2 * h]; };
-    auto eva = [&](int h, int l) { return ev[2 + 4 * l + 2 * h + 1]; };
-    auto xs = [&](int h) { return hidden + (size_t)h * H * QWEN_HIDDEN; };
-    auto kcs = [&](int h, int l) { return kc0 + (size_t)l * ls + (size_t)h * H * ss; };
-    auto vcs = [&](int h, int l) { return vc0 + (size_t)l * ls + (size_t)h * H * ss; };
-    // Q/K/V projection (+ RoPE, KV append) of half h, layer l, on the projection stream
-    auto head = [&](int h, int l) {
-      const Ws& w = wh[h];
-      const FastLayer& f = fast[l];
-      stream = s_proj;
-      if (l == 0)
-        launch_norm_quant(xs(h), QWEN_HIDDEN, H, QWEN_HIDDEN, f.ln, kNormDecode, w.xq, w.sx, w.sums, nullptr, stream);
-      GemmArgs fq{};
-      fq.fuse = kFuseQkvRope;
-      fq.pos = pos + h * H;
-      fq.rope = rope_decode;
-      fq.k_cache = kcs(h, l);
-      fq.v_cache = vcs(h, l);
-      fq.seq_stride = ss;
-      fq.limit = max_keys;
-      gemm(w, H, QWEN_HIDDEN, (int)kQkvRows, f.qkv, f.sw_qkv, f.b_qkv, w.qkv, kQkvRows, kEpiStore, nullptr, nullptr,
-           nullptr, 0, 0, &fq);
-      QWEN_HIP(hipEventRecord(evq(h, l), s_proj));
-    };
-    auto attn = [&](int h, int l) {
-      const Ws& w = wh[h];
-      QWEN_HIP(hipStreamWaitEvent(s_attn, evq(h, l), 0));
-      launch_attn_decode(w.qkv, (int)kQkvRows, kcs(h, l), vcs(h, l), ss, pos + h * H, H, max_keys, plan, w.part,
-                         w.pml, w.arrivals, nullptr, w.xq, w.sx, w.sums, s_attn);
-      QWEN_HIP(hipEventRecord(eva(h, l), s_attn));
-    };
-    // O, gate/up, down projections of half h, layer l (the next layer's RMSNorm + quantization fused)
-    auto tail = [&](int h, int l) {
-      const Ws& w = wh[h];
-      const FastLayer& f = fast[l];
-      stream = s_proj;
-      QWEN_HIP(hipStreamWaitEvent(s_proj, eva(h, l), 0));
-      GemmArgs fn{};
-      fn.fuse = kFuseNormQuant;
-      fn.norm = kNormDecode;
-      fn.xq_out = w.xq;
-      fn.sx_out = w.sx;
-      fn.sums_out = w.sums;
-      fn.norm_w = f.post_ln;
-      gemm(w, H, QWEN_HIDDEN, QWEN_HIDDEN, f.o, f.sw_o, nullptr, w.att, QWEN_HIDDEN, kEpiStore, nullptr, nullptr,
-           nullptr, 0, 0, &fn);
-      gemm(w, H, QWEN_HIDDEN, QWEN_INTERMEDIATE, f.gate, f.sw_gate, nullptr, w.s, QWEN_INTERMEDIATE, kEpiSiluMul,
-           f.up, f.sw_up, nullptr, 0, 0);
-      launch_norm_quant(w.s, QWEN_INTERMEDIATE, H, QWEN_INTERMEDIATE, nullptr, kNormNone, w.xq, w.sx, w.sums, nullptr,
-                        stream);
-      const bool fuse_next = l + 1 < layers;
-      fn.norm_w = fuse_next ? fast[l + 1].ln : nullptr;
-      gemm(w, H, QWEN_INTERMEDIATE, QWEN_HIDDEN, f.down, f.sw_down, nullptr, xs(h), QWEN_HIDDEN, kEpiResidual,
-           nullptr, nullptr, w.att, round, 0, fuse_next ? &fn : nullptr);
-    };
-    try {
-      // projection stream: head(0,0) head(1,0) | tail(0,l) head(0,l+1) tail(1,l) head(1,l+1) | ...
-      // attention stream:  attn(0,0) attn(1,0) attn(0,1) attn(1,1) ...
-      head(0, 0);
-      attn(0, 0);
-      head(1, 0);
-      attn(1, 0);
-      for (int l = 0; l < layers; ++l)
-        for (int h = 0; h < 2; ++h) {
-          tail(h, l);
-          if (l + 1 < layers) {
-            head(h, l + 1);
-            attn(h, l + 1);
-          }
-        }
-      QWEN_HIP(hipEventRecord(ev[1], s_proj));
-      QWEN_HIP(hipStreamWaitEvent(caller, ev[1], 0));
-    } catch (...) {
-      stream = caller;
-      throw;
-    }
-    stream = caller;
     QWEN_HIP(hipGetLastError());
   }
 
@@ -680,6 +532,31 @@ int qwen_hip_model_destroy(qwen_hip_model* m) {
 
 int qwen_hip_model_layers(const qwen_hip_model* m) { return m ? m->layers : 0; }
 
+int qwen_hip_model_layer_images(qwen_hip_model* m, int layer, uint8_t* weight_ddr, float* scale_ddr) {
+  if (!m || !weight_ddr || !scale_ddr || layer < 0 || layer >= m->layers) return invalid("invalid readback arguments");
+  std::lock_guard<std::mutex> lock(m->mu);
+  return guarded_model([&]() -> int {
+    QWEN_HIP(hipStreamSynchronize(m->stream));
+    QWEN_HIP(hipMemcpy(weight_ddr, m->raw_w + (size_t)layer * QWEN_LAYER_BYTES, QWEN_LAYER_BYTES,
+                       hipMemcpyDeviceToHost));
+    QWEN_HIP(hipMemcpy(scale_ddr, m->raw_s + (size_t)layer * (QWEN_LAYER_BYTES / 4), QWEN_LAYER_BYTES,
+                       hipMemcpyDeviceToHost));
+    return QWEN_OK;
+  });
+}
+
+int qwen_hip_model_head_tables(qwen_hip_model* m, uint16_t* embed_bf16, uint16_t* norm_bf16) {
+  if (!m || !embed_bf16 || !norm_bf16) return invalid("invalid readback arguments");
+  if (!m->embed || !m->head_norm) return invalid("model has no head (synthetic models, or qwen_hip_model_set_head)");
+  std::lock_guard<std::mutex> lock(m->mu);
+  return guarded_model([&]() -> int {
+    QWEN_HIP(hipStreamSynchronize(m->stream));
+    QWEN_HIP(hipMemcpy(embed_bf16, m->embed, (size_t)m->vocab * QWEN_HIDDEN * 2u, hipMemcpyDeviceToHost));
+    QWEN_HIP(hipMemcpy(norm_bf16, m->head_norm, QWEN_HIDDEN * 2u, hipMemcpyDeviceToHost));
+    return QWEN_OK;
+  });
+}
+
 void* qwen_hip_model_stream(qwen_hip_model* m) { return m ? static_cast<void*>(m->stream) : nullptr; }
 
 int qwen_hip_model_synchronize(qwen_hip_model* m) {
@@ -704,12 +581,12 @@ int qwen_hip_model_decode(qwen_hip_model* m, int mode, int batch, float* hidden,
     return invalid("KV strides too small for max_keys / batch");
   std::lock_guard<std::mutex> lock(m->mu);
   return guarded_model([&]() -> int {
-    // QWEN_SPLIT_CUS asks for the two-halves decode on CU-masked streams.  It is switched off: on
+    // QWEN_SPLIT_CUS asked for a two-halves decode on CU-masked streams.  That path was removed: on
     // MI355X its results matched the oracle, but the process then hung while the model (and with it
     // the CU-masked streams) was torn down, for a cause not found.
     const char* sp = std::getenv("QWEN_SPLIT_CUS");
     if (mode == QWEN_MODE_FAST && sp && std::atoi(sp) > 0)
-      throw std::runtime_error("QWEN_SPLIT_CUS: the CU-masked split decode is switched off");
+      throw std::runtime_error("QWEN_SPLIT_CUS: the CU-masked split decode was removed");
     if (mode == QWEN_MODE_FAST)
       m->decode_fast(batch, hidden, positions, max_keys, k_cache, v_cache, seq_stride, layer_stride, round,
                      pre_reduce);

@@ -47,6 +47,9 @@ HostLayer resolve_host_layer(const uint8_t* weight_ddr, const float* scale_ddr, 
 class Arena {
  public:
   void reset() { used_ = 0; }
+  // Bytes handed out so far, and a return to such a mark (later allocations reuse the space).
+  size_t mark() const { return used_; }
+  void rewind(size_t mark) { used_ = mark < used_ ? mark : used_; }
   // Reserve capacity before any pointer of this call is handed out (growing frees the old block).
   void reserve(size_t bytes);
   void* alloc(size_t bytes);
