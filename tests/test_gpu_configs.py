@@ -6,21 +6,29 @@
   (oracle_decode_layer_block, the reference decode arithmetic) within FAST_TOL, and the ORDERED
   output and rows bit for bit; this runs the attention plan of the bench (6 splits of 688 keys, the
   steady-state tile loop, the masked last tile and the 64-sequence last-arriving merge).  All 28
-  layers: FAST stays within DRIFT_28 of ORDERED with the driver's bf16 rounding after every layer.
+  layers: see the condition-aware bound below.
 * 8 x 2048 prefill: one layer's FAST outputs and K/V rows against the oracle's, committed as the
   golden fixture tests/golden/prefill_c4.npz (sampled rows in every key tile, and every row's max and
   sum).
 * 28-layer greedy generation, batch 1, a 512-token prompt then 128 decode steps (synthetic model seed
   2): layer 0 of the prefill and of the first decode step against the oracle (ORDERED bit for bit,
-  FAST within FAST_TOL); every greedy id equal to the argmax of the same mode's logits; FAST fed
-  ORDERED's token trajectory (teacher forcing) with logits within LOGIT_TOL of ORDERED's and ids equal
-  except where ORDERED's top two logits are closer than the logit difference allows.
+  FAST within FAST_TOL); the head of the first step against the oracle; every greedy id equal to the
+  argmax of the same mode's logits; FAST fed ORDERED's token trajectory (teacher forcing), with and
+  without the driver's bf16 rounding between layers.
 
-Tolerances (max |y - y_ref| / max |y_ref| per tensor):
-  FAST_TOL = 1e-3   one layer, fp32 output (no bf16 rounding), and each K/V tensor;
-  DRIFT_28 = 3e-2   hidden state after 28 FAST layers against 28 ORDERED layers, both bf16-rounded
-                    after every layer (a rounding flip is a whole bf16 step, 2^-8 relative);
-  LOGIT_TOL = 5e-2  logits after 28 layers and the head.
+Tolerances:
+  FAST_TOL = 1e-3 (max |y - y_ref| / max |y_ref| per tensor): one layer, fp32 output (no bf16
+    rounding), and each K/V tensor.
+  28 layers, condition-aware: the random-init synthetic models are chaotic over 28 layers: ORDERED
+    itself, with ONE input element moved by one bf16 ulp, ends 0.34 (64 x 4096 decode hidden state)
+    and 0.79 (greedy logits) of max away from unperturbed ORDERED; without the driver's bf16 rounding
+    between layers, 0.10 (greedy logits).  A fixed tolerance at 28 layers would therefore measure the
+    model, not the kernels.  The bound used is: FAST's deviation from ORDERED is at most
+    COND_FACTOR = 2 times the larger deviation of two such one-ulp-perturbed ORDERED runs (measured on
+    MI355X: 1.01x for the decode hidden state, 1.3x for the greedy logits); both modes are also
+    bit-identical run to run (no race in the fused, atomically merged kernels).
+  Head: every logit within max(1 bf16 ulp, 1e-5 x the row's largest |logit|) of the oracle's (the
+    device accumulates the 1536 products in fp32, the oracle in double; tests/test_gpu_head.py).
 """
 
 from __future__ import annotations
@@ -35,8 +43,7 @@ from work_llm_accelerator_amd.layout import HIDDEN, KV_WIDTH, LAYOUT
 pytestmark = pytest.mark.gpu
 
 FAST_TOL = 1e-3
-DRIFT_28 = 3e-2
-LOGIT_TOL = 5e-2
+COND_FACTOR = 2.0
 
 
 @pytest.fixture(scope="module")
@@ -49,6 +56,12 @@ def torch():
 def rel_err(got, ref):
     scale = float(np.max(np.abs(ref)))
     return float(np.max(np.abs(np.asarray(got, np.float64) - np.asarray(ref, np.float64)))) / max(scale, 1e-30)
+
+
+def bf16_order(x):
+    """Monotone integer image of the bf16 values held in fp32 x (neighbouring bf16 values differ by 1)."""
+    bits = (np.ascontiguousarray(x, dtype=np.float32).view(np.uint32) >> 16).astype(np.int64)
+    return np.where(bits & 0x8000, -(bits & 0x7FFF), bits & 0x7FFF)
 
 
 def layer_images(model, layer):
@@ -129,29 +142,49 @@ def test_decode_64x4096_one_layer(torch):
         m.close()
 
 
-def test_decode_64x4096_28_layers_fast_vs_ordered(torch):
-    from work_llm_accelerator_amd.model import MODE_FAST, MODE_ORDERED, DeviceModel, KvCache
+def perturbed(x, element):
+    """x with one element of every row moved by one bf16 ulp (x is a bf16 value held in fp32)."""
+    y = x.clone()
+    y[..., element] = y[..., element] * (1.0 + 2.0 ** -7)
+    return y
 
-    print("decode 64 x 4097..4128 keys, 28 layers (seed 4): FAST vs ORDERED drift", flush=True)
+
+def test_decode_64x4096_28_layers_fast_vs_ordered(torch):
+    from work_llm_accelerator_amd.model import FLAG_NO_BF16_ROUND, MODE_FAST, MODE_ORDERED, DeviceModel, KvCache
+
+    print("decode 64 x 4097..4128 keys, 28 layers (seed 4): FAST vs ORDERED, condition-aware", flush=True)
     m = DeviceModel(28, synthetic_seed=4)
     try:
         cache, hidden, pos, pasts, positions = c5_inputs(torch, m, 28)
-        outs = []
-        rows = []
-        for mode in (MODE_ORDERED, MODE_FAST):
+
+        def run(mode, x):
             c = KvCache(cache.k.clone(), cache.v.clone(), 28, B5, positions)
-            h = hidden.clone()
+            h = x.clone()
             m.decode(mode, h, pos, positions, c)
             m.synchronize()
-            outs.append(h.cpu().numpy())
             idx = torch.tensor(pasts, device="cuda", dtype=torch.long)
-            rows.append(c.k[27, torch.arange(B5, device="cuda"), idx].cpu().numpy())  # last layer's new K rows
+            k27 = c.k[27, torch.arange(B5, device="cuda"), idx].cpu().numpy()  # the last layer's new K rows
             del c
-        assert np.all(np.isfinite(outs[0])) and np.all(np.isfinite(outs[1]))
-        drift = max(rel_err(outs[1][b], outs[0][b]) for b in range(B5))
-        drift_k = max(rel_err(rows[1][b], rows[0][b]) for b in range(B5))
-        print(f"  28-layer drift FAST vs ORDERED: hidden {drift:.3g}, layer-27 K rows {drift_k:.3g}", flush=True)
-        assert drift <= DRIFT_28 and drift_k <= DRIFT_28, (drift, drift_k)
+            return h.cpu().numpy(), k27
+
+        def dev(a, b):
+            return max(rel_err(a[i], b[i]) for i in range(B5))
+
+        for flag, what in ((0, "with the driver's bf16 rounding"), (FLAG_NO_BF16_ROUND, "without rounding")):
+            o_h, o_k = run(MODE_ORDERED | flag, hidden)
+            f_h, f_k = run(MODE_FAST | flag, hidden)
+            assert np.all(np.isfinite(o_h)) and np.all(np.isfinite(f_h))
+            o2_h, _ = run(MODE_ORDERED | flag, hidden)
+            f2_h, f2_k = run(MODE_FAST | flag, hidden)
+            assert bits_equal(o2_h.reshape(-1), o_h.reshape(-1)), "ORDERED is not deterministic"
+            assert bits_equal(f2_h.reshape(-1), f_h.reshape(-1)) and bits_equal(f2_k.reshape(-1), f_k.reshape(-1)), \
+                "FAST is not deterministic"
+            p_h = [run(MODE_ORDERED | flag, perturbed(hidden, e))[0] for e in (7, 1000)]
+            cond = max(dev(p, o_h) for p in p_h)
+            d_h, d_k = dev(f_h, o_h), dev(f_k, o_k)
+            print(f"  {what}: FAST vs ORDERED hidden {d_h:.3g} (layer-27 K rows {d_k:.3g}); ORDERED vs "
+                  f"one-ulp-perturbed ORDERED {cond:.3g}", flush=True)
+            assert d_h <= COND_FACTOR * cond, (d_h, cond)
     finally:
         m.close()
 
@@ -216,6 +249,7 @@ PROMPT3, STEPS3 = 512, 128
 def test_greedy_28_layers_prompt512_128_steps(torch):
     from work_llm_accelerator_amd.model import (FLAG_NO_BF16_ROUND, MODE_FAST, MODE_ORDERED, DeviceModel,
                                                 KvCache)
+
     print("greedy 28 layers (seed 2): 512-token prompt + 128 teacher-forced steps, FAST vs ORDERED", flush=True)
     m = DeviceModel(28, synthetic_seed=2)
     vocab = m.vocab
@@ -231,17 +265,25 @@ def test_greedy_28_layers_prompt512_128_steps(torch):
 
         runs = {}
         pos_all = torch.arange(PROMPT3, PROMPT3 + STEPS3, dtype=torch.int32, device="cuda")
-        for name, mode in (("ordered", MODE_ORDERED), ("fast", MODE_FAST)):
+        x_pert = x0.clone()
+        x_pert[0, 0, 7] = x_pert[0, 0, 7] * (1.0 + 2.0 ** -7)  # one element of the first prompt token, one ulp
+        x_pert2 = x0.clone()
+        x_pert2[0, 0, 1000] = x_pert2[0, 0, 1000] * (1.0 + 2.0 ** -7)
+        NR = FLAG_NO_BF16_ROUND
+        for name, mode, x in (("ordered", MODE_ORDERED, x0), ("fast", MODE_FAST, x0), ("pert", MODE_ORDERED, x_pert),
+                              ("pert2", MODE_ORDERED, x_pert2), ("ordered_nr", MODE_ORDERED | NR, x0),
+                              ("fast_nr", MODE_FAST | NR, x0), ("pert_nr", MODE_ORDERED | NR, x_pert),
+                              ("pert2_nr", MODE_ORDERED | NR, x_pert2)):
             cache = KvCache.allocate(28, 1, positions)
-            hp = x0.clone()
+            hp = x.clone()
             m.prefill(mode, hp, cache)
             logits = torch.empty(STEPS3, vocab, dtype=torch.float32, device="cuda")
             ids = torch.empty(STEPS3, dtype=torch.int32, device="cuda")
             first = torch.empty(1, dtype=torch.int32, device="cuda")
             h = torch.empty(1, HIDDEN, dtype=torch.float32, device="cuda")
             m.greedy(hp[0, PROMPT3 - 1:], first)  # the prompt's next token starts the loop
-            # teacher forcing: FAST is fed ORDERED's tokens (step i embeds the id ORDERED chose at step i-1);
-            # every operation below is queued on the model's stream, in order
+            # teacher forcing: every other run is fed ORDERED's tokens (step i embeds the id ORDERED chose at
+            # step i-1); every operation below is queued on the model's stream, in order
             src_first = first if name == "ordered" else runs["ordered"]["first"]
             src_ids = ids if name == "ordered" else runs["ordered"]["ids"]
             for i in range(STEPS3):
@@ -255,15 +297,13 @@ def test_greedy_28_layers_prompt512_128_steps(torch):
                     torch.cuda.synchronize()
             m.synchronize()
             runs[name] = {"ids": ids, "first": first, "logits": logits, "cache": cache, "h0": h0}
-        fed = {name: np.concatenate([r["first"].cpu().numpy(), r["ids"].cpu().numpy()[:-1]])
-               for name, r in runs.items()}
-        fed["fast"] = np.concatenate([runs["ordered"]["first"].cpu().numpy(), runs["ordered"]["ids"].cpu().numpy()[:-1]])
+            if name not in ("ordered", "fast"):
+                del runs[name]["cache"]
 
         # every greedy id is the first maximum of the same mode's logits
         for name, r in runs.items():
             am = torch.argmax(r["logits"], dim=1).to(torch.int32)
             assert torch.equal(am, r["ids"]), f"{name}: greedy ids differ from the argmax of the logits"
-        assert np.array_equal(fed["fast"], fed["ordered"])
 
         # layer 0 against the oracle: prefill K/V rows (bit for bit in ORDERED), and the first decode step's
         # new K/V rows at position 512 (the embedded first generated token over the prefilled rows)
@@ -273,7 +313,7 @@ def test_greedy_28_layers_prompt512_128_steps(torch):
         vc = np.zeros(PROMPT3 * KV_WIDTH, np.float32)
         out0 = np.zeros(PROMPT3 * HIDDEN, np.float32)
         assert o.oracle_prefill_layer_uncapped(x0_host, PROMPT3, w0, s0, kc, vc, out0) == 0
-        for name, r in runs.items():
+        for name, r in ((n, runs[n]) for n in ("ordered", "fast")):
             gk = r["cache"].k[0, 0, :PROMPT3].cpu().numpy().reshape(-1)
             gv = r["cache"].v[0, 0, :PROMPT3].cpu().numpy().reshape(-1)
             if name == "ordered":
@@ -307,7 +347,7 @@ def test_greedy_28_layers_prompt512_128_steps(torch):
         vd[:PROMPT3 * KV_WIDTH] = vc
         outd = np.zeros(HIDDEN, np.float32)
         assert o.oracle_decode_layer_block(e.cpu().numpy().reshape(-1), PROMPT3, w0, s0, kd, vd, outd) == 0
-        for name, r in runs.items():
+        for name, r in ((n, runs[n]) for n in ("ordered", "fast")):
             gk = r["cache"].k[0, 0, PROMPT3].cpu().numpy()
             gv = r["cache"].v[0, 0, PROMPT3].cpu().numpy()
             rk, rv = kd[PROMPT3 * KV_WIDTH:], vd[PROMPT3 * KV_WIDTH:]
@@ -323,21 +363,33 @@ def test_greedy_28_layers_prompt512_128_steps(torch):
         h0 = runs["ordered"]["h0"].cpu().numpy()
         _, ref_logits = head_logits(h0, norm, embed)
         got0 = runs["ordered"]["logits"][0].cpu().numpy()
-        assert bits_equal(got0, ref_logits[0]), "head logits of step 0: " + first_mismatch(got0, ref_logits[0])
+        ulp = np.abs(bf16_order(got0) - bf16_order(ref_logits[0]))
+        floor = 1e-5 * float(np.max(np.abs(ref_logits[0])))
+        assert not np.any((ulp > 1) & (np.abs(got0 - ref_logits[0]) > floor)), "head logits of step 0"
+        assert np.mean(ulp == 0) >= 0.99
 
-        # FAST against ORDERED (same tokens): logits within LOGIT_TOL, ids equal except near-ties
-        lo = runs["ordered"]["logits"].cpu().numpy().astype(np.float64)
-        lf = runs["fast"]["logits"].cpu().numpy().astype(np.float64)
-        io = runs["ordered"]["ids"].cpu().numpy()
-        jf = runs["fast"]["ids"].cpu().numpy()
-        dl = np.max(np.abs(lf - lo), axis=1)
-        worst = float(np.max(dl / np.max(np.abs(lo), axis=1)))
-        diff = np.nonzero(io != jf)[0]
-        for i in diff:
-            gap = lo[i, io[i]] - lo[i, jf[i]]
-            assert gap <= 2.0 * dl[i], f"step {i}: ids {io[i]} vs {jf[i]} with ORDERED gap {gap:.4g} > 2 x {dl[i]:.4g}"
-        print(f"  logits FAST vs ORDERED: worst {worst:.3g} of max; ids equal at {STEPS3 - diff.size}/{STEPS3} steps "
-              f"(the rest are near-ties)", flush=True)
-        assert worst <= LOGIT_TOL, worst
+        # FAST against ORDERED (same tokens), against ORDERED's own one-ulp sensitivity, with the driver's
+        # bf16 rounding between layers and without it; where the ids differ, ORDERED's logits of the two ids
+        # are closer than the logit difference (a near-tie)
+        for suffix, what in (("", "with the driver's bf16 rounding"), ("_nr", "without rounding")):
+            lo = runs["ordered" + suffix]["logits"].cpu().numpy().astype(np.float64)
+            io = runs["ordered" + suffix]["ids"].cpu().numpy()
+
+            def logit_dev(name):
+                lx = runs[name + suffix]["logits"].cpu().numpy().astype(np.float64)
+                dl = np.max(np.abs(lx - lo), axis=1)
+                return dl, float(np.max(dl / np.max(np.abs(lo), axis=1)))
+
+            dl, worst = logit_dev("fast")
+            cond = max(logit_dev("pert")[1], logit_dev("pert2")[1])
+            jf = runs["fast" + suffix]["ids"].cpu().numpy()
+            diff = np.nonzero(io != jf)[0]
+            for i in diff:
+                gap = lo[i, io[i]] - lo[i, jf[i]]
+                assert gap <= 2.0 * dl[i], f"step {i}: ids {io[i]} vs {jf[i]}: ORDERED gap {gap:.4g} > 2 x {dl[i]:.4g}"
+            print(f"  {what}: logits FAST vs ORDERED worst {worst:.3g} of max; ORDERED vs one-ulp-perturbed ORDERED "
+                  f"{cond:.3g}; ids equal at {STEPS3 - diff.size}/{STEPS3} steps (the rest are near-ties); "
+                  f"{len(set(io.tolist()))} distinct ORDERED ids", flush=True)
+            assert worst <= COND_FACTOR * cond, (what, worst, cond)
     finally:
         m.close()

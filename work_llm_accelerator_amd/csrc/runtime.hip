@@ -155,42 +155,70 @@ DevLayer stage_layer(Arena& a, const HostLayer& h, hipStream_t st) {
 // ---------------------------------------------------------------------------------------------
 // Executors.  Intermediates come from the arena; sizes in floats per token:
 //   xn 1536, q 1536, k 256, v 256, ctx 1536 (attention);  pn 1536, g/u/s 3*8960 (MLP).
-size_t decode_workspace_bytes(int tokens) {
-  return (size_t)tokens * sizeof(float) * (5u * QWEN_HIDDEN + 2u * QWEN_KV_WIDTH + 3u * QWEN_INTERMEDIATE) +
-         16u * 256u;
-}
+size_t decode_workspace_bytes(int tokens) { return 2u * decode_workspace_floats(tokens) * sizeof(float) + 16u * 256u; }
 size_t prefill_workspace_bytes(int tokens) { return decode_workspace_bytes(tokens); }
+
+size_t decode_workspace_floats(int tokens) {
+  const size_t T = (size_t)tokens;
+  auto up = [](size_t n) { return (n + 63u) & ~size_t(63u); };
+  return 5u * up(T * QWEN_HIDDEN) + 2u * up(T * QWEN_KV_WIDTH) + 3u * up(T * QWEN_INTERMEDIATE);
+}
+
+DecodeWorkspace carve_decode_workspace(float* base, int tokens) {
+  const size_t T = (size_t)tokens;
+  auto up = [](size_t n) { return (n + 63u) & ~size_t(63u); };
+  DecodeWorkspace w;
+  float* p = base;
+  auto take = [&](size_t n) {
+    float* r = p;
+    p += up(n);
+    return r;
+  };
+  w.xn = take(T * QWEN_HIDDEN);
+  w.q = take(T * QWEN_HIDDEN);
+  w.k = take(T * QWEN_KV_WIDTH);
+  w.v = take(T * QWEN_KV_WIDTH);
+  w.ctx = take(T * QWEN_HIDDEN);
+  w.pn = take(T * QWEN_HIDDEN);
+  w.g = take(T * QWEN_INTERMEDIATE);
+  w.u = take(T * QWEN_INTERMEDIATE);
+  w.s = take(T * QWEN_INTERMEDIATE);
+  return w;
+}
+
+void run_decode_attention_ws(const DevLayer& L, const float* x, const DecodeBatch& b, float* att,
+                             const DecodeWorkspace& w, hipStream_t st) {
+  const int T = b.tokens;
+  launch_rmsnorm_ordered(x, L.ln, w.xn, T, false, st);
+  launch_project_ordered(w.xn, T, QWEN_HIDDEN, L.qw, L.qs, L.qb, QWEN_HIDDEN, w.q, nullptr, st);
+  launch_project_ordered(w.xn, T, QWEN_HIDDEN, L.kw, L.ks, L.kb, QWEN_KV_WIDTH, w.k, nullptr, st);
+  launch_project_ordered(w.xn, T, QWEN_HIDDEN, L.vw, L.vs, L.vb, QWEN_KV_WIDTH, w.v, nullptr, st);
+  launch_rope_append_decode(w.q, w.k, w.v, b.pos, b.rope, b.rope_per_token, b.k_cache, b.v_cache, b.cache_stride,
+                            b.max_keys, T, st);
+  launch_attention_ordered(w.q, b.k_cache, b.v_cache, b.cache_stride, b.pos, b.max_keys, T, false, 0, w.ctx, st);
+  launch_project_ordered(w.ctx, T, QWEN_HIDDEN, L.ow, L.os, nullptr, QWEN_HIDDEN, att, nullptr, st);
+  QWEN_HIP(hipGetLastError());
+}
+
+void run_decode_mlp_ws(const DevLayer& L, const float* att, int T, float* out, const DecodeWorkspace& w,
+                       hipStream_t st) {
+  launch_rmsnorm_ordered(att, L.post_ln, w.pn, T, false, st);
+  launch_project_ordered(w.pn, T, QWEN_HIDDEN, L.gw, L.gs, nullptr, QWEN_INTERMEDIATE, w.g, nullptr, st);
+  launch_project_ordered(w.pn, T, QWEN_HIDDEN, L.uw, L.us, nullptr, QWEN_INTERMEDIATE, w.u, nullptr, st);
+  launch_silu_mul(w.g, w.u, w.s, (size_t)T * QWEN_INTERMEDIATE, false, st);
+  launch_project_ordered(w.s, T, QWEN_INTERMEDIATE, L.dw, L.ds, nullptr, QWEN_HIDDEN, out, att, st);
+  QWEN_HIP(hipGetLastError());
+}
 
 void run_decode_attention(const DevLayer& L, const float* x, const DecodeBatch& b, float* att, Arena& a,
                           hipStream_t st) {
-  const int T = b.tokens;
-  float* xn = a.alloc_n<float>((size_t)T * QWEN_HIDDEN);
-  float* q = a.alloc_n<float>((size_t)T * QWEN_HIDDEN);
-  float* k = a.alloc_n<float>((size_t)T * QWEN_KV_WIDTH);
-  float* v = a.alloc_n<float>((size_t)T * QWEN_KV_WIDTH);
-  float* ctx = a.alloc_n<float>((size_t)T * QWEN_HIDDEN);
-  launch_rmsnorm_ordered(x, L.ln, xn, T, false, st);
-  launch_project_ordered(xn, T, QWEN_HIDDEN, L.qw, L.qs, L.qb, QWEN_HIDDEN, q, nullptr, st);
-  launch_project_ordered(xn, T, QWEN_HIDDEN, L.kw, L.ks, L.kb, QWEN_KV_WIDTH, k, nullptr, st);
-  launch_project_ordered(xn, T, QWEN_HIDDEN, L.vw, L.vs, L.vb, QWEN_KV_WIDTH, v, nullptr, st);
-  launch_rope_append_decode(q, k, v, b.pos, b.rope, b.rope_per_token, b.k_cache, b.v_cache, b.cache_stride,
-                            b.max_keys, T, st);
-  launch_attention_ordered(q, b.k_cache, b.v_cache, b.cache_stride, b.pos, b.max_keys, T, false, 0, ctx, st);
-  launch_project_ordered(ctx, T, QWEN_HIDDEN, L.ow, L.os, nullptr, QWEN_HIDDEN, att, nullptr, st);
-  QWEN_HIP(hipGetLastError());
+  const DecodeWorkspace w = carve_decode_workspace(a.alloc_n<float>(decode_workspace_floats(b.tokens)), b.tokens);
+  run_decode_attention_ws(L, x, b, att, w, st);
 }
 
 void run_decode_mlp(const DevLayer& L, const float* att, int T, float* out, Arena& a, hipStream_t st) {
-  float* pn = a.alloc_n<float>((size_t)T * QWEN_HIDDEN);
-  float* g = a.alloc_n<float>((size_t)T * QWEN_INTERMEDIATE);
-  float* u = a.alloc_n<float>((size_t)T * QWEN_INTERMEDIATE);
-  float* s = a.alloc_n<float>((size_t)T * QWEN_INTERMEDIATE);
-  launch_rmsnorm_ordered(att, L.post_ln, pn, T, false, st);
-  launch_project_ordered(pn, T, QWEN_HIDDEN, L.gw, L.gs, nullptr, QWEN_INTERMEDIATE, g, nullptr, st);
-  launch_project_ordered(pn, T, QWEN_HIDDEN, L.uw, L.us, nullptr, QWEN_INTERMEDIATE, u, nullptr, st);
-  launch_silu_mul(g, u, s, (size_t)T * QWEN_INTERMEDIATE, false, st);
-  launch_project_ordered(s, T, QWEN_INTERMEDIATE, L.dw, L.ds, nullptr, QWEN_HIDDEN, out, att, st);
-  QWEN_HIP(hipGetLastError());
+  const DecodeWorkspace w = carve_decode_workspace(a.alloc_n<float>(decode_workspace_floats(T)), T);
+  run_decode_mlp_ws(L, att, T, out, w, st);
 }
 
 void run_prefill_attention(const DevLayer& L, const float* x, int T, int past, const float* rope, float* k_rows,

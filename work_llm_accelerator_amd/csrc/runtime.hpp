@@ -127,6 +127,20 @@ size_t prefill_workspace_bytes(int tokens);
 void run_decode_attention(const DevLayer& L, const float* x, const DecodeBatch& b, float* att, Arena& a,
                           hipStream_t st);
 void run_decode_mlp(const DevLayer& L, const float* att, int tokens, float* out, Arena& a, hipStream_t st);
+
+// The same executors over caller-provided intermediates (device memory of `tokens` rows each):
+// attention xn, q [tokens][1536], k, v [tokens][256], ctx [tokens][1536]; MLP pn [tokens][1536],
+// g, u, s [tokens][8960].
+struct DecodeWorkspace {
+  float *xn, *q, *k, *v, *ctx, *pn, *g, *u, *s;
+};
+// Floats of a DecodeWorkspace of `tokens` rows, and its carve-up of `base` (each part 64-float aligned).
+size_t decode_workspace_floats(int tokens);
+DecodeWorkspace carve_decode_workspace(float* base, int tokens);
+void run_decode_attention_ws(const DevLayer& L, const float* x, const DecodeBatch& b, float* att,
+                             const DecodeWorkspace& w, hipStream_t st);
+void run_decode_mlp_ws(const DevLayer& L, const float* att, int tokens, float* out, const DecodeWorkspace& w,
+                       hipStream_t st);
 // Prefill attention of `tokens` new tokens at positions past..past+tokens-1 of one sequence whose cache
 // rows start at k_rows / v_rows (rows 0..past-1 hold the earlier tokens; the new rows are written).
 void run_prefill_attention(const DevLayer& L, const float* x, int tokens, int past, const float* rope, float* k_rows,
