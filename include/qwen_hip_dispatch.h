@@ -48,6 +48,21 @@ int qwen_hip_prefill_dispatch_layers(const qwen_prefill_descriptor* descriptors,
                                      const uint8_t* weight_ddr, const float* scale_ddr, float* kv_cache_ddr,
                                      float* activation_ddr, void* stream, int* completed_layer_count);
 
+/* No counterpart in the reference (its host wrappers run on the CPU and have no device memory to
+ * allocate).  For callers that cannot allocate device memory: code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc.  Same descriptors, DDR ports, validation, status
+ * codes, completed count and results (bit for bit) as qwen_hip_decode_dispatch_layers, except that it
+ * calls no allocating routine (no hipMalloc / hipFree, no allocating library call) and does not
+ * synchronize: every layer is queued on `stream` and the call returns.  The intermediates of the layer
+ * being run live in one static device array of 147,456 bytes per GPU (one token's workspace, the
+ * attention output row, the descriptor's RoPE row and position), held until the process ends; one
+ * token per descriptor fixes that need, so no argument can exceed it.  The array keeps the last
+ * call's contents, and every value a layer reads from it is written earlier in the same call.  Calls
+ * that overlap on one GPU (other streams, other threads) race on the array. */
+int qwen_hip_decode_dispatch_layers_noalloc(const qwen_decode_descriptor* descriptors, int layer_count,
+                                            const uint8_t* weight_ddr, const float* scale_ddr, float* kv_cache_ddr,
+                                            float* activation_ddr, void* stream, int* completed_layer_count);
+
 #ifdef __cplusplus
 }
 #endif

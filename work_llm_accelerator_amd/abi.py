@@ -89,6 +89,7 @@ EXTRA_SIGNATURES: dict[str, tuple[list, object]] = {
     # DDR images on the device
     "qwen_hip_decode_dispatch_layers": ([c_void_p, c_int, P, P, P, P, P, c_void_p], c_int),
     "qwen_hip_prefill_dispatch_layers": ([c_void_p, c_int, P, P, P, P, P, c_void_p], c_int),
+    "qwen_hip_decode_dispatch_layers_noalloc": ([c_void_p, c_int, P, P, P, P, P, c_void_p], c_int),
 }
 
 _LIB: ctypes.CDLL | None = None

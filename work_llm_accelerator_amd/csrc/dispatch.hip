@@ -10,6 +10,7 @@
 #include <mutex>
 #include <string>
 #include <vector>
+#include <stdexcept>
 
 #include "kernels.hpp"
 #include "qwen_hip_dispatch.h"
@@ -18,7 +19,33 @@
 
 using namespace qwen;
 
+// ---------------------------------------------------------------------------------------------
+// Scratch of the allocation-free decode dispatch: one token's intermediates (decode_workspace_floats(1))
+// plus the RoPE row and position of the descriptor being run.  One copy per GPU, held until the
+// process ends; host code reaches it only through the address hipGetSymbolAddress returns for the
+// current device (the array's name is a host-side stand-in, not a device address).
+// ---------------------------------------------------------------------------------------------
+constexpr size_t kNoAllocWorkspaceFloats = 35072;  // decode_workspace_floats(1)
+constexpr size_t kNoAllocAttOffset = kNoAllocWorkspaceFloats;             // attention output row
+constexpr size_t kNoAllocRopeOffset = kNoAllocAttOffset + QWEN_HIDDEN;    // cos[64] | sin[64]
+constexpr size_t kNoAllocPosOffset = kNoAllocRopeOffset + QWEN_HEAD_DIM;  // the position (an int)
+constexpr size_t kNoAllocScratchFloats = 36864;                          // 147,456 bytes in all
+static_assert(kNoAllocPosOffset < kNoAllocScratchFloats, "scratch layout");
+static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
+
 namespace {
+
+struct RopeRowArg {
+  float cs[128];  // cos[64] then sin[64] of one position (host libm, qwen_decode_attention_kernel.cpp:29-42)
+};
+
+// Writes the descriptor's RoPE row and position into the scratch (kernel arguments, so nothing is
+// copied from host memory and nothing is allocated).  One block of 128 threads.
+__global__ void __launch_bounds__(128) stage_rope_row_kernel(float* __restrict__ rope, int* __restrict__ pos,
+                                                              RopeRowArg row, int position) {
+  rope[threadIdx.x] = row.cs[threadIdx.x];
+  if (threadIdx.x == 0) *pos = position;
+}
 
 template <class Fn>
 int guarded_dispatch(Fn&& fn) {
@@ -43,6 +70,23 @@ DevLayer device_layer(const uint8_t* wd, const float* sd, uint64_t w_base, uint6
 
 void set_completed(int* completed, int n) {
   if (completed) *completed = n;
+}
+
+// Device address of `scratch` on the current device, looked up once per device.
+float* noalloc_scratch() {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static float* addr[kMaxDevices] = {};
+  int dev = 0;
+  QWEN_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) throw std::runtime_error("device index beyond the scratch table");
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[dev]) {
+    void* p = nullptr;
+    QWEN_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    addr[dev] = static_cast<float*>(p);
+  }
+  return addr[dev];
 }
 
 }  // namespace
@@ -124,6 +168,44 @@ int qwen_hip_prefill_dispatch_layers(const qwen_prefill_descriptor* dsc, int n, 
     }
     QWEN_HIP(hipStreamSynchronize(st));
     rt.arena.reset();
+    set_completed(completed, done);
+    return status;
+  });
+}
+
+int qwen_hip_decode_dispatch_layers_noalloc(const qwen_decode_descriptor* dsc, int n, const uint8_t* wd,
+                                            const float* sd, float* kv, float* act, void* stream, int* completed) {
+  set_completed(completed, 0);
+  if (!dsc || n <= 0) return QWEN_ERR_DECODE_DESC;  // qwen_decode_top_wrapper.cpp:118-120
+  return guarded_dispatch([&]() -> int {
+    if (decode_workspace_floats(1) > kNoAllocWorkspaceFloats)
+      throw std::runtime_error("one token's decode workspace exceeds the static scratch");
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    float* base = noalloc_scratch();
+    const DecodeWorkspace w = carve_decode_workspace(base, 1);
+    float* att = base + kNoAllocAttOffset;
+    float* rope = base + kNoAllocRopeOffset;
+    int* pos = reinterpret_cast<int*>(base + kNoAllocPosOffset);
+    int status = QWEN_OK, done = 0;
+    for (; done < n; ++done) {
+      const qwen_decode_descriptor& d = dsc[done];
+      if ((status = decode_descriptor_status(d)) != QWEN_OK) break;
+      if (!wd || !sd || !kv || !act) {
+        status = QWEN_ERR_DECODE_PORT;
+        break;
+      }
+      // every layer reuses the scratch in stream order: its RoPE row and position are written by a kernel
+      // queued before its own kernels, after the previous layer's
+      RopeRowArg row;
+      decode_rope_row_host(d.past_seq_len, row.cs);
+      hipLaunchKernelGGL(stage_rope_row_kernel, dim3(1), dim3(128), 0, st, rope, pos, row, d.past_seq_len);
+      const DevLayer L = device_layer(wd, sd, d.layer_weights_base_addr, d.layer_scales_base_addr);
+      DecodeBatch b{1, pos, rope, true, kv + d.k_cache_base_addr / 4, kv + d.v_cache_base_addr / 4, 0,
+                    d.past_seq_len + 1};
+      run_decode_attention_ws(L, act + d.input_token_addr / 4, b, att, w, st);
+      run_decode_mlp_ws(L, att, 1, act + d.output_token_addr / 4, w, st);
+    }
+    QWEN_HIP(hipGetLastError());
     set_completed(completed, done);
     return status;
   });
