@@ -1,21 +1,20 @@
 """Throughput of the quantized Qwen2.5-1.5B decoder-layer hot path on one MI355X.
 
-Default workload: 28-layer Qwen2.5-1.5B-shaped batched decode, 64 sequences, each with a
-4096-position KV history (K/V N(0,1), INT4 quantize/dequantize per row) and one new random token
-per step, positions 4096..4127 (32 steps, then the cycle repeats).  A step is one decode token for
-all 64 sequences through all 28 layers (embedding gather + 28 x [RMSNorm, QKV, RoPE + KV append,
-GQA attention, O, RMSNorm, gate/up + SiLU, down + residual, bf16 rounding]); weights are
-random-init N(0, 0.02), rounded to bf16 and quantized per row to INT4 on the device.
+The default run measures the whole metric (decode tok/s and prefill tok/s, with their rooflines) and
+prints ONE JSON line:
+  value     28-layer Qwen2.5-1.5B-shaped batched decode, 64 sequences, each with a 4096-position KV
+            history (K/V N(0,1), INT4 quantize/dequantize per row) and one new random token per step,
+            positions 4096..4127 (32 steps, then the cycle repeats); a step is one decode token for
+            all 64 sequences through all 28 layers (embedding gather + 28 x [RMSNorm, QKV, RoPE + KV
+            append, GQA attention, O, RMSNorm, gate/up + SiLU, down + residual, bf16 rounding]);
+  prefill   28-layer prefill of 8 independent sequences x 2048 random tokens (causal, full KV cache);
+  greedy    28-layer batch-1 greedy generation: a 512-token prompt prefilled, then 128 decode steps
+            through the final RMSNorm, the tied bf16 lm_head and argmax, all on the device.
+Weights are random-init N(0, 0.02), rounded to bf16 and quantized per row to INT4 on the device
+(seeds 4, 3 and 2).  Each part carries its dominant kernel's roofline (HIP events on the stream the
+kernel runs on) and the reference's CPU path timed on this machine's host cores on a bounded sample.
 
-Printed: one JSON line with whole-job tok/s, the dominant kernel's roofline (decode attention
-streaming the fp32 KV cache, timed in isolation with HIP events on the model's stream) and the
-reference C++ host path timed on this machine's CPU on a bounded sample.
-
---workload decode1 is batch-1 greedy generation (512-token prompt prefilled, then greedy steps
-through the final norm, the tied bf16 lm_head and argmax); --workload prefill is 8 x 2048 causal
-prefill.
-
-    python bench.py [--steps K] [--warmup W] [--workload decode64|decode1|prefill] [--mode fast|ordered]
+    python bench.py [--steps K] [--warmup W] [--workload all|decode64|decode1|prefill] [--mode fast|ordered]
 """
 
 from __future__ import annotations
@@ -45,9 +44,9 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=32)
     ap.add_argument("--warmup", type=int, default=4)
-    ap.add_argument("--workload", default="decode64", choices=["decode64", "decode1", "prefill"])
+    ap.add_argument("--workload", default="all", choices=["all", "decode64", "decode1", "prefill"])
     ap.add_argument("--mode", default="fast", choices=["fast", "ordered"])
-    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of each CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     return ap.parse_args()
 
@@ -94,11 +93,50 @@ def cpu_baseline_decode(past: int, budget_s: float) -> dict:
         if st != 0:
             raise RuntimeError(f"CPU baseline returned {st}")
     t_layer = float(np.median(times))
-    return {"value": 1.0 / (LAYERS * t_layer), "unit": "tok/s", "cores": 1, "kind": kind,
-            "sample": f"{len(times)} single-layer decode steps at KV length {past + 1} through "
+    return {"value": 1.0 / (LAYERS * t_layer), "unit": "tok/s", "cores": 1, "kind": kind, "per_sequence": True,
+            "sample": f"{len(times)} single-layer decode steps of one sequence at KV length {past + 1} through "
                       f"{'the reference decode .so built from its sources' if kind == 'reference' else 'the oracle'}"
-                      f" (median {t_layer * 1e3:.1f} ms/layer-token, 1 thread), extrapolated x{LAYERS} layers "
-                      f"for one sequence; CPU: {cpu_model()}, {os.cpu_count()} visible cores"}
+                      f" (median {t_layer * 1e3:.1f} ms/layer-token, 1 thread), extrapolated x{LAYERS} layers. "
+                      f"The reference decodes one sequence at a time, so this per-sequence rate is also its "
+                      f"throughput on a batch; CPU: {cpu_model()}, {os.cpu_count()} visible cores"}
+
+
+def cpu_baseline_prefill(seq: int, budget_s: float) -> dict:
+    """The reference prefill arithmetic on one host core: the oracle's restatement (the reference
+    prefill library needs Catapult's ac_channel.h and cannot be built here), one layer of `seq`
+    tokens per call, extrapolated x28 layers."""
+    from work_llm_accelerator_amd.layout import HIDDEN, KV_WIDTH, LAYOUT
+
+    port = ROOT / "oracle" / "build" / "libqwen_oracle.so"
+    if not port.exists():
+        os.system(f"make -s -C {ROOT / 'oracle'} oracle >/dev/null 2>&1")
+    lib = ctypes.CDLL(str(port))
+    f32 = np.ctypeslib.ndpointer(dtype=np.float32, ndim=1, flags="C_CONTIGUOUS")
+    u8 = np.ctypeslib.ndpointer(dtype=np.uint8, ndim=1, flags="C_CONTIGUOUS")
+    fn = lib.oracle_prefill_layer_uncapped
+    fn.argtypes = [f32, ctypes.c_int, u8, f32, f32, f32, f32]
+    fn.restype = ctypes.c_int
+    rng = np.random.default_rng(0)
+    w = rng.integers(0, 256, LAYOUT.total_parameter_bytes, dtype=np.uint8)
+    sc = np.full((LAYOUT.total_parameter_bytes + 3) // 4, 0.01, np.float32)
+    x = rng.standard_normal(seq * HIDDEN, dtype=np.float32)
+    kc = np.zeros(seq * KV_WIDTH, np.float32)
+    vc = np.zeros(seq * KV_WIDTH, np.float32)
+    out = np.zeros(seq * HIDDEN, np.float32)
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 2 or (time.perf_counter() < t_end and len(times) < 20):
+        t0 = time.perf_counter()
+        if fn(x, seq, w, sc, kc, vc, out) != 0:
+            raise RuntimeError("CPU prefill baseline failed")
+        times.append(time.perf_counter() - t0)
+    t_call = float(np.median(times))
+    return {"value": seq / (LAYERS * t_call), "unit": "tok/s", "cores": 1, "kind": "port",
+            "sample": f"{len(times)} single-layer prefills of {seq} tokens (the reference's per-call cap) through "
+                      f"the oracle restatement of the reference prefill arithmetic (median {t_call:.2f} s per call, "
+                      f"1 thread), extrapolated x{LAYERS} layers; at 2048 tokens the causal attention adds about "
+                      f"10% per token that this sample does not include; CPU: {cpu_model()}, "
+                      f"{os.cpu_count()} visible cores"}
 
 
 def cpu_model() -> str:
@@ -337,6 +375,24 @@ def bench_prefill(args, torch, batch: int, seq: int, seed: int) -> dict:
     return res
 
 
+def decode64_config():
+    return {"workload": "28-layer Qwen2.5-1.5B-shaped batched decode: 64 sequences x KV history 4096 (positions "
+                        "4096..4127), 1 new random token per sequence per step, seed 4",
+            "layers": LAYERS, "batch": 64, "kv_length": "4097..4128"}
+
+
+def prefill_config():
+    return {"workload": "28-layer Qwen2.5-1.5B-shaped prefill: 8 sequences x 2048 random tokens, causal, full KV "
+                        "cache written, seed 3", "layers": LAYERS, "batch": 8, "seq_len": 2048}
+
+
+def greedy_config(args, steps):
+    return {"workload": "28-layer Qwen2.5-1.5B-shaped greedy generation, batch 1: a 512-token prompt of uniform "
+                        f"random ids prefilled, then {steps} greedy decode steps (embedding, 28 layers, final RMSNorm, "
+                        "tied bf16 lm_head over 151936 tokens, argmax), seed 2", "layers": LAYERS, "batch": 1,
+            "prompt": 512, "kv_length": f"{512 + args.warmup + 1}..{512 + args.warmup + steps}"}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -349,39 +405,46 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs an MI355X (no GPU visible)", file=sys.stderr)
         sys.exit(1)
-    if args.workload == "decode64":
-        batch, history, seed = 64, 4096, 4
-        r = bench_decode(args, torch, batch, history, seed)
-        config = {"workload": "28-layer Qwen2.5-1.5B-shaped batched decode: 64 sequences x KV history 4096 "
-                              "(positions 4096..4127), 1 new random token per sequence per step, seed 4",
-                  "layers": LAYERS, "batch": batch, "kv_length": f"{history + 1}..{history + 32}", "mode": args.mode}
-        unit, cpu_past = "tok/s", history
+    dtype = "int4 weights x int8 two-limb MFMA, f32" if args.mode == "fast" else "f32"
+    common = {"n_gpus": 1, "warmup": args.warmup, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+              "dtype": dtype, "data": "synthetic (random-init weights, random tokens, N(0,1) quantized KV)"}
+
+    def part(r, config, steps):
+        d = {"value": r["value"], "unit": "tok/s", "steps": steps, "ms_per_step": r["ms_per_step"],
+             "config": {**config, "mode": args.mode}}
+        for k in ("roofline", "step_roofline", "kernels", "prefill"):
+            if k in r:
+                d[k] = r[k]
+        return d
+
+    greedy_steps = 128
+    if args.workload in ("all", "decode64"):
+        r = bench_decode(args, torch, 64, 4096, 4)
+        line = {"metric": METRIC, **part(r, decode64_config(), args.steps), **common}
+        if args.workload == "all":
+            pr = bench_prefill(argparse.Namespace(**{**vars(args), "steps": max(3, min(args.steps, 8)),
+                                                     "warmup": min(args.warmup, 2)}), torch, 8, 2048, 3)
+            line["prefill"] = part(pr, prefill_config(), max(3, min(args.steps, 8)))
+            gr = bench_greedy(argparse.Namespace(**{**vars(args), "steps": greedy_steps}), torch, 512, 2)
+            line["greedy"] = part(gr, greedy_config(args, greedy_steps), greedy_steps)
     elif args.workload == "decode1":
-        prompt, seed = 512, 2
-        r = bench_greedy(args, torch, prompt, seed)
-        config = {"workload": "28-layer Qwen2.5-1.5B-shaped greedy generation, batch 1: a 512-token prompt of "
-                              "uniform random ids prefilled, then greedy decode steps (embedding, 28 layers, final "
-                              "RMSNorm, tied bf16 lm_head over 151936 tokens, argmax), seed 2",
-                  "layers": LAYERS, "batch": 1, "prompt": prompt,
-                  "kv_length": f"{prompt + args.warmup + 1}..{prompt + args.warmup + args.steps}", "mode": args.mode}
-        unit, cpu_past = "tok/s", prompt
+        r = bench_greedy(args, torch, 512, 2)
+        line = {"metric": METRIC, **part(r, greedy_config(args, args.steps), args.steps), **common}
     else:
-        batch, seq, seed = 8, 2048, 3
-        r = bench_prefill(args, torch, batch, seq, seed)
-        config = {"workload": "28-layer Qwen2.5-1.5B-shaped prefill: 8 sequences x 2048 tokens, causal, full KV "
-                              "cache written, seed 3", "layers": LAYERS, "batch": batch, "seq_len": seq,
-                  "mode": args.mode}
-        unit, cpu_past = "tok/s", None
-    line = {"metric": METRIC, "value": r["value"], "unit": unit, "n_gpus": 1, "steps": args.steps,
-            "warmup": args.warmup, "ms_per_step": r["ms_per_step"], "higher_is_better": True, "scaling": "weak",
-            "vs_baseline": None, "dtype": "int4 weights x int8 two-limb MFMA, f32" if args.mode == "fast" else "f32",
-            "data": "synthetic (random-init weights, random tokens, N(0,1) quantized KV)", "config": config}
-    for k in ("roofline", "step_roofline", "kernels", "prefill"):
-        if k in r:
-            line[k] = r[k]
+        r = bench_prefill(args, torch, 8, 2048, 3)
+        line = {"metric": METRIC, **part(r, prefill_config(), args.steps), **common}
     line["copy_bandwidth"] = copy_bandwidth(torch)
-    if not args.no_cpu and cpu_past is not None:
-        line["cpu_baseline"] = cpu_baseline_decode(cpu_past, args.cpu_seconds)
+    if not args.no_cpu:
+        if args.workload in ("all", "decode64"):
+            line["cpu_baseline"] = cpu_baseline_decode(4096, args.cpu_seconds)
+        if args.workload == "all":
+            line["prefill"]["cpu_baseline"] = cpu_baseline_prefill(128, args.cpu_seconds / 2)
+            line["greedy"]["cpu_baseline"] = cpu_baseline_decode(576, args.cpu_seconds / 2)
+            line["greedy"]["cpu_baseline"]["sample"] += " (the lm_head is not included)"
+        elif args.workload == "decode1":
+            line["cpu_baseline"] = cpu_baseline_decode(576, args.cpu_seconds)
+        else:
+            line["cpu_baseline"] = cpu_baseline_prefill(128, args.cpu_seconds)
     print(json.dumps(line), flush=True)
 
 
