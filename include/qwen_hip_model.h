@@ -139,7 +139,9 @@ int qwen_hip_model_greedy(qwen_hip_model* m, const float* hidden, int count, int
 
 /* Re-runs one kernel of the most recent decode/prefill call `reps` times in isolation, on the
  * model's stream between two HIP events, with that call's shapes and the weights of `layer`;
- * *avg_ms receives the mean duration of one launch.  The re-run reads that call's positions and K/V
+ * *avg_ms receives the mean duration of one launch (the decode attention takes the layers' caches in
+ * turn from `layer` on, so that no launch re-reads rows a recent launch left in the last-level cache,
+ * as in a decode step).  The re-run reads that call's positions and K/V
  * caches through the pointers it was given, so the caller must keep those buffers allocated until
  * time_kernel returns (their contents may have changed: only the timing is reported). */
 int qwen_hip_model_time_kernel(qwen_hip_model* m, int kernel, int layer, int reps, float* avg_ms);

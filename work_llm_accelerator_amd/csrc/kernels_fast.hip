@@ -2483,9 +2483,9 @@ AttnDecodePlan plan_attn_decode(int batch, int max_keys, int cus) {
       per_cu = 1;
     return int2{prop.multiProcessorCount, per_cu};
   }();
-  const int slots = (cus > 0 && cus < dev_slots.x ? cus : dev_slots.x) * dev_slots.y;
-  // 3 of every 4 co-resident slots: the KV stream runs faster at 12 than at 16 waves per CU.
-  int nsplit = (3 * slots / 4) / (QWEN_KV_HEADS * (batch > 0 ? batch : 1));
+  // at most 3 co-resident blocks per CU: the KV stream runs faster at 12 than at 16 waves per CU
+  const int slots = (cus > 0 && cus < dev_slots.x ? cus : dev_slots.x) * (dev_slots.y < 3 ? dev_slots.y : 3);
+  int nsplit = slots / (QWEN_KV_HEADS * (batch > 0 ? batch : 1));
   nsplit = nsplit < 1 ? 1 : (nsplit > kAttnMaxSplits ? kAttnMaxSplits : nsplit);
   int chunk = (max_keys + nsplit - 1) / nsplit;
   // Small batches cannot fill the device: each extra split then costs more in the merge (one memory

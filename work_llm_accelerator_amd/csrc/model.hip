@@ -698,11 +698,17 @@ int qwen_hip_model_time_kernel(qwen_hip_model* m, int kernel, int layer, int rep
     const FastLayer& f = m->fast[layer];
     float* kc = c.k_cache + (size_t)layer * c.layer_stride;
     float* vc = c.v_cache + (size_t)layer * c.layer_stride;
+    int rep = 0;
     auto once = [&]() {
+      // the decode attention reads layer (layer + rep) % layers: each launch streams KV rows that no recent
+      // launch has read, as in a decode step (re-reading one layer's rows would be served partly from the
+      // 256 MB last-level cache)
+      const size_t la = (size_t)((layer + rep++) % m->layers) * c.layer_stride;
       switch (kernel) {
         case QWEN_KERNEL_ATTN_DECODE:
-          launch_attn_decode(w.qkv, (int)kQkvRows, kc, vc, c.seq_stride, c.positions, c.batch, c.max_keys, plan,
-                             w.part, w.pml, w.arrivals, nullptr, w.xq, w.sx, w.sums, m->stream);
+          launch_attn_decode(w.qkv, (int)kQkvRows, c.k_cache + la, c.v_cache + la, c.seq_stride, c.positions,
+                             c.batch, c.max_keys, plan, w.part, w.pml, w.arrivals, nullptr, w.xq, w.sx, w.sums,
+                             m->stream);
           break;
         case QWEN_KERNEL_GEMM_GATE_UP:
           m->gemm(w, T, QWEN_HIDDEN, QWEN_INTERMEDIATE, f.gate, f.sw_gate, nullptr, w.tmp, QWEN_INTERMEDIATE,
