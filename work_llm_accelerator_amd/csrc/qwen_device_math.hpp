@@ -123,41 +123,6 @@ QWEN_HD float approx_exp(float v) {  // :87-110; `term *= s / deg` divides first
   return series > 0.0f ? series : 0.0f;
 }
 
-// approx_exp evaluated in Horner form with reciprocal constants (no divisions): the same
-// halving ladder and degree-6 series, within a few ulp of approx_exp.  FAST kernels only.
-// approx_exp_fast_ladder is the ladder written as loops; approx_exp_fast computes the same values
-// without data-dependent branches: the number k of halvings is read from the exponent of -v
-// (k = ceil(log2(-v)) for v < -1, k <= 4 above -16), v*2^-k is exact (ldexp), and the k squarings
-// are applied by selects.  Both give identical bits for every input (host check in the tests).
-QWEN_HD float approx_exp_fast_ladder(float v) {
-  if (v <= -16.0f) return 0.0f;
-  int halves = 0;
-  float s = v;
-  while (s < -1.0f) {
-    s *= 0.5f;
-    ++halves;
-  }
-  float r = 1.0f + s * (1.0f + s * (0.5f + s * (1.0f / 6.0f + s * (1.0f / 24.0f + s * (1.0f / 120.0f +
-                                                                                        s * (1.0f / 720.0f))))));
-  for (int k = 0; k < halves; ++k) r *= r;
-  return r > 0.0f ? r : 0.0f;
-}
-
-QWEN_HD float approx_exp_fast(float v) {
-  const uint32_t nb = f32_bits(-v);
-  const int e = (int)((nb >> 23) & 0xFFu) - 127;
-  const int k = v < -1.0f ? e + ((nb & 0x7FFFFFu) != 0u ? 1 : 0) : 0;
-  const float s = ldexpf(v, -k);
-  float r = 1.0f + s * (1.0f + s * (0.5f + s * (1.0f / 6.0f + s * (1.0f / 24.0f + s * (1.0f / 120.0f +
-                                                                                        s * (1.0f / 720.0f))))));
-  r = k > 0 ? r * r : r;
-  r = k > 1 ? r * r : r;
-  r = k > 2 ? r * r : r;
-  r = k > 3 ? r * r : r;
-  r = v <= -16.0f ? 0.0f : r;
-  return r > 0.0f ? r : 0.0f;
-}
-
 __device__ __forceinline__ float silu_decode(float v) { return v / (1.0f + glibc_expf(-v)); }  // mlp :79-81
 QWEN_HD float silu_prefill(float v) { return v / (1.0f + approx_exp(-v)); }                   // mlp :256-258
 
