@@ -1122,19 +1122,21 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   const size_t row_stride_x = (size_t)a.in_dim * 2u;
 
   // activation slice -> LDS: chunk c, rows 4q..4q+3 per load (1 KiB), wave w takes chunks w, w+4KSW, ..
-  for (int c = threadIdx.x >> 6; c < (kMade ? 0 : NKC); c += 4 * KSW) {
+  auto issue_slice = [&]() {
+    for (int c = threadIdx.x >> 6; c < NKC; c += 4 * KSW) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int row = 4 * q + (lane >> 4);
-      const int tok = min(tok0 + row, a.tokens - 1);  // rows past the last token reload a valid row
-      const int seg = (lane & 15) ^ row;
-      const uint8_t* src = reinterpret_cast<const uint8_t*>(a.xq) + (size_t)tok * row_stride_x +
-                           (size_t)(kc0 + c) * 256u + seg * 16;
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src),
-                                       (__attribute__((address_space(3))) void*)(xs + (c * 16 + 4 * q) * 256), 16, 0,
-                                       0);
+      for (int q = 0; q < 4; ++q) {
+        const int row = 4 * q + (lane >> 4);
+        const int tok = min(tok0 + row, a.tokens - 1);  // rows past the last token reload a valid row
+        const int seg = (lane & 15) ^ row;
+        const uint8_t* src = reinterpret_cast<const uint8_t*>(a.xq) + (size_t)tok * row_stride_x +
+                             (size_t)(kc0 + c) * 256u + seg * 16;
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src),
+                                         (__attribute__((address_space(3))) void*)(xs + (c * 16 + 4 * q) * 256), 16,
+                                         0, 0);
+      }
     }
-  }
+  };
   // decode position of this lane's token (RoPE epilogue), loaded with the weights
   const int P = ROPE ? a.pos[min(tok0 + col, a.tokens - 1)] : 0;
   uint4 wv[RTW][D][KC];
@@ -1143,23 +1145,46 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   const int tok_l = min(tok0 + col, a.tokens - 1);
   float sx_l = 0.0f;
   int sh_l = 0, sl_l = 0;
-  // Weight tiles -> registers, then the epilogue's per-row scales (and bias) and per-token scale and
-  // limb sums: none depends on the MFMAs, and loaded after them they would cost one more round trip.
-  // With a made slice (kMade) this runs inside the prologue, after the prologue's own loads: a wave's
-  // loads return in order, so the prologue's few loads must not queue behind the weights.
-  auto issue_loads = [&]() {
+  // The decode SiLU's exp table, copied to LDS before the MFMAs: read from constant memory in the
+  // epilogue, each of a lane's SiLU evaluations waited on one more memory round trip (several tokens;
+  // with one token the copy cost as much as it saved).
+  constexpr bool kTab = EPI == kEpiSiluMul && !kMade;
+  __shared__ uint64_t exp_tab[kTab ? 32 : 1];
+  uint64_t tab_v = 0;
 #pragma unroll
-    for (int r = 0; r < RTW; ++r) {
-      const int rt = rg * 4 * RTW + wave + 4 * r;
-      ok[r] = rt < row_tiles;
-      const size_t base = ((size_t)(ok[r] ? rt : 0) * nkc_all + kc0 + kg * KC) * 64u + lane;
+  for (int r = 0; r < RTW; ++r) ok[r] = rg * 4 * RTW + wave + 4 * r < row_tiles;
+  // Weight tiles -> registers in K-chunk order (one 16-byte load per chunk and tile, chunk c's loads
+  // before chunk c+1's), and the epilogue's per-row scales (and bias) and per-token scale and limb
+  // sums: none depends on the MFMAs, and loaded after them they would cost one more round trip.
+  // (A made slice waits for every load before its first MFMA, so there the loads go tile by tile:
+  // each tile's chunks are one contiguous run of memory.)
+  auto issue_weights = [&]() {
+    if constexpr (kMade) {
 #pragma unroll
-      for (int d = 0; d < D; ++d) {
-        const uint4* wp = reinterpret_cast<const uint4*>(d ? a.wp2 : a.wp) + base;
+      for (int r = 0; r < RTW; ++r) {
+        const int rt = rg * 4 * RTW + wave + 4 * r;
+        const size_t base = ((size_t)(ok[r] ? rt : 0) * nkc_all + kc0 + kg * KC) * 64u + lane;
 #pragma unroll
-        for (int c = 0; c < KC; ++c) wv[r][d][c] = wp[(size_t)c * 64u];  // cached: reused by the XCD's other token tiles
+        for (int d = 0; d < D; ++d) {
+          const uint4* wp = reinterpret_cast<const uint4*>(d ? a.wp2 : a.wp) + base;
+#pragma unroll
+          for (int c = 0; c < KC; ++c) wv[r][d][c] = wp[(size_t)c * 64u];
+        }
       }
+    } else {
+#pragma unroll
+      for (int c = 0; c < KC; ++c)
+#pragma unroll
+        for (int r = 0; r < RTW; ++r) {
+          const int rt = rg * 4 * RTW + wave + 4 * r;
+          const size_t base = ((size_t)(ok[r] ? rt : 0) * nkc_all + kc0 + kg * KC + c) * 64u + lane;
+#pragma unroll
+          for (int d = 0; d < D; ++d)  // cached: reused by the XCD's other token tiles
+            wv[r][d][c] = reinterpret_cast<const uint4*>(d ? a.wp2 : a.wp)[base];
+        }
     }
+  };
+  auto issue_scalars = [&]() {
 #pragma unroll
     for (int r = 0; r < RTW; ++r) {
       const int row0 = (ok[r] ? rg * 4 * RTW + wave + 4 * r : 0) * 16 + 4 * g;
@@ -1175,6 +1200,14 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
       sh_l = a.sums[2 * tok_l];
       sl_l = a.sums[2 * tok_l + 1];
     }
+    if constexpr (kTab) tab_v = kExp2Tab[lane & 31];
+  };
+  // With a made slice (kMade) the weights and scalars are issued inside the prologue, after the
+  // prologue's own loads: a wave's loads return in order, so the prologue's few loads must not queue
+  // behind the weights.
+  auto issue_loads = [&]() {
+    issue_weights();
+    issue_scalars();
   };
   __shared__ float pre_sx;
   __shared__ int pre_sums[2];
@@ -1192,10 +1225,25 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
     else
       issue_loads();
   }
-  if constexpr (!kMade) issue_loads();
-  __builtin_amdgcn_sched_barrier(0);  // every load above is in flight before any use
-  wait_vmcnt<0>();
-  __syncthreads();
+  if constexpr (kMade) {
+    __builtin_amdgcn_sched_barrier(0);  // every load above is in flight before any use
+    wait_vmcnt<0>();
+    __syncthreads();
+  } else {
+    // Scalars, then the activation slice, then the weights in chunk order.  A wave's loads return in
+    // order, so once at most the weight loads are outstanding its part of the slice has landed, and
+    // after the barrier the whole slice has; chunk c's MFMAs then wait only for chunk c's weights
+    // (the compiler's own waits on the weight registers), so the MFMAs run under the weight stream.
+    issue_scalars();
+    issue_slice();
+    issue_weights();
+    __builtin_amdgcn_sched_barrier(0);  // every load above is in flight before any use
+    wait_vmcnt<RTW * D * KC>();
+    if (kTab && threadIdx.x < 32) exp_tab[threadIdx.x] = tab_v;
+    if (kTab) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the table store lands before the barrier
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);  // the slice reads below stay after the barrier
+  }
 
   // RoPE cos/sin of pairs p = 16*wave + 4g + q, q < 4, at position P: in flight during the MFMAs
   const bool rope_in = ROPE && P >= 0 && P < a.limit;
@@ -1294,7 +1342,7 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
       if (EPI == kEpiSiluMul) {
         const double tot2 = (double)(accH[r][D - 1][q] - sh8) * 256.0 + (double)(accL[r][D - 1][q] - sl8);
         const float u = (float)(tot2 * sx) * sw2v[r][q];
-        const float sg = a.prefill_silu ? silu_prefill(v) : silu_decode(v);
+        const float sg = a.prefill_silu ? silu_prefill(v) : silu_decode(v, kTab ? exp_tab : kExp2Tab);
         y[r][q] = sg * u;
       } else if (EPI == kEpiResidual) {
         y[r][q] = a.resid[(size_t)tok * a.resid_stride + row0 + q] + v;

@@ -40,7 +40,9 @@ __device__ __constant__ static const uint64_t kExp2Tab[32] = {
     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
 };
 
-__device__ __forceinline__ float glibc_expf(float x) {
+// `tab` is kExp2Tab or a copy of it (e.g. in LDS, so that a kernel epilogue does not wait on a
+// memory load per call); the result does not depend on where the table is read from.
+__device__ __forceinline__ float glibc_expf(float x, const uint64_t* tab = kExp2Tab) {
   // Special cases for |x| >= 88 (inf, nan, overflow, underflow), as in the published routine.
   const uint32_t ux = f32_bits(x);
   const uint32_t abstop = (ux >> 20) & 0x7ffu;
@@ -60,7 +62,7 @@ __device__ __forceinline__ float glibc_expf(float x) {
   const uint64_t ki = f64_bits(kd);
   kd -= kShift;
   const double r = __builtin_fma(kInvLn2N, xd, -kd);
-  uint64_t t = kExp2Tab[ki % 32u];
+  uint64_t t = tab[ki % 32u];
   t += ki << 47;
   const double s = bits_f64(t);
   const double z = __builtin_fma(c0, r, c1);
@@ -123,7 +125,9 @@ QWEN_HD float approx_exp(float v) {  // :87-110; `term *= s / deg` divides first
   return series > 0.0f ? series : 0.0f;
 }
 
-__device__ __forceinline__ float silu_decode(float v) { return v / (1.0f + glibc_expf(-v)); }  // mlp :79-81
+__device__ __forceinline__ float silu_decode(float v, const uint64_t* tab = kExp2Tab) {  // mlp :79-81
+  return v / (1.0f + glibc_expf(-v, tab));
+}
 QWEN_HD float silu_prefill(float v) { return v / (1.0f + approx_exp(-v)); }                   // mlp :256-258
 
 // Signed INT4 nibble of byte b: low nibble for even flat index (qwen_decode_attention_kernel.cpp:44-48).
