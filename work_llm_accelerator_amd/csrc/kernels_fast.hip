@@ -584,8 +584,13 @@ __device__ __forceinline__ void reg_tie(v4i& r) { asm volatile("" : "+v"(r)); }
 
 constexpr int kRasterGroup = 8;  // token tiles per raster group of the pipelined GEMM
 
-template <int NT, int RTW, int NBUF, int EPI, bool DUAL, int TW, int WPE = 1>
+// OWN (one token group of 4 tiles, TW = 1, NT = 4): the token tile a wave loads itself (tile wv) is
+// its accumulator slot 0, and the wave runs half of that slot's MFMAs before the chunk's barrier (its
+// own loads have landed by its own wait), so waves that reach the barrier late are absorbed by matrix
+// work instead of stalling the others.  Slot n holds token tile (wv + n) mod 4.
+template <int NT, int RTW, int NBUF, int EPI, bool DUAL, int TW, int WPE = 1, bool OWN = false>
 __global__ void __launch_bounds__(256 * TW) __attribute__((amdgpu_waves_per_eu(WPE))) gemm_i8_pipe_kernel(GemmArgs a) {
+  static_assert(!OWN || (TW == 1 && NT == 4), "own tile first: each of the 4 waves loads one token tile");
   constexpr int D = DUAL ? 2 : 1;
   constexpr int TOK = 16 * NT * TW;        // tokens per block (TW token groups of 16*NT)
   constexpr int XB = TOK * 256;                 // activation bytes per stage
@@ -690,8 +695,10 @@ __global__ void __launch_bounds__(256 * TW) __attribute__((amdgpu_waves_per_eu(W
         // chunk i has landed (this wave's part); the barrier covers the other waves' parts and
         // frees stage sidx-1, which the next issue refills.
         wait_vmcnt<(NBUF - 2) * OPS>();
-        __builtin_amdgcn_s_barrier();
-        issue(i + NBUF - 1, XS[(sidx + NBUF - 1) % NBUF], WS[(sidx + NBUF - 1) % NBUF]);
+        if (!OWN) {
+          __builtin_amdgcn_s_barrier();
+          issue(i + NBUF - 1, XS[(sidx + NBUF - 1) % NBUF], WS[(sidx + NBUF - 1) % NBUF]);
+        }
         // LDS reads of the stage: the weight tiles and token tile 0 first, then tile n+1 while the
         // matrix cores work on tile n.  They are issued as ds_read_b128 with explicit lgkmcnt waits:
         // the compiler cannot tell which stage an in-flight direct load writes, and would otherwise
@@ -705,40 +712,58 @@ __global__ void __launch_bounds__(256 * TW) __attribute__((amdgpu_waves_per_eu(W
         for (int d = 0; d < D; ++d)
 #pragma unroll
           for (int r = 0; r < RTW; ++r) wr[d][r] = lds_read_b128(wa + (uint32_t)((d * RTW + r) * 1024));
+        // LDS offset of the token tile in accumulator slot n
+        auto slot_off = [&](int n) { return (uint32_t)((((OWN ? wv : 0) + n) & (NT - 1)) * 16 * 256); };
         v4i bx[2][4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) bx[0][q] = lds_read_b128(xo[q]);
+        for (int q = 0; q < 4; ++q) bx[0][q] = lds_read_b128(xo[q] + slot_off(0));
         v4i a1[D][RTW], a2[D][RTW];
+        auto mfma_slot = [&](int n, const v4i* cur, int p0, int p1) {  // (d, r) pairs p0 <= p < p1
 #pragma unroll
-        for (int n = 0; n < NT; ++n) {
-          v4i* cur = bx[n & 1];
-          if (n + 1 < NT) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) bx[(n + 1) & 1][q] = lds_read_b128(xo[q] + (uint32_t)((n + 1) * 16 * 256));
-            lgkm_wait_tie<4>(cur[0], cur[1], cur[2], cur[3]);
-          } else {
-            lgkm_wait_tie<0>(cur[0], cur[1], cur[2], cur[3]);
+          for (int pr = 0; pr < D * RTW; ++pr) {
+            if (pr < p0 || pr >= p1) continue;
+            const int d = pr / RTW, r = pr % RTW;
+            accH[d][r][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[d][r], cur[0], accH[d][r][n], 0, 0, 0);
+            accH[d][r][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2[d][r], cur[1], accH[d][r][n], 0, 0, 0);
+            accL[d][r][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[d][r], cur[2], accL[d][r][n], 0, 0, 0);
+            accL[d][r][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2[d][r], cur[3], accL[d][r][n], 0, 0, 0);
           }
-          if (n == 0) {
-#pragma unroll
-            for (int d = 0; d < D; ++d)
-#pragma unroll
-              for (int r = 0; r < RTW; ++r) {
-                reg_tie(wr[d][r]);  // landed before token tile 0 (LDS reads complete in order)
-                unpack16(make_uint4((uint32_t)wr[d][r][0], (uint32_t)wr[d][r][1], (uint32_t)wr[d][r][2],
-                                    (uint32_t)wr[d][r][3]),
-                         a1[d][r], a2[d][r]);
-              }
-          }
+        };
+        auto unpack_weights = [&]() {
 #pragma unroll
           for (int d = 0; d < D; ++d)
 #pragma unroll
             for (int r = 0; r < RTW; ++r) {
-              accH[d][r][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[d][r], cur[0], accH[d][r][n], 0, 0, 0);
-              accH[d][r][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2[d][r], cur[1], accH[d][r][n], 0, 0, 0);
-              accL[d][r][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[d][r], cur[2], accL[d][r][n], 0, 0, 0);
-              accL[d][r][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2[d][r], cur[3], accL[d][r][n], 0, 0, 0);
+              reg_tie(wr[d][r]);  // landed before token tile 0 (LDS reads complete in order)
+              unpack16(make_uint4((uint32_t)wr[d][r][0], (uint32_t)wr[d][r][1], (uint32_t)wr[d][r][2],
+                                  (uint32_t)wr[d][r][3]),
+                       a1[d][r], a2[d][r]);
             }
+        };
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+          v4i* cur = bx[n & 1];
+          if (OWN && n == 0) {
+            // own tile and weights: landed by this wave's wait; the other tiles only after the barrier
+            lgkm_wait_tie<0>(cur[0], cur[1], cur[2], cur[3]);
+            unpack_weights();
+            mfma_slot(0, cur, 0, D * RTW / 2);
+            __builtin_amdgcn_s_barrier();
+            issue(i + NBUF - 1, XS[(sidx + NBUF - 1) % NBUF], WS[(sidx + NBUF - 1) % NBUF]);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) bx[1][q] = lds_read_b128(xo[q] + slot_off(1));
+            mfma_slot(0, cur, D * RTW / 2, D * RTW);
+            continue;
+          }
+          if (n + 1 < NT) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) bx[(n + 1) & 1][q] = lds_read_b128(xo[q] + slot_off(n + 1));
+            lgkm_wait_tie<4>(cur[0], cur[1], cur[2], cur[3]);
+          } else {
+            lgkm_wait_tie<0>(cur[0], cur[1], cur[2], cur[3]);
+          }
+          if (n == 0) unpack_weights();
+          mfma_slot(n, cur, 0, D * RTW);
         }
       }
     }
@@ -754,7 +779,7 @@ __global__ void __launch_bounds__(256 * TW) __attribute__((amdgpu_waves_per_eu(W
   int sh8[NT], sl8[NT];
 #pragma unroll
   for (int n = 0; n < NT; ++n) {
-    tok[n] = tok0 + tw * 16 * NT + n * 16 + col;
+    tok[n] = tok0 + tw * 16 * NT + (((OWN ? wv : 0) + n) & (NT - 1)) * 16 + col;
     const int tc = min(tok[n], a.tokens - 1);
     sxv[n] = a.sx[tc];
     const int2 sm = *reinterpret_cast<const int2*>(a.sums + 2 * tc);
@@ -2363,12 +2388,12 @@ static void launch_reduce(const GemmArgs& a, int splits, hipStream_t st) {
   }
 }
 
-template <int NT, int RTW, int NBUF, int EPI, bool DUAL, int TW = 1, int WPE = 1>
+template <int NT, int RTW, int NBUF, int EPI, bool DUAL, int TW = 1, int WPE = 1, bool OWN = false>
 static void launch_gemm_pipe_t(const GemmArgs& a, int splits, hipStream_t st) {
   const int row_tiles = a.out_dim / 16;
   const int nblk = ((a.tokens + 16 * NT * TW - 1) / (16 * NT * TW)) * ((row_tiles + 4 * RTW - 1) / (4 * RTW));
   const dim3 grid(8 * ((nblk + 7) / 8), 1, splits);
-  hipLaunchKernelGGL((gemm_i8_pipe_kernel<NT, RTW, NBUF, EPI, DUAL, TW, WPE>), grid, dim3(256 * TW), 0, st, a);
+  hipLaunchKernelGGL((gemm_i8_pipe_kernel<NT, RTW, NBUF, EPI, DUAL, TW, WPE, OWN>), grid, dim3(256 * TW), 0, st, a);
   if (!DUAL && (splits > 1 || a.fuse != kFuseNone)) launch_reduce<EPI>(a, splits, st);
 }
 
@@ -2442,9 +2467,9 @@ static void launch_gemm_epi(const GemmArgs& a, hipStream_t st) {
   // tokens: gate/up 0.94-0.98 -> 0.79 ms, down 0.38-0.40 -> 0.34 ms, QKV 111-118 -> 97-100 us.
   if (a.tokens > kSplitTokens && a.fuse == kFuseNone) {
     if constexpr (DUAL)
-      launch_gemm_pipe_t<4, 2, 2, EPI, DUAL, 1, 2>(a, 1, st);
+      launch_gemm_pipe_t<4, 2, 2, EPI, DUAL, 1, 2, true>(a, 1, st);
     else
-      launch_gemm_pipe_t<4, 4, 2, EPI, DUAL, 1, 2>(a, 1, st);
+      launch_gemm_pipe_t<4, 4, 2, EPI, DUAL, 1, 2, true>(a, 1, st);
     return;
   }
   if constexpr (DUAL) {
