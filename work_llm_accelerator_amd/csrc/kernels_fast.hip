@@ -632,11 +632,11 @@ __global__ void __launch_bounds__(256 * TW) __attribute__((amdgpu_waves_per_eu(W
   const int first_t = group * G;
   const int gsize = min(tiles_t - first_t, G);
   const int within = lin - group * G * tiles_r;
-  const int rt0 = ((within / gsize) * 4 + wave) * RTW;
+  const int rt0 = ((within / gsize) * 4 + wave) * RTW;  // the wave's first row tile
+  const int tok0 = (first_t + within % gsize) * TOK;   // the block's first token
   const int nkc_all = a.in_dim / kKChunk;
   const int nch = nkc_all / gridDim.z;
   const int kc0 = blockIdx.z * nch;
-  const int tok0 = (first_t + within % gsize) * TOK;
   const size_t row_stride_x = (size_t)a.in_dim * 2u;
 
   // per-lane global sources (chunk offsets are added per issue)
@@ -649,18 +649,17 @@ __global__ void __launch_bounds__(256 * TW) __attribute__((amdgpu_waves_per_eu(W
     xsrc[j] = reinterpret_cast<const uint8_t*>(a.xq) + (size_t)tok * row_stride_x + seg * 16;
   }
   const uint8_t* wsrc[D][RTW];
-  bool rt_ok[RTW];
 #pragma unroll
   for (int r = 0; r < RTW; ++r) {
-    rt_ok[r] = rt0 + r < row_tiles;
-    const size_t off = (((size_t)(rt_ok[r] ? rt0 + r : 0) * nkc_all) * 64u + lane) * 16u;
+    const size_t off = (((size_t)(rt0 + r < row_tiles ? rt0 + r : 0) * nkc_all) * 64u + lane) * 16u;
     wsrc[0][r] = a.wp + off;
     if (DUAL) wsrc[D - 1][r] = a.wp2 + off;
   }
-  // chunk kc0 + i into one stage; past the last chunk the last one is loaded again into a stage
-  // nobody reads, which keeps the number of loads per iteration constant (and the waits exact)
-  auto issue = [&](int i, uint8_t* xst, uint8_t* wst) {
-    const int kc = kc0 + min(i, nch - 1);
+  // The next chunk to load.  Past the last chunk the last one is loaded again into a stage nobody
+  // reads, which keeps the number of loads per iteration constant (and the waits exact).
+  int it_c = 0;
+  auto issue = [&](uint8_t* xst, uint8_t* wst) {
+    const int kc = kc0 + it_c;
 #pragma unroll
     for (int j = 0; j < NT; ++j)
       __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(xsrc[j] + (size_t)kc * 256u),
@@ -674,178 +673,189 @@ __global__ void __launch_bounds__(256 * TW) __attribute__((amdgpu_waves_per_eu(W
           __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(wsrc[d][r] + (size_t)kc * 1024u),
                                            (__attribute__((address_space(3))) void*)(wst + ((wave * D + d) * RTW + r) * 1024),
                                            16, 0, 0);
+    if (it_c + 1 < nch) ++it_c;
   };
 
   v4i accH[D][RTW][NT], accL[D][RTW][NT];
+  auto zero_acc = [&]() {
 #pragma unroll
-  for (int d = 0; d < D; ++d)
+    for (int d = 0; d < D; ++d)
 #pragma unroll
-    for (int r = 0; r < RTW; ++r)
+      for (int r = 0; r < RTW; ++r)
 #pragma unroll
-      for (int n = 0; n < NT; ++n) accH[d][r][n] = accL[d][r][n] = v4i{0, 0, 0, 0};
+        for (int n = 0; n < NT; ++n) accH[d][r][n] = accL[d][r][n] = v4i{0, 0, 0, 0};
+  };
 
+  // One chunk: the stage (xst, wst) holds it; (xnx, wnx) is the stage the next issue refills.
+  auto chunk = [&](uint8_t* xst, uint8_t* wst, uint8_t* xnx, uint8_t* wnx) {
+    // exactly NBUF-2 chunks were issued after this one: waiting for all but their loads means it has
+    // landed (this wave's part); the barrier covers the other waves' parts and frees the stage the
+    // next issue refills (read in the previous chunk).
+    wait_vmcnt<(NBUF - 2) * OPS>();
+    if (!OWN) {
+      __builtin_amdgcn_s_barrier();
+      issue(xnx, wnx);
+    }
+    // LDS reads of the stage: the weight tiles and token tile 0 first, then tile n+1 while the
+    // matrix cores work on tile n.  They are issued as ds_read_b128 with explicit lgkmcnt waits:
+    // the compiler cannot tell which stage an in-flight direct load writes, and would otherwise
+    // drain every outstanding load (s_waitcnt vmcnt(0)) before each read, i.e. the whole pipeline.
+    const uint32_t wa = lds_addr(wst) + (uint32_t)(wave * D * RTW * 1024 + lane * 16);
+    const uint32_t xb = lds_addr(xst) + (uint32_t)((tw * 16 * NT + col) * 256);
+    const uint32_t xo[4] = {xb + (uint32_t)(((2 * g) ^ col) << 4), xb + (uint32_t)(((2 * g + 1) ^ col) << 4),
+                            xb + (uint32_t)(((8 + 2 * g) ^ col) << 4), xb + (uint32_t)(((9 + 2 * g) ^ col) << 4)};
+    v4i wr[D][RTW];
 #pragma unroll
-  for (int i = 0; i < NBUF - 1; ++i) issue(i, XS[i], WS[i]);
+    for (int d = 0; d < D; ++d)
+#pragma unroll
+      for (int r = 0; r < RTW; ++r) wr[d][r] = lds_read_b128(wa + (uint32_t)((d * RTW + r) * 1024));
+    // LDS offset of the token tile in accumulator slot n
+    auto slot_off = [&](int n) { return (uint32_t)((((OWN ? wv : 0) + n) & (NT - 1)) * 16 * 256); };
+    v4i bx[2][4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) bx[0][q] = lds_read_b128(xo[q] + slot_off(0));
+    v4i a1[D][RTW], a2[D][RTW];
+    auto mfma_slot = [&](int n, const v4i* cur, int p0, int p1) {  // (d, r) pairs p0 <= p < p1
+#pragma unroll
+      for (int pr = 0; pr < D * RTW; ++pr) {
+        if (pr < p0 || pr >= p1) continue;
+        const int d = pr / RTW, r = pr % RTW;
+        accH[d][r][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[d][r], cur[0], accH[d][r][n], 0, 0, 0);
+        accH[d][r][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2[d][r], cur[1], accH[d][r][n], 0, 0, 0);
+        accL[d][r][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[d][r], cur[2], accL[d][r][n], 0, 0, 0);
+        accL[d][r][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2[d][r], cur[3], accL[d][r][n], 0, 0, 0);
+      }
+    };
+    auto unpack_weights = [&]() {
+#pragma unroll
+      for (int d = 0; d < D; ++d)
+#pragma unroll
+        for (int r = 0; r < RTW; ++r) {
+          reg_tie(wr[d][r]);  // landed before token tile 0 (LDS reads complete in order)
+          unpack16(make_uint4((uint32_t)wr[d][r][0], (uint32_t)wr[d][r][1], (uint32_t)wr[d][r][2],
+                              (uint32_t)wr[d][r][3]),
+                   a1[d][r], a2[d][r]);
+        }
+    };
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+      v4i* cur = bx[n & 1];
+      if (OWN && n == 0) {
+        // own tile and weights: landed by this wave's wait; the other tiles only after the barrier
+        lgkm_wait_tie<0>(cur[0], cur[1], cur[2], cur[3]);
+        unpack_weights();
+        mfma_slot(0, cur, 0, D * RTW / 2);
+        __builtin_amdgcn_s_barrier();
+        issue(xnx, wnx);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) bx[1][q] = lds_read_b128(xo[q] + slot_off(1));
+        mfma_slot(0, cur, D * RTW / 2, D * RTW);
+        continue;
+      }
+      if (n + 1 < NT) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) bx[(n + 1) & 1][q] = lds_read_b128(xo[q] + slot_off(n + 1));
+        lgkm_wait_tie<4>(cur[0], cur[1], cur[2], cur[3]);
+      } else {
+        lgkm_wait_tie<0>(cur[0], cur[1], cur[2], cur[3]);
+      }
+      if (n == 0) unpack_weights();
+      mfma_slot(n, cur, 0, D * RTW);
+    }
+  };
+
+  const bool partial = gridDim.z > 1 || (!DUAL && a.fuse != kFuseNone);  // a reduce kernel finishes
+  // Epilogue.  Every operand load is issued before the first use, so the wave waits for memory once
+  // rather than once per (row tile, token tile); token columns past the last token read the last
+  // token's values and store nothing.
+  auto epilogue = [&]() {
+    int tok[NT];
+    float sxv[NT];
+    int sh8[NT], sl8[NT];
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+      tok[n] = tok0 + tw * 16 * NT + (((OWN ? wv : 0) + n) & (NT - 1)) * 16 + col;
+      const int tc = min(tok[n], a.tokens - 1);
+      sxv[n] = a.sx[tc];
+      const int2 sm = *reinterpret_cast<const int2*>(a.sums + 2 * tc);
+      sh8[n] = 8 * sm.x;
+      sl8[n] = 8 * sm.y;
+    }
+    float sw[RTW][4], sw2[RTW][4], bias[RTW][4];
+#pragma unroll
+    for (int r = 0; r < RTW; ++r) {
+      const int row0 = min(rt0 + r, row_tiles - 1) * 16 + 4 * g;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        sw[r][q] = a.sw[row0 + q];
+        sw2[r][q] = DUAL ? a.sw2[row0 + q] : 0.0f;
+        bias[r][q] = (EPI == kEpiStore && a.bias) ? a.bias[row0 + q] : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < RTW; ++r) {
+      if (rt0 + r >= row_tiles) continue;
+      const int row0 = (rt0 + r) * 16 + 4 * g;
+      float4 res[NT];
+      if (EPI == kEpiResidual && !partial) {
+#pragma unroll
+        for (int n = 0; n < NT; ++n)
+          res[n] = *reinterpret_cast<const float4*>(a.resid + (size_t)min(tok[n], a.tokens - 1) * a.resid_stride + row0);
+      }
+#pragma unroll
+      for (int n = 0; n < NT; ++n) {
+        float out[4];
+        if (partial) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            out[q] = ((float)accH[0][r][n][q] * 256.0f + (float)accL[0][r][n][q]) * sxv[n] * sw[r][q];
+          if (tok[n] < a.tokens)
+            *reinterpret_cast<float4*>(a.part + ((size_t)blockIdx.z * a.tokens + tok[n]) * a.out_dim + row0) =
+                make_float4(out[0], out[1], out[2], out[3]);
+          continue;
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          // fp32 dequantization: the int32 sums are exact; fp32 adds ~2^-24 relative, far inside the
+          // FAST tolerance, at a quarter of the cost of the fp64 form
+          const float tot = (float)(accH[0][r][n][q] - sh8[n]) * 256.0f + (float)(accL[0][r][n][q] - sl8[n]);
+          const float v = tot * sxv[n] * sw[r][q];
+          if (EPI == kEpiSiluMul) {
+            const float tot2 =
+                (float)(accH[D - 1][r][n][q] - sh8[n]) * 256.0f + (float)(accL[D - 1][r][n][q] - sl8[n]);
+            const float u = tot2 * sxv[n] * sw2[r][q];
+            const float sg = a.prefill_silu ? silu_prefill_fast(v) : silu_decode(v);
+            out[q] = sg * u;
+          } else if (EPI == kEpiResidual) {
+            out[q] = (&res[n].x)[q] + v;
+          } else {
+            out[q] = v + bias[r][q];
+          }
+        }
+        if (tok[n] >= a.tokens) continue;
+        if (EPI == kEpiResidual && a.y_raw)
+          *reinterpret_cast<float4*>(a.y_raw + (size_t)tok[n] * a.y_stride + row0) =
+              make_float4(out[0], out[1], out[2], out[3]);
+        if (EPI == kEpiResidual && a.round_bf16)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) out[q] = round_bf16(out[q]);
+        *reinterpret_cast<float4*>(a.y + (size_t)tok[n] * a.y_stride + row0) =
+            make_float4(out[0], out[1], out[2], out[3]);
+      }
+    }
+  };
+
+  zero_acc();
+#pragma unroll
+  for (int i = 0; i < NBUF - 1; ++i) issue(XS[i], WS[i]);
   for (int i0 = 0; i0 < nch; i0 += NBUF) {
 #pragma unroll
     for (int sidx = 0; sidx < NBUF; ++sidx) {
-      const int i = i0 + sidx;
-      if (i < nch) {
-        // exactly NBUF-2 chunks were issued after chunk i: waiting for all but their loads means
-        // chunk i has landed (this wave's part); the barrier covers the other waves' parts and
-        // frees stage sidx-1, which the next issue refills.
-        wait_vmcnt<(NBUF - 2) * OPS>();
-        if (!OWN) {
-          __builtin_amdgcn_s_barrier();
-          issue(i + NBUF - 1, XS[(sidx + NBUF - 1) % NBUF], WS[(sidx + NBUF - 1) % NBUF]);
-        }
-        // LDS reads of the stage: the weight tiles and token tile 0 first, then tile n+1 while the
-        // matrix cores work on tile n.  They are issued as ds_read_b128 with explicit lgkmcnt waits:
-        // the compiler cannot tell which stage an in-flight direct load writes, and would otherwise
-        // drain every outstanding load (s_waitcnt vmcnt(0)) before each read, i.e. the whole pipeline.
-        const uint32_t wa = lds_addr(WS[sidx]) + (uint32_t)(wave * D * RTW * 1024 + lane * 16);
-        const uint32_t xb = lds_addr(XS[sidx]) + (uint32_t)((tw * 16 * NT + col) * 256);
-        const uint32_t xo[4] = {xb + (uint32_t)(((2 * g) ^ col) << 4), xb + (uint32_t)(((2 * g + 1) ^ col) << 4),
-                                xb + (uint32_t)(((8 + 2 * g) ^ col) << 4), xb + (uint32_t)(((9 + 2 * g) ^ col) << 4)};
-        v4i wr[D][RTW];
-#pragma unroll
-        for (int d = 0; d < D; ++d)
-#pragma unroll
-          for (int r = 0; r < RTW; ++r) wr[d][r] = lds_read_b128(wa + (uint32_t)((d * RTW + r) * 1024));
-        // LDS offset of the token tile in accumulator slot n
-        auto slot_off = [&](int n) { return (uint32_t)((((OWN ? wv : 0) + n) & (NT - 1)) * 16 * 256); };
-        v4i bx[2][4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) bx[0][q] = lds_read_b128(xo[q] + slot_off(0));
-        v4i a1[D][RTW], a2[D][RTW];
-        auto mfma_slot = [&](int n, const v4i* cur, int p0, int p1) {  // (d, r) pairs p0 <= p < p1
-#pragma unroll
-          for (int pr = 0; pr < D * RTW; ++pr) {
-            if (pr < p0 || pr >= p1) continue;
-            const int d = pr / RTW, r = pr % RTW;
-            accH[d][r][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[d][r], cur[0], accH[d][r][n], 0, 0, 0);
-            accH[d][r][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2[d][r], cur[1], accH[d][r][n], 0, 0, 0);
-            accL[d][r][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[d][r], cur[2], accL[d][r][n], 0, 0, 0);
-            accL[d][r][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2[d][r], cur[3], accL[d][r][n], 0, 0, 0);
-          }
-        };
-        auto unpack_weights = [&]() {
-#pragma unroll
-          for (int d = 0; d < D; ++d)
-#pragma unroll
-            for (int r = 0; r < RTW; ++r) {
-              reg_tie(wr[d][r]);  // landed before token tile 0 (LDS reads complete in order)
-              unpack16(make_uint4((uint32_t)wr[d][r][0], (uint32_t)wr[d][r][1], (uint32_t)wr[d][r][2],
-                                  (uint32_t)wr[d][r][3]),
-                       a1[d][r], a2[d][r]);
-            }
-        };
-#pragma unroll
-        for (int n = 0; n < NT; ++n) {
-          v4i* cur = bx[n & 1];
-          if (OWN && n == 0) {
-            // own tile and weights: landed by this wave's wait; the other tiles only after the barrier
-            lgkm_wait_tie<0>(cur[0], cur[1], cur[2], cur[3]);
-            unpack_weights();
-            mfma_slot(0, cur, 0, D * RTW / 2);
-            __builtin_amdgcn_s_barrier();
-            issue(i + NBUF - 1, XS[(sidx + NBUF - 1) % NBUF], WS[(sidx + NBUF - 1) % NBUF]);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) bx[1][q] = lds_read_b128(xo[q] + slot_off(1));
-            mfma_slot(0, cur, D * RTW / 2, D * RTW);
-            continue;
-          }
-          if (n + 1 < NT) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) bx[(n + 1) & 1][q] = lds_read_b128(xo[q] + slot_off(n + 1));
-            lgkm_wait_tie<4>(cur[0], cur[1], cur[2], cur[3]);
-          } else {
-            lgkm_wait_tie<0>(cur[0], cur[1], cur[2], cur[3]);
-          }
-          if (n == 0) unpack_weights();
-          mfma_slot(n, cur, 0, D * RTW);
-        }
-      }
+      if (i0 + sidx < nch) chunk(XS[sidx], WS[sidx], XS[(sidx + NBUF - 1) % NBUF], WS[(sidx + NBUF - 1) % NBUF]);
     }
   }
   wait_vmcnt<0>();  // the trailing reloads land before the wave moves on
-
-  const bool partial = gridDim.z > 1 || (!DUAL && a.fuse != kFuseNone);  // a reduce kernel finishes
-  // Epilogue operands.  Every load is issued before the first use, so the wave waits for memory
-  // once rather than once per (row tile, token tile); token columns past the last token read the
-  // last token's values and store nothing.
-  int tok[NT];
-  float sxv[NT];
-  int sh8[NT], sl8[NT];
-#pragma unroll
-  for (int n = 0; n < NT; ++n) {
-    tok[n] = tok0 + tw * 16 * NT + (((OWN ? wv : 0) + n) & (NT - 1)) * 16 + col;
-    const int tc = min(tok[n], a.tokens - 1);
-    sxv[n] = a.sx[tc];
-    const int2 sm = *reinterpret_cast<const int2*>(a.sums + 2 * tc);
-    sh8[n] = 8 * sm.x;
-    sl8[n] = 8 * sm.y;
-  }
-  float sw[RTW][4], sw2[RTW][4], bias[RTW][4];
-#pragma unroll
-  for (int r = 0; r < RTW; ++r) {
-    const int row0 = min(rt0 + r, row_tiles - 1) * 16 + 4 * g;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      sw[r][q] = a.sw[row0 + q];
-      sw2[r][q] = DUAL ? a.sw2[row0 + q] : 0.0f;
-      bias[r][q] = (EPI == kEpiStore && a.bias) ? a.bias[row0 + q] : 0.0f;
-    }
-  }
-#pragma unroll
-  for (int r = 0; r < RTW; ++r) {
-    if (!rt_ok[r]) continue;
-    const int row0 = (rt0 + r) * 16 + 4 * g;
-    float4 res[NT];
-    if (EPI == kEpiResidual && !partial) {
-#pragma unroll
-      for (int n = 0; n < NT; ++n)
-        res[n] = *reinterpret_cast<const float4*>(a.resid + (size_t)min(tok[n], a.tokens - 1) * a.resid_stride + row0);
-    }
-#pragma unroll
-    for (int n = 0; n < NT; ++n) {
-      float out[4];
-      if (partial) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          out[q] = ((float)accH[0][r][n][q] * 256.0f + (float)accL[0][r][n][q]) * sxv[n] * sw[r][q];
-        if (tok[n] < a.tokens)
-          *reinterpret_cast<float4*>(a.part + ((size_t)blockIdx.z * a.tokens + tok[n]) * a.out_dim + row0) =
-              make_float4(out[0], out[1], out[2], out[3]);
-        continue;
-      }
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        // fp32 dequantization: the int32 sums are exact; fp32 adds ~2^-24 relative, far inside the
-        // FAST tolerance, at a quarter of the cost of the fp64 form
-        const float tot = (float)(accH[0][r][n][q] - sh8[n]) * 256.0f + (float)(accL[0][r][n][q] - sl8[n]);
-        const float v = tot * sxv[n] * sw[r][q];
-        if (EPI == kEpiSiluMul) {
-          const float tot2 = (float)(accH[D - 1][r][n][q] - sh8[n]) * 256.0f + (float)(accL[D - 1][r][n][q] - sl8[n]);
-          const float u = tot2 * sxv[n] * sw2[r][q];
-          const float sg = a.prefill_silu ? silu_prefill_fast(v) : silu_decode(v);
-          out[q] = sg * u;
-        } else if (EPI == kEpiResidual) {
-          out[q] = (&res[n].x)[q] + v;
-        } else {
-          out[q] = v + bias[r][q];
-        }
-      }
-      if (tok[n] >= a.tokens) continue;
-      if (EPI == kEpiResidual && a.y_raw)
-        *reinterpret_cast<float4*>(a.y_raw + (size_t)tok[n] * a.y_stride + row0) =
-            make_float4(out[0], out[1], out[2], out[3]);
-      if (EPI == kEpiResidual && a.round_bf16)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) out[q] = round_bf16(out[q]);
-      *reinterpret_cast<float4*>(a.y + (size_t)tok[n] * a.y_stride + row0) = make_float4(out[0], out[1], out[2], out[3]);
-    }
-  }
+  epilogue();
 }
 
 // ---------------------------------------------------------------------------------------------
