@@ -33,7 +33,10 @@ constexpr int kEpiStore = 0, kEpiSiluMul = 1, kEpiResidual = 2;
 //   kFuseQkvRope:   [q|k|v] rows + bias, decode RoPE of q and k, K/V cache append (kEpiStore);
 //   kFuseNormQuant: the finished row (kEpiStore, or kEpiResidual after bf16 rounding) is RMS-normalized
 //                   with norm_w and quantized into xq_out / sx_out / sums_out for the next projection.
-constexpr int kFuseNone = 0, kFuseQkvRope = 1, kFuseNormQuant = 2;
+// Fused into the epilogue of the pipelined GEMM (more than kSplitTokens tokens):
+//   kFuseRopePrefill: [q|k|v] rows + bias, prefill RoPE of q (in place in y) and k, K/V cache append;
+//                     token t is sequence t / seq_len at position past + t % seq_len.
+constexpr int kFuseNone = 0, kFuseQkvRope = 1, kFuseNormQuant = 2, kFuseRopePrefill = 3;
 
 // Bytes of the two-limb code of `rows` activation rows of width n.
 inline size_t xq_bytes(size_t rows, size_t n) { return rows * n * 2u; }
@@ -83,6 +86,7 @@ struct GemmArgs {
   int* sums_out;
   int defer_reduce;     // kFuseNormQuant, one token: write the partials only; the next projection's
                         // blocks finish the row (launch_gemm_i8_pre)
+  int seq_len, past;    // kFuseRopePrefill (with rope, k_cache, v_cache, seq_stride, limit)
 };
 
 // K splits across blocks: at most kMaxSplits splits, only for GEMMs of at most kSplitTokens tokens;

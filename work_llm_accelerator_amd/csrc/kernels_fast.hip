@@ -17,6 +17,8 @@
 // and the 15-bit activation quantization.
 #include <hip/hip_runtime.h>
 
+#include <stdexcept>
+
 #include "kernels.hpp"
 #include "qwen_device_math.hpp"
 
@@ -588,9 +590,14 @@ constexpr int kRasterGroup = 8;  // token tiles per raster group of the pipeline
 // its accumulator slot 0, and the wave runs half of that slot's MFMAs before the chunk's barrier (its
 // own loads have landed by its own wait), so waves that reach the barrier late are absorbed by matrix
 // work instead of stalling the others.  Slot n holds token tile (wv + n) mod 4.
-template <int NT, int RTW, int NBUF, int EPI, bool DUAL, int TW, int WPE = 1, bool OWN = false>
+// ROPE (the fused [q | k | v] projection of a prefill, kFuseRopePrefill): wave w of a block (2 heads,
+// 16 row tiles) holds row tiles h*8 + 2*(w & 1) + {0, 1} and the same + 4 of head h = w >> 1, so that
+// tiles r and r + 2 hold the rotation pairs (p, p + 64) of one head and the epilogue rotates q and k and
+// appends K/V to the cache, as rope_qkv_kernel does after a plain store.
+template <int NT, int RTW, int NBUF, int EPI, bool DUAL, int TW, int WPE = 1, bool OWN = false, bool ROPE = false>
 __global__ void __launch_bounds__(256 * TW) __attribute__((amdgpu_waves_per_eu(WPE))) gemm_i8_pipe_kernel(GemmArgs a) {
   static_assert(!OWN || (TW == 1 && NT == 4), "own tile first: each of the 4 waves loads one token tile");
+  static_assert(!ROPE || (RTW == 4 && TW == 1 && !DUAL && EPI == kEpiStore), "prefill RoPE: 2 heads per block");
   constexpr int D = DUAL ? 2 : 1;
   constexpr int TOK = 16 * NT * TW;        // tokens per block (TW token groups of 16*NT)
   constexpr int XB = TOK * 256;                 // activation bytes per stage
@@ -633,6 +640,10 @@ __global__ void __launch_bounds__(256 * TW) __attribute__((amdgpu_waves_per_eu(W
   const int gsize = min(tiles_t - first_t, G);
   const int within = lin - group * G * tiles_r;
   const int rt0 = ((within / gsize) * 4 + wave) * RTW;  // the wave's first row tile
+  // row tile of the wave's tile r
+  auto row_tile = [&](int r) {
+    return ROPE ? (within / gsize) * 16 + (wave >> 1) * 8 + (wave & 1) * 2 + (r & 1) + (r >> 1) * 4 : rt0 + r;
+  };
   const int tok0 = (first_t + within % gsize) * TOK;   // the block's first token
   const int nkc_all = a.in_dim / kKChunk;
   const int nch = nkc_all / gridDim.z;
@@ -651,7 +662,7 @@ __global__ void __launch_bounds__(256 * TW) __attribute__((amdgpu_waves_per_eu(W
   const uint8_t* wsrc[D][RTW];
 #pragma unroll
   for (int r = 0; r < RTW; ++r) {
-    const size_t off = (((size_t)(rt0 + r < row_tiles ? rt0 + r : 0) * nkc_all) * 64u + lane) * 16u;
+    const size_t off = (((size_t)(row_tile(r) < row_tiles ? row_tile(r) : 0) * nkc_all) * 64u + lane) * 16u;
     wsrc[0][r] = a.wp + off;
     if (DUAL) wsrc[D - 1][r] = a.wp2 + off;
   }
@@ -784,13 +795,66 @@ __global__ void __launch_bounds__(256 * TW) __attribute__((amdgpu_waves_per_eu(W
     float sw[RTW][4], sw2[RTW][4], bias[RTW][4];
 #pragma unroll
     for (int r = 0; r < RTW; ++r) {
-      const int row0 = min(rt0 + r, row_tiles - 1) * 16 + 4 * g;
+      const int row0 = min(row_tile(r), row_tiles - 1) * 16 + 4 * g;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         sw[r][q] = a.sw[row0 + q];
         sw2[r][q] = DUAL ? a.sw2[row0 + q] : 0.0f;
         bias[r][q] = (EPI == kEpiStore && a.bias) ? a.bias[row0 + q] : 0.0f;
       }
+    }
+    if constexpr (ROPE) {
+      // tiles r and r + 2 (r < 2): dims p .. p + 3 and p + 64 .. p + 67 of head rt / 8; cos/sin of the
+      // lane's tokens are loaded per pair, so that one pair's 32 registers are live at a time
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int rt = row_tile(r);
+        const int head = rt >> 3;
+        const int p = (rt & 7) * 16 + 4 * g;
+        int Pn[NT], seqn[NT];
+        float4 cs[NT], sn[NT];
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+          const int tc = min(tok[n], a.tokens - 1);
+          seqn[n] = tc / a.seq_len;
+          Pn[n] = a.past + tc % a.seq_len;
+          const int Pc = min(max(Pn[n], 0), a.limit - 1);
+          cs[n] = *reinterpret_cast<const float4*>(a.rope + (size_t)Pc * 128 + p);
+          sn[n] = *reinterpret_cast<const float4*>(a.rope + (size_t)Pc * 128 + 64 + p);
+        }
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+          if (tok[n] >= a.tokens || Pn[n] < 0 || Pn[n] >= a.limit) continue;
+          float e[4], od[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            e[q] = (float)(accH[0][r][n][q] - sh8[n]) * 256.0f + (float)(accL[0][r][n][q] - sl8[n]);
+            e[q] = e[q] * sxv[n] * sw[r][q] + bias[r][q];
+            od[q] = (float)(accH[0][r + 2][n][q] - sh8[n]) * 256.0f + (float)(accL[0][r + 2][n][q] - sl8[n]);
+            od[q] = od[q] * sxv[n] * sw[r + 2][q] + bias[r + 2][q];
+          }
+          const float c4[4] = {cs[n].x, cs[n].y, cs[n].z, cs[n].w}, s4[4] = {sn[n].x, sn[n].y, sn[n].z, sn[n].w};
+          float lo[4], hi[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const bool v_head = head >= QWEN_Q_HEADS + QWEN_KV_HEADS;
+            lo[q] = v_head ? e[q] : e[q] * c4[q] - od[q] * s4[q];
+            hi[q] = v_head ? od[q] : od[q] * c4[q] + e[q] * s4[q];
+          }
+          float* dst;
+          if (head < QWEN_Q_HEADS) {
+            dst = a.y + (size_t)tok[n] * a.y_stride + head * QWEN_HEAD_DIM + p;
+          } else {
+            const size_t crow = (size_t)seqn[n] * a.seq_stride + (size_t)Pn[n] * QWEN_KV_WIDTH;
+            dst = head < QWEN_Q_HEADS + QWEN_KV_HEADS
+                      ? a.k_cache + crow + (head - QWEN_Q_HEADS) * QWEN_HEAD_DIM + p
+                      : a.v_cache + crow + (head - QWEN_Q_HEADS - QWEN_KV_HEADS) * QWEN_HEAD_DIM + p;
+          }
+          *reinterpret_cast<float4*>(dst) = make_float4(lo[0], lo[1], lo[2], lo[3]);
+          *reinterpret_cast<float4*>(dst + 64) = make_float4(hi[0], hi[1], hi[2], hi[3]);
+        }
+      }
+      return;
     }
 #pragma unroll
     for (int r = 0; r < RTW; ++r) {
@@ -2398,13 +2462,16 @@ static void launch_reduce(const GemmArgs& a, int splits, hipStream_t st) {
   }
 }
 
-template <int NT, int RTW, int NBUF, int EPI, bool DUAL, int TW = 1, int WPE = 1, bool OWN = false>
+template <int NT, int RTW, int NBUF, int EPI, bool DUAL, int TW = 1, int WPE = 1, bool OWN = false, bool ROPE = false>
 static void launch_gemm_pipe_t(const GemmArgs& a, int splits, hipStream_t st) {
   const int row_tiles = a.out_dim / 16;
   const int nblk = ((a.tokens + 16 * NT * TW - 1) / (16 * NT * TW)) * ((row_tiles + 4 * RTW - 1) / (4 * RTW));
   const dim3 grid(8 * ((nblk + 7) / 8), 1, splits);
-  hipLaunchKernelGGL((gemm_i8_pipe_kernel<NT, RTW, NBUF, EPI, DUAL, TW, WPE, OWN>), grid, dim3(256 * TW), 0, st, a);
-  if (!DUAL && (splits > 1 || a.fuse != kFuseNone)) launch_reduce<EPI>(a, splits, st);
+  hipLaunchKernelGGL((gemm_i8_pipe_kernel<NT, RTW, NBUF, EPI, DUAL, TW, WPE, OWN, ROPE>), grid, dim3(256 * TW), 0, st,
+                     a);
+  // K splits, or an epilogue fused into the reduce step, finish in the reduce kernel; the prefill RoPE
+  // epilogue is complete in the GEMM itself
+  if (!DUAL && !ROPE && (splits > 1 || a.fuse != kFuseNone)) launch_reduce<EPI>(a, splits, st);
 }
 
 // Skinny GEMMs for at most kSkinnyTokens tokens with in_dim 1536 (12 K chunks in one block) or 8960
@@ -2481,6 +2548,15 @@ static void launch_gemm_epi(const GemmArgs& a, hipStream_t st) {
     else
       launch_gemm_pipe_t<4, 4, 2, EPI, DUAL, 1, 2, true>(a, 1, st);
     return;
+  }
+  if constexpr (!DUAL && EPI == kEpiStore) {
+    if (a.fuse == kFuseRopePrefill) {
+      if (a.tokens <= kSplitTokens || a.out_dim != QWEN_QKV_ROWS || a.seq_len <= 0 || a.past < 0 || !a.rope ||
+          !a.k_cache || !a.v_cache)
+        throw std::runtime_error("prefill RoPE epilogue: more than 256 tokens of the [q | k | v] projection");
+      launch_gemm_pipe_t<4, 4, 2, EPI, DUAL, 1, 2, true, true>(a, 1, st);
+      return;
+    }
   }
   if constexpr (DUAL) {
     if (a.tokens <= 64)

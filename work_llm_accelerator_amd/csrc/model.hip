@@ -369,8 +369,23 @@ struct qwen_hip_model {
       float* vc = vc0 + (size_t)l * ls;
       launch_norm_quant(hidden, QWEN_HIDDEN, T, QWEN_HIDDEN, f.ln, kNormPrefill, w.xq, w.sx, w.sums, nullptr,
                         stream);
-      gemm(w, T, QWEN_HIDDEN, (int)kQkvRows, f.qkv, f.sw_qkv, f.b_qkv, w.qkv, kQkvRows, kEpiStore);
-      launch_rope_qkv(w.qkv, (int)kQkvRows, nullptr, S, past, past + S, T, rope_prefill, kc, vc, ss, stream);
+      if (T > kSplitTokens) {
+        // RoPE of q and k and the K/V cache append in the Q/K/V projection's epilogue
+        GemmArgs fr{};
+        fr.fuse = kFuseRopePrefill;
+        fr.rope = rope_prefill;
+        fr.k_cache = kc;
+        fr.v_cache = vc;
+        fr.seq_stride = ss;
+        fr.seq_len = S;
+        fr.past = past;
+        fr.limit = past + S;
+        gemm(w, T, QWEN_HIDDEN, (int)kQkvRows, f.qkv, f.sw_qkv, f.b_qkv, w.qkv, kQkvRows, kEpiStore, nullptr, nullptr,
+             nullptr, 0, 0, &fr);
+      } else {
+        gemm(w, T, QWEN_HIDDEN, (int)kQkvRows, f.qkv, f.sw_qkv, f.b_qkv, w.qkv, kQkvRows, kEpiStore);
+        launch_rope_qkv(w.qkv, (int)kQkvRows, nullptr, S, past, past + S, T, rope_prefill, kc, vc, ss, stream);
+      }
       launch_attn_prefill(w.qkv, (int)kQkvRows, kc, vc, ss, S, past, B, w.kvt, w.ctx, stream);
       launch_norm_quant(w.ctx, QWEN_HIDDEN, T, QWEN_HIDDEN, nullptr, kNormNone, w.xq, w.sx, w.sums, nullptr, stream);
       gemm(w, T, QWEN_HIDDEN, QWEN_HIDDEN, f.o, f.sw_o, nullptr, w.att, QWEN_HIDDEN, kEpiStore);
