@@ -331,6 +331,75 @@ __global__ void __launch_bounds__(256) norm_quant_kernel(const float* __restrict
                      xn ? xn + (size_t)t * n : nullptr);
 }
 
+// Many-row two-limb quantization (prefill rows of 1,536 or 8,960): one wave per row with NV float4 per
+// lane (n = 256*NV), the whole row loaded at once with non-temporal loads (each value is read once),
+// wave reductions only (no LDS, no barrier), and each store instruction writing two whole 128-byte
+// limb segments.  The values equal norm_quant_row's for kNormNone (the maximum and the integer limb
+// sums do not depend on the order of the reduction); for kNormPrefill the sum of squares is added in
+// another order, a different fp32 rounding of the same sum.  grid = ceil(rows / 4), block = 256.
+template <int NV>
+__global__ void __launch_bounds__(256) quant_rows_wave_kernel(const float* __restrict__ x, size_t x_stride,
+                                                              int rows, const float* __restrict__ w, int norm,
+                                                              int8_t* __restrict__ xq, float* __restrict__ sx,
+                                                              int* __restrict__ sums) {
+  constexpr int n = 256 * NV;
+  const int lane = threadIdx.x & 63;
+  const int t = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+  if (t >= rows) return;  // wave-uniform
+  const float4* xr = reinterpret_cast<const float4*>(x + (size_t)t * x_stride);
+  float4 v[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) v[j] = ld_stream(xr + lane + 64 * j);
+  if (norm == kNormPrefill) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
+    ss = wave_sum(ss);
+    const float inv = 1.0f / approx_sqrt(ss / (float)n + QWEN_RMS_EPS);
+    const float4* w4 = reinterpret_cast<const float4*>(w);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const float4 ww = w4[lane + 64 * j];
+      v[j] = make_float4(v[j].x * inv * ww.x, v[j].y * inv * ww.y, v[j].z * inv * ww.z, v[j].w * inv * ww.w);
+    }
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j)
+    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
+  amax = wave_max(amax);
+  const float inv = amax > 0.0f ? (float)kQuantMax / amax : 0.0f;
+  int8_t* row = xq + (size_t)t * (size_t)(2 * n);
+  int sh = 0, sl = 0;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int k = lane + 64 * j;  // float4 index: elements 4k .. 4k+3 of K chunk k / 32
+    const float e[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+    uint32_t hw = 0, lw = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float xf = fminf(fmaxf(rintf(e[q] * inv), -(float)kQuantMax), (float)kQuantMax);
+      const int X = (int)xf;
+      const int H = (X + 128) >> 8;
+      const int L = X - (H << 8);
+      hw |= (uint32_t)(H & 0xFF) << (8 * q);
+      lw |= (uint32_t)(L & 0xFF) << (8 * q);
+      sh += H;
+      sl += L;
+    }
+    const int base = (k >> 5) * 256 + (k & 31) * 4;
+    *reinterpret_cast<uint32_t*>(row + base) = hw;
+    *reinterpret_cast<uint32_t*>(row + base + 128) = lw;
+  }
+  sh = wave_sum_i(sh);
+  sl = wave_sum_i(sl);
+  if (lane == 0) {
+    sx[t] = amax > 0.0f ? amax / (float)kQuantMax : 1.0f;
+    sums[2 * t] = sh;
+    sums[2 * t + 1] = sl;
+  }
+}
+
 // ---------------------------------------------------------------------------------------------
 // INT4 x two-limb int8 GEMM on the matrix cores:
 //   y[t][o] = sw[o] * sx[t] * ( 256*(sum_k u(o,k) H(t,k) - 8 SH(t)) + (sum_k u(o,k) L(t,k) - 8 SL(t)) )
@@ -2430,6 +2499,17 @@ void launch_repack_int4(const uint8_t* W, int out_dim, int in_dim, uint8_t* WP, 
 
 void launch_norm_quant(const float* x, size_t x_stride, int rows, int n, const float* w, int norm, int8_t* xq,
                        float* sx, int* sums, float* xn, hipStream_t st) {
+  // many rows (prefill): one wave per row
+  if (rows >= 256 && !xn && norm != kNormDecode && (n == QWEN_HIDDEN || n == QWEN_INTERMEDIATE) && x_stride % 4 == 0) {
+    const dim3 grid((unsigned)((rows + 3) / 4));
+    if (n == QWEN_HIDDEN)
+      hipLaunchKernelGGL(quant_rows_wave_kernel<QWEN_HIDDEN / 256>, grid, dim3(256), 0, st, x, x_stride, rows, w, norm,
+                         xq, sx, sums);
+    else
+      hipLaunchKernelGGL(quant_rows_wave_kernel<QWEN_INTERMEDIATE / 256>, grid, dim3(256), 0, st, x, x_stride, rows,
+                         w, norm, xq, sx, sums);
+    return;
+  }
   if (n <= 2048)
     hipLaunchKernelGGL(norm_quant_kernel<2>, dim3(rows), dim3(256), 0, st, x, x_stride, n, w, norm, xq, sx, sums, xn);
   else
