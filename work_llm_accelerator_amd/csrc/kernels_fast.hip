@@ -1044,6 +1044,10 @@ template <int EPI, class Issue = NoIssue>
 __device__ __forceinline__ void reduce_norm_quant_row(const GemmArgs& a, int splits, int tok, int8_t* xq_row,
                                                       int chunk_stride, float* sx_out, int* sums_out, bool write_y,
                                                       Issue&& issue = Issue{});
+template <int EPI, int ZB, class Issue>
+__device__ __forceinline__ void reduce_norm_quant_row_zb(const GemmArgs& a, int splits, int tok, int8_t* xq_row,
+                                                         int chunk_stride, float* sx_out, int* sums_out, bool write_y,
+                                                         Issue&& issue);
 
 // Two-limb quantization of one fp32 row x[0, n) (n % 4 == 0, n <= NV * 1024) by a 256-thread block
 // with norm_quant_row's arithmetic and thread mapping (float4 k = t + 256 j): the code of K chunks
@@ -1388,8 +1392,9 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   if constexpr (PRE) {
     // token 0's row of the slice: K chunk c at xs + c * 16 * 256 (row 0 of the chunk, unswizzled)
     if (threadIdx.x < 64)
-      reduce_norm_quant_row<PRE_EPI>(pre, pre_splits, 0, reinterpret_cast<int8_t*>(xs), 16 * 256, &pre_sx, pre_sums,
-                                     blockIdx.x == 0, issue_loads);
+      // the O projection's one K group (store epilogue) or the down projection's five splits (residual)
+      reduce_norm_quant_row_zb<PRE_EPI, PRE_EPI == kEpiResidual ? 5 : 1>(
+          pre, pre_splits, 0, reinterpret_cast<int8_t*>(xs), 16 * 256, &pre_sx, pre_sums, blockIdx.x == 0, issue_loads);
     else
       issue_loads();
   }
@@ -1755,49 +1760,48 @@ __global__ void __launch_bounds__(256) reduce_norm_quant_kernel(GemmArgs a, int 
 // or a token row of a GEMM's LDS activation slice), the scale and limb sums to sx_out / sums_out;
 // the finished row goes to a.y (and a.y_raw) when write_y.
 // `issue` runs right after the row's loads are issued (a caller's own loads then queue behind them).
-template <int EPI, class Issue>
-__device__ __forceinline__ void reduce_norm_quant_row(const GemmArgs& a, int splits, int tok, int8_t* xq_row,
-                                                      int chunk_stride, float* sx_out, int* sums_out, bool write_y,
-                                                      Issue&& issue) {
+template <int EPI, int ZB, class Issue>
+__device__ __forceinline__ void reduce_norm_quant_row_zb(const GemmArgs& a, int splits, int tok, int8_t* xq_row,
+                                                         int chunk_stride, float* sx_out, int* sums_out, bool write_y,
+                                                         Issue&& issue) {
   constexpr int NV = QWEN_HIDDEN / 256;
   const int lane = threadIdx.x & 63;
-  const size_t zstride = (size_t)a.tokens * QWEN_HIDDEN;
+  const size_t zstride4 = (size_t)a.tokens * (QWEN_HIDDEN / 4);
   const float4* pt = reinterpret_cast<const float4*>(a.part + (size_t)tok * QWEN_HIDDEN) + lane;
   const float4* sw4 = reinterpret_cast<const float4*>(a.sw) + lane;
-  const float4* w4 = reinterpret_cast<const float4*>(a.norm_w) + lane;
-  const float4* r4 = EPI == kEpiResidual ? reinterpret_cast<const float4*>(a.resid + (size_t)tok * a.resid_stride) + lane
-                                         : reinterpret_cast<const float4*>(a.bias) + lane;
   const bool has_add = EPI == kEpiResidual || a.bias != nullptr;
   const bool has_w = a.norm != kNormNone;
-  // Every load in one batch (a single memory round trip for up to kZB splits): the token's limb sums
-  // and scale, the per-row operands, then the split partials.
-  constexpr int kZB = 5;
+  // Every load in one batch and without branches (a single memory round trip for up to ZB splits): an
+  // absent operand (bias, norm weights) is read from the row scales and zeroed after, and the splits of
+  // a batch past the last one read the last split again and are not added.
+  const float4* r4 = EPI == kEpiResidual ? reinterpret_cast<const float4*>(a.resid + (size_t)tok * a.resid_stride) + lane
+                                         : (a.bias ? reinterpret_cast<const float4*>(a.bias) + lane : sw4);
+  const float4* w4 = has_w ? reinterpret_cast<const float4*>(a.norm_w) + lane : sw4;
   const int sum_h = a.sums[2 * tok], sum_l = a.sums[2 * tok + 1];
   const float sx_tok = a.sx[tok];
   float4 acc[NV], sw[NV], ad[NV], wn[NV];
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     sw[j] = sw4[64 * j];
-    ad[j] = has_add ? r4[64 * j] : make_float4(0, 0, 0, 0);
-    wn[j] = has_w ? w4[64 * j] : make_float4(0, 0, 0, 0);
+    ad[j] = r4[64 * j];
+    wn[j] = w4[64 * j];
   }
   // split sums in z order
 #pragma unroll
   for (int j = 0; j < NV; ++j) acc[j] = make_float4(0, 0, 0, 0);
-  for (int z0 = 0; z0 < splits; z0 += kZB) {
-    float4 pz[kZB][NV];
+  for (int z0 = 0; z0 < splits; z0 += ZB) {
+    float4 pz[ZB][NV];
 #pragma unroll
-    for (int u = 0; u < kZB; ++u)
+    for (int u = 0; u < ZB; ++u)
 #pragma unroll
-      for (int j = 0; j < NV; ++j)
-        pz[u][j] = z0 + u < splits ? pt[(size_t)(z0 + u) * (zstride / 4) + 64 * j] : make_float4(0, 0, 0, 0);
+      for (int j = 0; j < NV; ++j) pz[u][j] = pt[(size_t)min(z0 + u, splits - 1) * zstride4 + 64 * j];
     if (z0 == 0) {
       __builtin_amdgcn_sched_barrier(0);
       issue();
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
-    for (int u = 0; u < kZB; ++u)
+    for (int u = 0; u < ZB; ++u)
       if (z0 + u < splits)
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
@@ -1806,6 +1810,12 @@ __device__ __forceinline__ void reduce_norm_quant_row(const GemmArgs& a, int spl
           acc[j].z += pz[u][j].z;
           acc[j].w += pz[u][j].w;
         }
+  }
+  if (splits < 1) issue();  // the caller's loads are issued exactly once, also without splits
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    if (!has_add) ad[j] = make_float4(0, 0, 0, 0);
+    if (!has_w) wn[j] = make_float4(0, 0, 0, 0);
   }
   const double corr = -8.0 * (256.0 * (double)sum_h + (double)sum_l) * (double)sx_tok;
   float4 v[NV];
@@ -1867,6 +1877,17 @@ __device__ __forceinline__ void reduce_norm_quant_row(const GemmArgs& a, int spl
     sums_out[0] = sh;
     sums_out[1] = sl;
   }
+}
+
+// One split (the O projection's single K group) or up to five (the down projection's) in one batch.
+template <int EPI, class Issue>
+__device__ __forceinline__ void reduce_norm_quant_row(const GemmArgs& a, int splits, int tok, int8_t* xq_row,
+                                                      int chunk_stride, float* sx_out, int* sums_out, bool write_y,
+                                                      Issue&& issue) {
+  if (splits == 1)
+    reduce_norm_quant_row_zb<EPI, 1>(a, splits, tok, xq_row, chunk_stride, sx_out, sums_out, write_y, issue);
+  else
+    reduce_norm_quant_row_zb<EPI, 5>(a, splits, tok, xq_row, chunk_stride, sx_out, sums_out, write_y, issue);
 }
 
 // grid = tokens, block = 64 (one wave per row, spread over as many CUs as rows).
