@@ -177,6 +177,19 @@ __device__ __forceinline__ int block_sum4_i(int v, int* s4) {
   __syncthreads();
   return r;
 }
+// Two integer sums in one round (s8: 8 ints of LDS).
+__device__ __forceinline__ void block_sum4_i2(int& a, int& b, int* s8) {
+  a = wave_sum_i(a);
+  b = wave_sum_i(b);
+  if ((threadIdx.x & 63) == 0) {
+    s8[threadIdx.x >> 6] = a;
+    s8[4 + (threadIdx.x >> 6)] = b;
+  }
+  __syncthreads();
+  a = (s8[0] + s8[1]) + (s8[2] + s8[3]);
+  b = (s8[4] + s8[5]) + (s8[6] + s8[7]);
+  __syncthreads();
+}
 
 // ---------------------------------------------------------------------------------------------
 // Two-limb activation quantization of one row held in LDS (n values, n % 128 == 0), done by a
@@ -205,8 +218,7 @@ __device__ void quantize_row_lds(const float* __restrict__ v, int n, int8_t* __r
     sh += H;
     sl += L;
   }
-  sh = block_sum4_i(sh, red_i);
-  sl = block_sum4_i(sl, red_i);
+  block_sum4_i2(sh, sl, red_i);
   if (threadIdx.x == 0) {
     *sx_out = sx;
     sums_out[0] = sh;
@@ -229,7 +241,7 @@ __device__ __forceinline__ void norm_quant_row(float4 (&v)[NV], int n, const flo
                                                int* __restrict__ sums_out, float* __restrict__ xn_row) {
   __shared__ float red_f[4];
   __shared__ double red_d[4];
-  __shared__ int red_i[4];
+  __shared__ int red_i[8];
   const int n4 = n >> 2;
   if (norm == kNormDecode) {
     double ss = 0.0;
@@ -301,8 +313,7 @@ __device__ __forceinline__ void norm_quant_row(float4 (&v)[NV], int n, const flo
       *reinterpret_cast<uint32_t*>(row + base + 128) = lw;
     }
   }
-  sh = block_sum4_i(sh, red_i);
-  sl = block_sum4_i(sl, red_i);
+  block_sum4_i2(sh, sl, red_i);
   if (threadIdx.x == 0) {
     *sx_out = amax > 0.0f ? amax / (float)kQuantMax : 1.0f;
     sums_out[0] = sh;
@@ -1058,17 +1069,19 @@ __device__ __forceinline__ void quant_row_slice(const float* __restrict__ x, int
                                                 int chunk_stride, float* sx_lds, int* sums_lds, float* sx_g,
                                                 int* sums_g, Issue&& issue) {
   __shared__ float red_f[4];
-  __shared__ int red_i[4];
+  __shared__ int red_i[8];
   const int n4 = n >> 2;
   const float4* x4 = reinterpret_cast<const float4*>(x);
   float4 v[NV];
+  // branch-free: past the row's end the loads read its last float4 again, zeroed after
 #pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    const int k = threadIdx.x + 256 * j;
-    v[j] = k < n4 ? x4[k] : make_float4(0, 0, 0, 0);
-  }
+  for (int j = 0; j < NV; ++j) v[j] = x4[min((int)threadIdx.x + 256 * j, n4 - 1)];
   __builtin_amdgcn_sched_barrier(0);
   issue();  // the caller's loads queue behind the row's
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int j = 0; j < NV; ++j)
+    if ((int)threadIdx.x + 256 * j >= n4) v[j] = make_float4(0, 0, 0, 0);
   __builtin_amdgcn_sched_barrier(0);
   float amax = 0.0f;
 #pragma unroll
@@ -1102,8 +1115,7 @@ __device__ __forceinline__ void quant_row_slice(const float* __restrict__ x, int
       }
     }
   }
-  sh = block_sum4_i(sh, red_i);
-  sl = block_sum4_i(sl, red_i);
+  block_sum4_i2(sh, sl, red_i);
   if (threadIdx.x == 0) {
     const float sx = amax > 0.0f ? amax / (float)kQuantMax : 1.0f;
     *sx_lds = sx;
@@ -1128,7 +1140,7 @@ __device__ __forceinline__ void attn_merge_quant_slice(const AttnMergeArgs& am, 
                                                        Issue&& issue) {
   __shared__ float ml[QWEN_Q_HEADS * kAttnMaxSplits * 2];  // (m, l) per head and split, then merge weights
   __shared__ float red_f[4];
-  __shared__ int red_i[4];
+  __shared__ int red_i[8];
   // The loads do not wait for the position: the first kFirst splits' partials and every (m, l) pair
   // are loaded whatever the key count; the merge below reads only the splits that hold keys.  Thread
   // t owns float4 f = t and t + 256 (f < 384) of the context row: head f >> 5, dims 4 (f & 31) .. + 3;
@@ -1136,16 +1148,17 @@ __device__ __forceinline__ void attn_merge_quant_slice(const AttnMergeArgs& am, 
   constexpr int kFirst = 16;  // one-sequence plans use at most 24 splits
   const int nsplit = am.nsplit;
   float4 pv[2][kFirst];
+  // Branch-free within a wave: past the last split the loads read the last split again (used by
+  // nobody), so every load of a batch is issued at once; waves 2 and 3 own one float4 of the row.
   auto load_part = [&](int s0) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      const int f = threadIdx.x + 256 * u;
+      if (u == 1 && threadIdx.x >= QWEN_HIDDEN / 4 - 256) break;  // wave-uniform: waves 2, 3 own one float4
+      const int f = (int)threadIdx.x + 256 * u;
 #pragma unroll
       for (int j = 0; j < kFirst; ++j)
-        pv[u][j] = (f < QWEN_HIDDEN / 4 && s0 + j < nsplit)
-                       ? *reinterpret_cast<const float4*>(am.part + ((size_t)(f >> 5) * nsplit + s0 + j) * QWEN_HEAD_DIM +
-                                                          4 * (f & 31))
-                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        pv[u][j] = *reinterpret_cast<const float4*>(
+            am.part + ((size_t)(f >> 5) * nsplit + min(s0 + j, nsplit - 1)) * QWEN_HEAD_DIM + 4 * (f & 31));
     }
   };
   const int p0 = am.pos[0];
@@ -1154,8 +1167,8 @@ __device__ __forceinline__ void attn_merge_quant_slice(const AttnMergeArgs& am, 
   float2 mlv[kMlPer];
 #pragma unroll
   for (int u = 0; u < kMlPer; ++u) {
-    const int i = threadIdx.x + 256 * u;
-    mlv[u] = i < QWEN_Q_HEADS * nsplit ? am.pml[i] : make_float2(0.0f, 0.0f);  // pml[h][sp] at h * nsplit + sp
+    const int i = min((int)threadIdx.x + 256 * u, QWEN_Q_HEADS * nsplit - 1);
+    mlv[u] = am.pml[i];  // pml[h][sp] at h * nsplit + sp
   }
   __builtin_amdgcn_sched_barrier(0);
   issue();  // the caller's loads queue behind the partials
@@ -1236,8 +1249,7 @@ __device__ __forceinline__ void attn_merge_quant_slice(const AttnMergeArgs& am, 
       *reinterpret_cast<uint32_t*>(dst + 128) = lw;
     }
   }
-  sh = block_sum4_i(sh, red_i);
-  sl = block_sum4_i(sl, red_i);
+  block_sum4_i2(sh, sl, red_i);
   if (threadIdx.x == 0) {
     const float sx = amax > 0.0f ? amax / (float)kQuantMax : 1.0f;
     *sx_lds = sx;
@@ -2052,7 +2064,7 @@ attn_decode_kernel(const float* __restrict__ qkv, int qkv_stride, const float* _
   __shared__ __align__(16) float s_acc[4][QWEN_GROUPS][QWEN_HEAD_DIM];  // reused by the merge step
   __shared__ float s_m[4][QWEN_GROUPS], s_l[4][QWEN_GROUPS];
   __shared__ float red_f[4];
-  __shared__ int red_i[4];
+  __shared__ int red_i[8];
   __shared__ int s_last;
   static_assert(2 * QWEN_Q_HEADS * kAttnMaxSplits <= 4 * QWEN_GROUPS * QWEN_HEAD_DIM && QWEN_HIDDEN <= 16 * kQRow,
                 "merge scratch");
