@@ -111,7 +111,8 @@ __global__ void __launch_bounds__(64) repack_int4_kernel(const uint8_t* __restri
 // Max and integer sum do not depend on the order of the operations, so they reduce each row of 16
 // lanes with DPP moves (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_ror:4, row_ror:8: every lane
 // ends with its row's result) and combine the four rows from v_readlane, instead of six LDS
-// permutes.  Float and double sums keep the xor butterfly (their rounding depends on the order).
+// permutes.  Float sums keep the xor butterfly (the prefill norm's rounding follows that order); the
+// double sum of the decode RMSNorm takes the DPP order (another rounding of an f64 sum of squares).
 template <int CTRL>
 __device__ __forceinline__ int dpp_i(int v) {
   return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
@@ -130,10 +131,24 @@ __device__ __forceinline__ float wave_sum(float v) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
   return v;
 }
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const int lo = dpp_i<CTRL>((int)(uint32_t)u), hi = dpp_i<CTRL>((int)(uint32_t)(u >> 32));
+  return __builtin_bit_cast(double, ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+}
+__device__ __forceinline__ double readlane_d(double v, int l) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)u, l), hi = __builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), l);
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+// wave_sum_i's order (pairs, quads, rows of 16 by DPP, then the four rows) on doubles.
 __device__ __forceinline__ double wave_sum_d(double v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  v += dpp_d<0xB1>(v);
+  v += dpp_d<0x4E>(v);
+  v += dpp_d<0x124>(v);
+  v += dpp_d<0x128>(v);
+  return (readlane_d(v, 0) + readlane_d(v, 16)) + (readlane_d(v, 32) + readlane_d(v, 48));
 }
 __device__ __forceinline__ int wave_sum_i(int v) {
   v += dpp_i<0xB1>(v);
