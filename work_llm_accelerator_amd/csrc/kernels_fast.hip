@@ -1070,7 +1070,7 @@ template <int EPI, class Issue = NoIssue>
 __device__ __forceinline__ void reduce_norm_quant_row(const GemmArgs& a, int splits, int tok, int8_t* xq_row,
                                                       int chunk_stride, float* sx_out, int* sums_out, bool write_y,
                                                       Issue&& issue = Issue{});
-template <int EPI, int ZB, class Issue>
+template <int EPI, int ZB, class Issue, int W = 1>
 __device__ __forceinline__ void reduce_norm_quant_row_zb(const GemmArgs& a, int splits, int tok, int8_t* xq_row,
                                                          int chunk_stride, float* sx_out, int* sums_out, bool write_y,
                                                          Issue&& issue);
@@ -1779,20 +1779,28 @@ __global__ void __launch_bounds__(256) reduce_norm_quant_kernel(GemmArgs a, int 
                     a.sums_out + 2 * tok, nullptr);
 }
 
-// kFuseNormQuant for 1536-wide rows, one wave per token row: the arithmetic of
-// reduce_norm_quant_kernel with wave reductions in place of block reductions, and every load of the
-// row (split partials, scales, residual or bias, norm weights) issued before the first use, so a
-// row costs one memory round trip.  Lane l owns float4 columns l + 64 j, j < 6.  The two-limb code
+// kFuseNormQuant for 1536-wide rows, W waves per token row (one in the GEMM prologues, two in
+// reduce_norm_quant_pair_kernel): the arithmetic of reduce_norm_quant_kernel with wave reductions
+// (and for W = 2 one LDS exchange each) in place of block reductions, and every load of the row (split
+// partials, scales, residual or bias, norm weights) issued before the first use, so a row costs one
+// memory round trip.  Lane l of the row owns float4 columns l + 64 W j, j < 6 / W.  The two-limb code
 // goes to xq_row ([K chunk][limb][128 bytes], K chunk c at byte c * chunk_stride: a row of a.xq_out,
 // or a token row of a GEMM's LDS activation slice), the scale and limb sums to sx_out / sums_out;
 // the finished row goes to a.y (and a.y_raw) when write_y.
 // `issue` runs right after the row's loads are issued (a caller's own loads then queue behind them).
-template <int EPI, int ZB, class Issue>
+template <int EPI, int ZB, class Issue, int W>
 __device__ __forceinline__ void reduce_norm_quant_row_zb(const GemmArgs& a, int splits, int tok, int8_t* xq_row,
                                                          int chunk_stride, float* sx_out, int* sums_out, bool write_y,
                                                          Issue&& issue) {
-  constexpr int NV = QWEN_HIDDEN / 256;
-  const int lane = threadIdx.x & 63;
+  static_assert(W == 1 || W == 2, "one or two waves per row");
+  constexpr int NV = QWEN_HIDDEN / (256 * W);
+  constexpr int LS = 64 * W;                  // float4 stride between a lane's columns
+  const int lane = threadIdx.x & (LS - 1);    // the lane's place among the row's W waves
+  // W = 2: the two waves' partial reductions meet in LDS, one slot per reduction (one barrier each)
+  __shared__ double x_ss[W > 1 ? 2 : 1];
+  __shared__ float x_ssf[W > 1 ? 2 : 1], x_amax[W > 1 ? 2 : 1];
+  __shared__ int x_sums[W > 1 ? 4 : 1];
+  const int wv = (threadIdx.x >> 6) & (W - 1);
   const size_t zstride4 = (size_t)a.tokens * (QWEN_HIDDEN / 4);
   const float4* pt = reinterpret_cast<const float4*>(a.part + (size_t)tok * QWEN_HIDDEN) + lane;
   const float4* sw4 = reinterpret_cast<const float4*>(a.sw) + lane;
@@ -1809,9 +1817,9 @@ __device__ __forceinline__ void reduce_norm_quant_row_zb(const GemmArgs& a, int 
   float4 acc[NV], sw[NV], ad[NV], wn[NV];
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
-    sw[j] = sw4[64 * j];
-    ad[j] = r4[64 * j];
-    wn[j] = w4[64 * j];
+    sw[j] = sw4[LS * j];
+    ad[j] = r4[LS * j];
+    wn[j] = w4[LS * j];
   }
   // split sums in z order
 #pragma unroll
@@ -1821,7 +1829,7 @@ __device__ __forceinline__ void reduce_norm_quant_row_zb(const GemmArgs& a, int 
 #pragma unroll
     for (int u = 0; u < ZB; ++u)
 #pragma unroll
-      for (int j = 0; j < NV; ++j) pz[u][j] = pt[(size_t)min(z0 + u, splits - 1) * zstride4 + 64 * j];
+      for (int j = 0; j < NV; ++j) pz[u][j] = pt[(size_t)min(z0 + u, splits - 1) * zstride4 + LS * j];
     if (z0 == 0) {
       __builtin_amdgcn_sched_barrier(0);
       issue();
@@ -1848,13 +1856,18 @@ __device__ __forceinline__ void reduce_norm_quant_row_zb(const GemmArgs& a, int 
   float4 v[NV];
 #pragma unroll
   for (int j = 0; j < NV; ++j)
-    v[j] = rnq_combine<EPI>(a, tok, 4 * (lane + 64 * j), acc[j], sw[j], ad[j], corr, write_y);
+    v[j] = rnq_combine<EPI>(a, tok, 4 * (lane + LS * j), acc[j], sw[j], ad[j], corr, write_y);
   // RMSNorm (norm_quant_row's arithmetic, wave reductions)
   if (a.norm == kNormDecode) {
     double ss = 0.0;
 #pragma unroll
     for (int j = 0; j < NV; ++j) ss += rnq_sq4(v[j]);
     ss = wave_sum_d(ss);
+    if constexpr (W > 1) {
+      if ((threadIdx.x & 63) == 0) x_ss[wv] = ss;
+      __syncthreads();
+      ss = x_ss[0] + x_ss[1];
+    }
     const double inv = 1.0 / sqrt(ss / (double)QWEN_HIDDEN + (double)QWEN_RMS_EPS);
 #pragma unroll
     for (int j = 0; j < NV; ++j) v[j] = rnq_norm4(v[j], inv, wn[j]);
@@ -1863,6 +1876,11 @@ __device__ __forceinline__ void reduce_norm_quant_row_zb(const GemmArgs& a, int 
 #pragma unroll
     for (int j = 0; j < NV; ++j) ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
     ss = wave_sum(ss);
+    if constexpr (W > 1) {
+      if ((threadIdx.x & 63) == 0) x_ssf[wv] = ss;
+      __syncthreads();
+      ss = x_ssf[0] + x_ssf[1];
+    }
     const float inv = 1.0f / approx_sqrt(ss / (float)QWEN_HIDDEN + QWEN_RMS_EPS);
 #pragma unroll
     for (int j = 0; j < NV; ++j)
@@ -1874,12 +1892,17 @@ __device__ __forceinline__ void reduce_norm_quant_row_zb(const GemmArgs& a, int 
   for (int j = 0; j < NV; ++j)
     amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
   amax = wave_max(amax);
+  if constexpr (W > 1) {
+    if ((threadIdx.x & 63) == 0) x_amax[wv] = amax;
+    __syncthreads();
+    amax = fmaxf(x_amax[0], x_amax[1]);
+  }
   const float qinv = amax > 0.0f ? (float)kQuantMax / amax : 0.0f;
   int8_t* row = xq_row;
   int sh = 0, sl = 0;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
-    const int k = lane + 64 * j;
+    const int k = lane + LS * j;
     const float e[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
     uint32_t hw = 0, lw = 0;
 #pragma unroll
@@ -1899,6 +1922,15 @@ __device__ __forceinline__ void reduce_norm_quant_row_zb(const GemmArgs& a, int 
   }
   sh = wave_sum_i(sh);
   sl = wave_sum_i(sl);
+  if constexpr (W > 1) {
+    if ((threadIdx.x & 63) == 0) {
+      x_sums[2 * wv] = sh;
+      x_sums[2 * wv + 1] = sl;
+    }
+    __syncthreads();
+    sh = x_sums[0] + x_sums[2];
+    sl = x_sums[1] + x_sums[3];
+  }
   if (lane == 0) {
     *sx_out = amax > 0.0f ? amax / (float)kQuantMax : 1.0f;
     sums_out[0] = sh;
@@ -1917,12 +1949,19 @@ __device__ __forceinline__ void reduce_norm_quant_row(const GemmArgs& a, int spl
     reduce_norm_quant_row_zb<EPI, 5>(a, splits, tok, xq_row, chunk_stride, sx_out, sums_out, write_y, issue);
 }
 
-// grid = tokens, block = 64 (one wave per row, spread over as many CUs as rows).
+// grid = tokens, block = 128 (two waves per row: half the per-lane work of the one-wave form, three
+// LDS exchanges); the values equal the one-wave form's except the norm's sum of squares, added in
+// another order.
 template <int EPI>
-__global__ void __launch_bounds__(64) reduce_norm_quant_wave_kernel(GemmArgs a, int splits) {
+__global__ void __launch_bounds__(128) reduce_norm_quant_pair_kernel(GemmArgs a, int splits) {
   const int tok = blockIdx.x;
-  reduce_norm_quant_row<EPI>(a, splits, tok, a.xq_out + (size_t)tok * (2 * QWEN_HIDDEN), 256, a.sx_out + tok,
-                             a.sums_out + 2 * tok, true);
+  int8_t* xq_row = a.xq_out + (size_t)tok * (2 * QWEN_HIDDEN);
+  if (splits == 1)
+    reduce_norm_quant_row_zb<EPI, 1, NoIssue, 2>(a, splits, tok, xq_row, 256, a.sx_out + tok, a.sums_out + 2 * tok, true,
+                                                  NoIssue{});
+  else
+    reduce_norm_quant_row_zb<EPI, 5, NoIssue, 2>(a, splits, tok, xq_row, 256, a.sx_out + tok, a.sums_out + 2 * tok, true,
+                                                  NoIssue{});
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -2580,7 +2619,7 @@ static void launch_reduce(const GemmArgs& a, int splits, hipStream_t st) {
     hipLaunchKernelGGL(reduce_qkv_rope_kernel, dim3(a.tokens), dim3(256), 0, st, a, splits);
   } else if (a.fuse == kFuseNormQuant) {
     if (a.out_dim == QWEN_HIDDEN)
-      hipLaunchKernelGGL((reduce_norm_quant_wave_kernel<EPI>), dim3(a.tokens), dim3(64), 0, st, a, splits);
+      hipLaunchKernelGGL((reduce_norm_quant_pair_kernel<EPI>), dim3(a.tokens), dim3(128), 0, st, a, splits);
     else
       hipLaunchKernelGGL((reduce_norm_quant_kernel<EPI>), dim3(a.tokens), dim3(256), 0, st, a, splits);
   } else {
