@@ -110,3 +110,30 @@ def test_chunk_arguments_rejected(torch):
         m.synchronize()
     finally:
         m.close()
+
+
+def test_chunked_prefill_fast_wide_chunks(torch, layers2):
+    """Chunks of more than 256 tokens take the pipelined GEMMs with RoPE and the K/V append in the
+    Q/K/V projection's epilogue: three sequences of 200 tokens in two chunks of 100 (300 tokens per
+    launch; the second at past 100, inside a 32-key tile), FAST without bf16 rounding, against the
+    oracle's single prefill of each sequence (the three run in threads: the oracle releases the GIL)."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    from work_llm_accelerator_amd.model import FLAG_NO_BF16_ROUND, MODE_FAST, DeviceModel
+
+    B, S, chunks = 3, 200, [100, 100]
+    m = DeviceModel(1, layers2[1].weight_ddr, layers2[1].scale_ddr)
+    try:
+        xs = [round_bfloat16_array(random_hidden(6000 + b, S)) for b in range(B)]
+        got, cache = run_chunks(torch, m, MODE_FAST | FLAG_NO_BF16_ROUND, xs, chunks, S, 1)
+        with ThreadPoolExecutor(B) as ex:
+            refs = list(ex.map(lambda x: oracle_prefill(layers2[1:], x, S, rounding=False), xs))
+        for b, (ref, ks, vs) in enumerate(refs):
+            for c0, c1 in ((0, 100), (100, 200)):
+                sl = slice(c0 * HIDDEN, c1 * HIDDEN)
+                assert rel_err(got[b][sl], ref[sl]) <= FAST_TOL, (b, c0, rel_err(got[b][sl], ref[sl]))
+            gk = cache.k[0, b, :S].cpu().numpy().reshape(-1)
+            gv = cache.v[0, b, :S].cpu().numpy().reshape(-1)
+            assert rel_err(gk, ks[0]) <= FAST_TOL and rel_err(gv, vs[0]) <= FAST_TOL
+    finally:
+        m.close()
