@@ -327,9 +327,10 @@ def test_model_decode_fast_split(torch, layers2, model2, monkeypatch, pcus):
             assert rel_err(gk, rk) <= FAST_TOL, (b, l, rel_err(gk, rk))
 
 
-@pytest.mark.parametrize("S", [40, 150, 300])
+@pytest.mark.parametrize("S", [1, 16, 40, 150, 300])
 def test_model_prefill_fast_mid(torch, layers2, S):
-    """40 tokens: the 17..64-token GEMM path on prefill shapes; 150 tokens: the 65..256-token GEMM
+    """1 token: a one-token prompt (one key, a one-query attention block); 16 tokens: exactly one
+    token tile of the skinny GEMMs; 40 tokens: the 17..64-token GEMM path on prefill shapes; 150 tokens: the 65..256-token GEMM
     path and five causal 32-key tiles of the prefill attention (partial last tile); 300 tokens: the
     many-token GEMM (4-wave blocks: four full 64-token tiles and a partial one), ten key tiles and a
     partial last 16-query attention block."""
