@@ -50,6 +50,16 @@ __device__ __forceinline__ void store_agent(float* p, float v) {
 __device__ __forceinline__ float load_agent(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// The same for a pair of floats, as one 8-byte access.
+__device__ __forceinline__ void store_agent2(float2* p, float x, float y) {
+  const uint64_t v = (uint64_t)__float_as_uint(x) | ((uint64_t)__float_as_uint(y) << 32);
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float2 load_agent2(const float2* p) {
+  const uint64_t v =
+      __hip_atomic_load(reinterpret_cast<uint64_t*>(const_cast<float2*>(p)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return make_float2(__uint_as_float((uint32_t)v), __uint_as_float((uint32_t)(v >> 32)));
+}
 
 // Prefill SiLU for the FAST GEMM epilogue: v / (1 + e(-v)) with the division as v * rcp(1 + e)
 // (v_rcp_f32, 1 ulp).  For s = -v >= -1 the reference's approx_exp is its degree-6 Taylor series
@@ -2224,9 +2234,7 @@ attn_decode_kernel(const float* __restrict__ qkv, int qkv_stride, const float* _
       const int qh = kvh * QWEN_GROUPS + head;
       store_agent(&part[(((size_t)b * QWEN_Q_HEADS + qh) * nsplit + c) * QWEN_HEAD_DIM + d], A);
       if (d == 0) {
-        float* ml = reinterpret_cast<float*>(&pml[((size_t)b * QWEN_Q_HEADS + qh) * nsplit + c]);
-        store_agent(ml, M);
-        store_agent(ml + 1, L);
+        store_agent2(&pml[((size_t)b * QWEN_Q_HEADS + qh) * nsplit + c], M, L);
       }
     }
   }
@@ -2249,7 +2257,7 @@ attn_decode_kernel(const float* __restrict__ qkv, int qkv_stride, const float* _
   const int nc = (n + chunk - 1) / chunk;  // splits that hold keys
   float* ml = &s_acc[0][0][0];             // [12][kAttnMaxSplits][2] (m, l), then merge weights in place
   float* row = &qs[0][0];                  // [1536] context row
-  const float* pb = reinterpret_cast<const float*>(pml + (size_t)b * QWEN_Q_HEADS * nsplit);
+  const float2* pb = pml + (size_t)b * QWEN_Q_HEADS * nsplit;
   const int d = threadIdx.x & 127;
   const int h0 = threadIdx.x >> 7;
   const float* pa = part + (size_t)b * QWEN_Q_HEADS * nsplit * QWEN_HEAD_DIM + d;
@@ -2264,8 +2272,9 @@ attn_decode_kernel(const float* __restrict__ qkv, int qkv_stride, const float* _
   load_part(0);
   for (int i = threadIdx.x; i < QWEN_Q_HEADS * nc; i += 256) {
     const int h = i / nc, sp = i % nc;
-    ml[(h * kAttnMaxSplits + sp) * 2] = load_agent(pb + 2 * (h * nsplit + sp));
-    ml[(h * kAttnMaxSplits + sp) * 2 + 1] = load_agent(pb + 2 * (h * nsplit + sp) + 1);
+    const float2 v = load_agent2(pb + h * nsplit + sp);  // (m, l) in one memory round trip
+    ml[(h * kAttnMaxSplits + sp) * 2] = v.x;
+    ml[(h * kAttnMaxSplits + sp) * 2 + 1] = v.y;
   }
   __syncthreads();
   if (threadIdx.x < QWEN_Q_HEADS) {
