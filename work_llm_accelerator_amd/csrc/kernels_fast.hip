@@ -1394,6 +1394,13 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
     }
   };
   auto issue_scalars = [&]() {
+    // The bias is loaded unconditionally (the row scales stand in when there is none, masked to +0
+    // by their bits, which leaves the epilogue's arithmetic as it is): a load under a run-time
+    // condition is a branch, after which the compiler waits for every load in flight, so each of
+    // them would be a memory round trip of its own.
+    constexpr bool kBias = EPI == kEpiStore && !DUAL;
+    const float* bsrc = kBias && a.bias ? a.bias : a.sw;
+    const uint32_t bmask = kBias && a.bias ? 0xFFFFFFFFu : 0u;
 #pragma unroll
     for (int r = 0; r < RTW; ++r) {
       const int row0 = (ok[r] ? rg * 4 * RTW + wave + 4 * r : 0) * 16 + 4 * g;
@@ -1401,7 +1408,7 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
       for (int q = 0; q < 4; ++q) {
         swv[r][q] = a.sw[row0 + q];
         sw2v[r][q] = DUAL ? a.sw2[row0 + q] : 0.0f;
-        biasv[r][q] = (EPI == kEpiStore && !DUAL && a.bias) ? a.bias[row0 + q] : 0.0f;
+        biasv[r][q] = kBias ? __uint_as_float(__float_as_uint(bsrc[row0 + q]) & bmask) : 0.0f;
       }
     }
     if constexpr (!kMade) {
