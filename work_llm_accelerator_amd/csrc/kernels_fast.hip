@@ -1462,11 +1462,14 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
     __builtin_amdgcn_sched_barrier(0);  // the slice reads below stay after the barrier
   }
 
-  // RoPE cos/sin of pairs p = 16*wave + 4g + q, q < 4, at position P: in flight during the MFMAs
+  // RoPE cos/sin of pairs p = 16*wave + 4g + q, q < 4, at position P: in flight during the MFMAs.
+  // Loaded by every lane at a clamped position (rope_in selects their use): under a run-time
+  // condition the load is a branch, whose join waited for every load in flight, the weight stream
+  // included, before the first MFMA.
   const bool rope_in = ROPE && P >= 0 && P < a.limit;
   float4 rc = make_float4(1.0f, 1.0f, 1.0f, 1.0f), rs = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-  if (rope_in && kg == 0) {
-    const float* rr = a.rope + (size_t)P * 128 + 16 * wave + 4 * g;
+  if constexpr (ROPE) {
+    const float* rr = a.rope + (size_t)min(max(P, 0), a.limit - 1) * 128 + 16 * wave + 4 * g;
     rc = *reinterpret_cast<const float4*>(rr);
     rs = *reinterpret_cast<const float4*>(rr + 64);
   }
@@ -2047,24 +2050,25 @@ __global__ void __launch_bounds__(64) rope_qkv_kernel(float* __restrict__ qkv, i
 typedef float v4f __attribute__((ext_vector_type(4)));
 constexpr int kQRow = QWEN_HEAD_DIM + 4;  // LDS floats per query row (16-byte pad: no bank aliasing)
 
-// Loads of one 16-key tile of attn_decode_kernel (keys tb..tb+15; MASK: keys >= t1 are not read).
+// Loads of one 16-key tile of attn_decode_kernel (keys tb..tb+15).  MASK: keys >= t1 read row t1 - 1
+// instead, as the first tile does: their scores are masked to -inf, so their weight is exactly 0
+// and the finite rows add 0.  (Loads under a per-lane condition were branches, each followed by a
+// wait for every load in flight, so the tile's loads went out one round trip at a time.)
 template <bool MASK>
 __device__ __forceinline__ void attn_decode_tile_load(const float* __restrict__ kb, const float* __restrict__ vb,
                                                       int tb, int t1, int col, int g, float4 (&kr)[8],
                                                       float4 (&vr)[4][2]) {
-  const int tk = tb + col;
+  const int tk = MASK ? min(tb + col, t1 - 1) : tb + col;
   const float* krow = kb + (size_t)tk * QWEN_KV_WIDTH + 4 * g;
 #pragma unroll
-  for (int j = 0; j < 8; ++j)
-    kr[j] = (!MASK || tk < t1) ? ld_stream(reinterpret_cast<const float4*>(krow + 16 * j)) : make_float4(0, 0, 0, 0);
-  const float* vrow = vb + (size_t)(tb + 4 * g) * QWEN_KV_WIDTH + 4 * col;
+  for (int j = 0; j < 8; ++j) kr[j] = ld_stream(reinterpret_cast<const float4*>(krow + 16 * j));
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
+  for (int r = 0; r < 4; ++r) {
+    const int tv = MASK ? min(tb + 4 * g + r, t1 - 1) : tb + 4 * g + r;
+    const float* vrow = vb + (size_t)tv * QWEN_KV_WIDTH + 4 * col;
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
-      vr[r][h] = (!MASK || tb + 4 * g + r < t1)
-                     ? ld_stream(reinterpret_cast<const float4*>(vrow + r * QWEN_KV_WIDTH + 64 * h))
-                     : make_float4(0, 0, 0, 0);
+    for (int h = 0; h < 2; ++h) vr[r][h] = ld_stream(reinterpret_cast<const float4*>(vrow + 64 * h));
+  }
   // All 16 loads of the tile are issued before any math (16 KiB in flight per wave): without this
   // fence the register-capped scheduler interleaves each load with its first use.
   __builtin_amdgcn_sched_barrier(0);
