@@ -87,12 +87,23 @@ struct GemmArgs {
   int defer_reduce;     // kFuseNormQuant, one token: write the partials only; the next projection's
                         // blocks finish the row (launch_gemm_i8_pre)
   int seq_len, past;    // kFuseRopePrefill (with rope, k_cache, v_cache, seq_stride, limit)
+  // Grouped two-limb code of the down projection's input (decode batches of 2..64 tokens): every
+  // 64-wide K group g of token t has its own scale gsx[t * (n/64) + g] and offset term
+  // 256 * sum H + sum L over the group in gcorr[t * (n/64) + g].  The gate/up projection writes it
+  // (xq_out, gsx_out, gcorr_out, in place of its fp32 output) and the skinny down projection reads it
+  // (gsx, gcorr; its partials then carry the offset correction, so the reduce step gets zero sums).
+  float* gsx_out;
+  int* gcorr_out;
+  const float* gsx;
+  const int* gcorr;
 };
 
 // K splits across blocks: at most kMaxSplits splits, only for GEMMs of at most kSplitTokens tokens;
 // the workspace holds kMaxSplits x kSplitTokens x out floats.
 constexpr int kMaxSplits = 16;
 constexpr int kSplitTokens = 256;
+// Decode GEMMs of at most kSkinnyTokens tokens (in_dim 1536 or 8960) run the skinny kernels.
+constexpr int kSkinnyTokens = 64;
 inline size_t splitk_bytes(size_t out) { return (size_t)kMaxSplits * kSplitTokens * out * 4u; }
 
 void launch_repack_int4(const uint8_t* W, int out_dim, int in_dim, uint8_t* WP, hipStream_t st);

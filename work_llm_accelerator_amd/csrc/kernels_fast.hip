@@ -1298,7 +1298,7 @@ __device__ __forceinline__ void attn_merge_quant_slice(const AttnMergeArgs& am, 
 // (one token, KSW = 1, the 1536-wide context row): every block merges the decode attention's split
 // partials (am) and quantizes the row into the slice; block 0 writes its scale and limb sums.
 template <int RTW, bool DUAL, int EPI, int NKC, bool ROPE, int KSW, bool PRE, int PRE_EPI = kEpiStore,
-          bool PRE_QUANT = false, bool PRE_ATTN = false>
+          bool PRE_QUANT = false, bool PRE_ATTN = false, bool GRP = false>
 __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count, int rg_count, int splits,
                                                  const GemmArgs& pre, int pre_splits,
                                                  const AttnMergeArgs& am = AttnMergeArgs{}) {
@@ -1308,6 +1308,10 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   static_assert(!PRE_ATTN || (KSW == 1 && !PRE && !PRE_QUANT && NKC * kKChunk == QWEN_HIDDEN),
                 "PRE_ATTN: one K group over the 1536-wide context row");
   constexpr bool kMade = PRE || PRE_QUANT || PRE_ATTN;  // the slice is made by the block
+  // GRP: the activations are the grouped two-limb code (GemmArgs::gsx, gcorr): each 64-wide K group,
+  // one MFMA of a K chunk, is dequantized with its own scale, so the block's partials are fp32 sums
+  // over groups that already carry the offset correction
+  static_assert(!GRP || (!DUAL && !ROPE && KSW == 1 && !kMade), "grouped code: the skinny down projection");
   constexpr int KC = NKC / KSW;  // K chunks per wave group
   static_assert(NKC % KSW == 0, "K chunks split evenly over the wave groups");
   static_assert(RTW * D * 8 * 1024 <= NKC * 16 * 256 || KSW == 1, "K-group reduction fits the slice buffer");
@@ -1350,10 +1354,19 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   const int P = ROPE ? a.pos[min(tok0 + col, a.tokens - 1)] : 0;
   uint4 wv[RTW][D][KC];
   bool ok[RTW];
+  // Row tile of the wave's tile r: rg*4*RTW + wave + 4r.  A gate/up block writing the grouped code
+  // takes instead the four row tiles of one K group of the down projection's input: the down
+  // projection's 16x16x64 products cover, per 128-wide K chunk c, the K of row tiles 8c + {0,2,4,6}
+  // (one product) and 8c + {1,3,5,7} (the other), so block rg takes tiles 8(rg/2) + 2 wave + rg%2 and
+  // its 64 rows are exactly group rg.
+  const bool gmap = EPI == kEpiSiluMul && DUAL && !kMade && KSW == 1 && RTW == 1 && a.gsx_out != nullptr;
+  auto row_tile = [&](int r) { return gmap ? 8 * (rg >> 1) + 2 * wave + (rg & 1) : rg * 4 * RTW + wave + 4 * r; };
   float swv[RTW][4], sw2v[RTW][4], biasv[RTW][4];
   const int tok_l = min(tok0 + col, a.tokens - 1);
   float sx_l = 0.0f;
   int sh_l = 0, sl_l = 0;
+  float gsv[GRP ? 2 * KC : 1];  // GRP: scales and offset terms of the lane's token's 2*KC groups
+  int gcv[GRP ? 2 * KC : 1];
   // The decode SiLU's exp table, copied to LDS before the MFMAs: read from constant memory in the
   // epilogue, each of a lane's SiLU evaluations waited on one more memory round trip (several tokens;
   // with one token the copy cost as much as it saved).
@@ -1361,7 +1374,7 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   __shared__ uint64_t exp_tab[kTab ? 32 : 1];
   uint64_t tab_v = 0;
 #pragma unroll
-  for (int r = 0; r < RTW; ++r) ok[r] = rg * 4 * RTW + wave + 4 * r < row_tiles;
+  for (int r = 0; r < RTW; ++r) ok[r] = row_tile(r) < row_tiles;
   // Weight tiles -> registers in K-chunk order (one 16-byte load per chunk and tile, chunk c's loads
   // before chunk c+1's), and the epilogue's per-row scales (and bias) and per-token scale and limb
   // sums: none depends on the MFMAs, and loaded after them they would cost one more round trip.
@@ -1371,7 +1384,7 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
     if constexpr (kMade) {
 #pragma unroll
       for (int r = 0; r < RTW; ++r) {
-        const int rt = rg * 4 * RTW + wave + 4 * r;
+        const int rt = row_tile(r);
         const size_t base = ((size_t)(ok[r] ? rt : 0) * nkc_all + kc0 + kg * KC) * 64u + lane;
 #pragma unroll
         for (int d = 0; d < D; ++d) {
@@ -1385,7 +1398,7 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
       for (int c = 0; c < KC; ++c)
 #pragma unroll
         for (int r = 0; r < RTW; ++r) {
-          const int rt = rg * 4 * RTW + wave + 4 * r;
+          const int rt = row_tile(r);
           const size_t base = ((size_t)(ok[r] ? rt : 0) * nkc_all + kc0 + kg * KC + c) * 64u + lane;
 #pragma unroll
           for (int d = 0; d < D; ++d)  // cached: reused by the XCD's other token tiles
@@ -1403,7 +1416,7 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
     const uint32_t bmask = kBias && a.bias ? 0xFFFFFFFFu : 0u;
 #pragma unroll
     for (int r = 0; r < RTW; ++r) {
-      const int row0 = (ok[r] ? rg * 4 * RTW + wave + 4 * r : 0) * 16 + 4 * g;
+      const int row0 = (ok[r] ? row_tile(r) : 0) * 16 + 4 * g;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         swv[r][q] = a.sw[row0 + q];
@@ -1415,6 +1428,17 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
       sx_l = a.sx[tok_l];
       sh_l = a.sums[2 * tok_l];
       sl_l = a.sums[2 * tok_l + 1];
+    }
+    if constexpr (GRP) {
+      static_assert((2 * KC) % 4 == 0, "groups in float4 loads");
+      const size_t gb = (size_t)tok_l * (a.in_dim / 64) + 2 * (kc0 + kg * KC);  // 16-byte aligned: KC even, in_dim % 256 == 0
+#pragma unroll
+      for (int i = 0; i < 2 * KC; i += 4) {
+        const float4 s4 = *reinterpret_cast<const float4*>(a.gsx + gb + i);
+        const int4 c4 = *reinterpret_cast<const int4*>(a.gcorr + gb + i);
+        gsv[i] = s4.x, gsv[i + 1] = s4.y, gsv[i + 2] = s4.z, gsv[i + 3] = s4.w;
+        gcv[i] = c4.x, gcv[i + 1] = c4.y, gcv[i + 2] = c4.z, gcv[i + 3] = c4.w;
+      }
     }
     if constexpr (kTab) tab_v = kExp2Tab[lane & 31];
   };
@@ -1478,8 +1502,38 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   for (int r = 0; r < RTW; ++r)
 #pragma unroll
     for (int d = 0; d < D; ++d) accH[r][d] = accL[r][d] = v4i{0, 0, 0, 0};
+  float gacc[GRP ? RTW : 1][4] = {};  // GRP: sum over groups of scale * (exact group dot product)
 #pragma unroll
   for (int c = 0; c < KC; ++c) {
+    if constexpr (GRP) {
+      const uint8_t* xr = xs + ((kg * KC + c) * 16 + col) * 256;
+      const v4i bh1 = *reinterpret_cast<const v4i*>(xr + (((2 * g) ^ col) << 4));
+      const v4i bh2 = *reinterpret_cast<const v4i*>(xr + (((2 * g + 1) ^ col) << 4));
+      const v4i bl1 = *reinterpret_cast<const v4i*>(xr + (((8 + 2 * g) ^ col) << 4));
+      const v4i bl2 = *reinterpret_cast<const v4i*>(xr + (((9 + 2 * g) ^ col) << 4));
+#pragma unroll
+      for (int r = 0; r < RTW; ++r) {
+        v4i a1, a2;
+        unpack16(wv[r][0][c], a1, a2);
+        const v4i z = v4i{0, 0, 0, 0};
+        const v4i h1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bh1, z, 0, 0, 0);  // group 2c: K 0..63
+        const v4i l1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bl1, z, 0, 0, 0);
+        const v4i h2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2, bh2, z, 0, 0, 0);  // group 2c+1: K 64..127
+        const v4i l2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2, bl2, z, 0, 0, 0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)  // the group's integer dot product, exact in int32 (< 2^26), then fp32
+          gacc[r][q] += gsv[2 * c] * (float)(h1[q] * 256 + l1[q] - 8 * gcv[2 * c]) +
+                        gsv[2 * c + 1] * (float)(h2[q] * 256 + l2[q] - 8 * gcv[2 * c + 1]);
+      }
+      // each chunk's products are consumed before the next chunk's: without an accumulator chain the
+      // compiler would issue every chunk's MFMAs first and hold all their results
+#pragma unroll
+      for (int r = 0; r < RTW; ++r)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) asm volatile("" : "+v"(gacc[r][q]));
+      __builtin_amdgcn_sched_barrier(0);
+      continue;
+    }
     const uint8_t* xr = xs + ((kg * KC + c) * 16 + col) * 256;
     const v4i bh1 = *reinterpret_cast<const v4i*>(xr + (((2 * g) ^ col) << 4));
     const v4i bh2 = *reinterpret_cast<const v4i*>(xr + (((2 * g + 1) ^ col) << 4));
@@ -1526,6 +1580,73 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
         }
   }
 
+  if constexpr (EPI == kEpiSiluMul && DUAL && !kMade && KSW == 1 && RTW == 1) {
+    if (a.gsx_out) {
+      // Grouped code of the SiLU·up rows for the down projection: the block's 64 rows (rows 64rg..,
+      // K group rg of the down projection's input) of each of its tokens are quantized with the group's
+      // own maximum, by the row quantizer's arithmetic (X = clip(rint(s * 32512 / max)), limbs
+      // H = (X + 128) >> 8 and L = X - 256 H), and written with the group's scale and offset term.
+      __shared__ float gq_max[4][16];
+      __shared__ int gq_h[4][16], gq_l[4][16];
+      const int tok = tok0 + col;
+      const bool valid = tok < a.tokens && ok[0];
+      const int row0 = row_tile(0) * 16 + 4 * g;
+      const int sh8 = 8 * sh_l, sl8 = 8 * sl_l;
+      const double sx = (double)sx_l;
+      float s[4], m = 0.0f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const double tot = (double)(accH[0][0][q] - sh8) * 256.0 + (double)(accL[0][0][q] - sl8);
+        const double tot2 = (double)(accH[0][1][q] - sh8) * 256.0 + (double)(accL[0][1][q] - sl8);
+        const float v = (float)(tot * sx) * swv[0][q];
+        const float u = (float)(tot2 * sx) * sw2v[0][q];
+        const float sg = a.prefill_silu ? silu_prefill(v) : silu_decode(v, kTab ? exp_tab : kExp2Tab);
+        s[q] = valid ? sg * u : 0.0f;
+        m = fmaxf(m, fabsf(s[q]));
+      }
+      m = fmaxf(m, __shfl_xor(m, 16, 64));  // over the wave's 16 rows of the token (g)
+      m = fmaxf(m, __shfl_xor(m, 32, 64));
+      if (g == 0) gq_max[wave][col] = m;
+      __syncthreads();
+      const float amax = fmaxf(fmaxf(gq_max[0][col], gq_max[1][col]), fmaxf(gq_max[2][col], gq_max[3][col]));
+      const float inv = amax > 0.0f ? (float)kQuantMax / amax : 0.0f;
+      uint32_t hw = 0, lw = 0;
+      int sh = 0, sl = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float xf = fminf(fmaxf(rintf(s[q] * inv), -(float)kQuantMax), (float)kQuantMax);
+        const int X = (int)xf;
+        const int H = (X + 128) >> 8;
+        const int L = X - (H << 8);
+        hw |= (uint32_t)(H & 0xFF) << (8 * q);
+        lw |= (uint32_t)(L & 0xFF) << (8 * q);
+        sh += H;
+        sl += L;
+      }
+      sh += __shfl_xor(sh, 16, 64);
+      sh += __shfl_xor(sh, 32, 64);
+      sl += __shfl_xor(sl, 16, 64);
+      sl += __shfl_xor(sl, 32, 64);
+      if (g == 0) {
+        gq_h[wave][col] = sh;
+        gq_l[wave][col] = sl;
+      }
+      __syncthreads();
+      if (valid) {  // limbs of K = row0 .. row0+3: chunk row0 / 128, H at +0, L at +128
+        int8_t* dst = a.xq_out + (size_t)tok * (2 * (size_t)a.out_dim) + (row0 >> 7) * 256 + (row0 & 127);
+        *reinterpret_cast<uint32_t*>(dst) = hw;
+        *reinterpret_cast<uint32_t*>(dst + 128) = lw;
+      }
+      if (wave == 0 && g == 0 && tok < a.tokens) {
+        const size_t gi = (size_t)tok * (a.out_dim / 64) + rg;
+        a.gsx_out[gi] = amax > 0.0f ? amax / (float)kQuantMax : 1.0f;
+        a.gcorr_out[gi] = 256 * (gq_h[0][col] + gq_h[1][col] + gq_h[2][col] + gq_h[3][col]) +
+                          (gq_l[0][col] + gq_l[1][col] + gq_l[2][col] + gq_l[3][col]);
+      }
+      return;
+    }
+  }
+
   // epilogue: lane holds rows 16*rt + 4g + q (q < 4) of token tok0 + col
   const int tok = tok0 + col;
   if (tok >= a.tokens) return;
@@ -1535,11 +1656,12 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
 #pragma unroll
     for (int r = 0; r < RTW; ++r) {
       if (!ok[r]) continue;
-      const int row0 = (rg * 4 * RTW + wave + 4 * r) * 16 + 4 * g;
+      const int row0 = row_tile(r) * 16 + 4 * g;
       float out[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q)
-        out[q] = (float)(((double)accH[r][0][q] * 256.0 + (double)accL[r][0][q]) * sx) * swv[r][q];
+        out[q] = GRP ? gacc[r][q] * swv[r][q]
+                     : (float)(((double)accH[r][0][q] * 256.0 + (double)accL[r][0][q]) * sx) * swv[r][q];
       *reinterpret_cast<float4*>(a.part + ((size_t)z * a.tokens + tok) * a.out_dim + row0) =
           make_float4(out[0], out[1], out[2], out[3]);
     }
@@ -1550,7 +1672,7 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   float y[RTW][4];
 #pragma unroll
   for (int r = 0; r < RTW; ++r) {
-    const int row0 = (rg * 4 * RTW + wave + 4 * r) * 16 + 4 * g;
+    const int row0 = row_tile(r) * 16 + 4 * g;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       if (!ok[r]) {
@@ -1602,7 +1724,7 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
 #pragma unroll
     for (int r = 0; r < RTW; ++r) {
       if (!ok[r]) continue;
-      const int row0 = (rg * 4 * RTW + wave + 4 * r) * 16 + 4 * g;
+      const int row0 = row_tile(r) * 16 + 4 * g;
       float o[4] = {y[r][0], y[r][1], y[r][2], y[r][3]};
       if (EPI == kEpiResidual && a.y_raw)
         *reinterpret_cast<float4*>(a.y_raw + (size_t)tok * a.y_stride + row0) = make_float4(o[0], o[1], o[2], o[3]);
@@ -1614,10 +1736,11 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   }
 }
 
-template <int RTW, bool DUAL, int EPI, int NKC, bool ROPE, int KSW>
+template <int RTW, bool DUAL, int EPI, int NKC, bool ROPE, int KSW, bool GRP = false>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(3)))
 gemm_skinny_kernel(GemmArgs a, int tt_count, int rg_count, int splits) {
-  gemm_skinny_body<RTW, DUAL, EPI, NKC, ROPE, KSW, false>(a, tt_count, rg_count, splits, a, 0);
+  gemm_skinny_body<RTW, DUAL, EPI, NKC, ROPE, KSW, false, kEpiStore, false, false, GRP>(a, tt_count, rg_count, splits,
+                                                                                      a, 0);
 }
 
 // One token, the activation row quantized by every block for its own K chunks (see PRE_QUANT above).
@@ -2663,15 +2786,14 @@ static void launch_gemm_pipe_t(const GemmArgs& a, int splits, hipStream_t st) {
 
 // Skinny GEMMs for at most kSkinnyTokens tokens with in_dim 1536 (12 K chunks in one block) or 8960
 // (5 splits of 14 chunks, finished by the reduce step).  Returns false for other shapes.
-constexpr int kSkinnyTokens = 64;
 
-template <int RTW, bool DUAL, int EPI, int NKC, bool ROPE, int KSW = 1>
+template <int RTW, bool DUAL, int EPI, int NKC, bool ROPE, int KSW = 1, bool GRP = false>
 static void launch_skinny_t(const GemmArgs& a, int rg_count, int splits, hipStream_t st) {
   const int tt = (a.tokens + 15) / 16;
   const int groups = rg_count * splits;
   const int blocks = 8 * tt * ((groups + 7) / 8);
-  hipLaunchKernelGGL((gemm_skinny_kernel<RTW, DUAL, EPI, NKC, ROPE, KSW>), dim3(blocks), dim3(256 * KSW), 0, st, a, tt,
-                     rg_count, splits);
+  hipLaunchKernelGGL((gemm_skinny_kernel<RTW, DUAL, EPI, NKC, ROPE, KSW, GRP>), dim3(blocks), dim3(256 * KSW), 0, st, a,
+                     tt, rg_count, splits);
 }
 
 template <int EPI, bool DUAL>
@@ -2697,7 +2819,10 @@ static bool launch_skinny(const GemmArgs& a, hipStream_t st) {
   }
   if constexpr (!DUAL) {
     if (a.in_dim == QWEN_INTERMEDIATE && a.part && a.fuse != kFuseQkvRope) {
-      launch_skinny_t<1, false, EPI, 14, false>(a, row_tiles / 4, 5, st);
+      if (a.gsx && a.gcorr)  // the grouped code of the SiLU·up rows
+        launch_skinny_t<1, false, EPI, 14, false, 1, true>(a, row_tiles / 4, 5, st);
+      else
+        launch_skinny_t<1, false, EPI, 14, false>(a, row_tiles / 4, 5, st);
       if (!(a.defer_reduce && a.tokens == 1 && a.fuse == kFuseNormQuant)) launch_reduce<EPI>(a, 5, st);
       return true;
     }

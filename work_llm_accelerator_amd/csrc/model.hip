@@ -92,7 +92,16 @@ struct qwen_hip_model {
     unsigned* arrivals;
     float* splitk;  // K-split partials of the non-dual projections (out <= 2048)
     uint8_t* kvt;   // prefill attention: bf16 hi/lo K/V tiles of one layer
+    int8_t* gxq;    // grouped code of the SiLU·up rows (2..64 tokens): limbs, per-(token, 64-row group)
+    float* gsx;     //   scales and offset terms
+    int* gcorr;
+    const int* zero_sums;  // kSkinnyTokens x (0, 0): the limb sums of code whose offsets are applied per group
   };
+  // Fixed region at the start of the workspace: the decode attention's arrival counters, then the zero
+  // limb sums; both are zeroed once per workspace buffer and never written otherwise (the counters
+  // are re-armed by the attention itself).
+  static constexpr size_t kZeroSumsOffset = (kMaxArrivals * 4u + 255u) & ~size_t(255u);
+  static constexpr size_t kFixedBytes = kZeroSumsOffset + ((kSkinnyTokens * 8u + 255u) & ~size_t(255u));
   Ws carve(size_t tokens, size_t batch, size_t nsplit, size_t kvt_bytes = 0) {
     size_t off = 0;
     auto take = [&](size_t bytes) {
@@ -100,7 +109,8 @@ struct qwen_hip_model {
       off = (off + bytes + 255u) & ~size_t(255u);
       return o;
     };
-    const size_t o_arr = take(kMaxArrivals * 4u);  // fixed offset: never overlaps the parts below
+    const size_t o_arr = take(kMaxArrivals * 4u);  // fixed offsets: never overlap the parts below
+    const size_t o_zs = take(kSkinnyTokens * 8u);
     const size_t o_xq = take(xq_bytes(tokens, QWEN_INTERMEDIATE));
     const size_t o_sx = take(tokens * 4u);
     const size_t o_sums = take(tokens * 8u);
@@ -113,10 +123,15 @@ struct qwen_hip_model {
     const size_t o_pml = take(batch * QWEN_Q_HEADS * nsplit * 8u);
     const size_t o_splitk = take(splitk_bytes(kQkvRows));
     const size_t o_kvt = take(kvt_bytes);
+    const size_t gtok = tokens < (size_t)kSkinnyTokens ? tokens : (size_t)kSkinnyTokens;
+    const size_t o_gxq = take(xq_bytes(gtok, QWEN_INTERMEDIATE));
+    const size_t o_gsx = take(gtok * (QWEN_INTERMEDIATE / 64) * 4u);
+    const size_t o_gcorr = take(gtok * (QWEN_INTERMEDIATE / 64) * 4u);
     char* b = static_cast<char*>(ws.get(off));
     unsigned* arr = reinterpret_cast<unsigned*>(b + o_arr);
-    if (ws.generation != arrivals_ready) {  // fresh buffer: arm the counters once
-      launch_zero_u32(arr, kMaxArrivals, stream);
+    if (ws.generation != arrivals_ready) {  // fresh buffer: arm the counters and zero the sums once
+      static_assert(kZeroSumsOffset == kMaxArrivals * 4u, "counters and zero sums are one run of words");
+      launch_zero_u32(arr, (int)(kMaxArrivals + 2 * kSkinnyTokens), stream);
       arrivals_ready = ws.generation;
     }
     return Ws{reinterpret_cast<int8_t*>(b + o_xq), reinterpret_cast<float*>(b + o_sx),
@@ -124,12 +139,14 @@ struct qwen_hip_model {
               reinterpret_cast<float*>(b + o_ctx), reinterpret_cast<float*>(b + o_att),
               reinterpret_cast<float*>(b + o_s), reinterpret_cast<float*>(b + o_tmp),
               reinterpret_cast<float*>(b + o_part), reinterpret_cast<float2*>(b + o_pml), arr,
-              reinterpret_cast<float*>(b + o_splitk), reinterpret_cast<uint8_t*>(b + o_kvt)};
+              reinterpret_cast<float*>(b + o_splitk), reinterpret_cast<uint8_t*>(b + o_kvt),
+              reinterpret_cast<int8_t*>(b + o_gxq), reinterpret_cast<float*>(b + o_gsx), reinterpret_cast<int*>(b + o_gcorr),
+              reinterpret_cast<const int*>(b + o_zs)};
   }
 
-  // Plain scratch of `bytes` in the workspace, past the arrival counters.
+  // Plain scratch of `bytes` in the workspace, past the fixed region.
   float* scratch(size_t bytes) {
-    const size_t off = (kMaxArrivals * 4u + 255u) & ~size_t(255u);
+    const size_t off = kFixedBytes;
     return reinterpret_cast<float*>(static_cast<char*>(ws.get(off + bytes)) + off);
   }
 
@@ -260,6 +277,10 @@ struct qwen_hip_model {
     const Ws w = carve(B, B, plan.nsplit);
     const bool fused = B <= kSplitTokens;
     const bool one = fused && B == 1 && pre_reduce;  // one sequence: reduce steps in the next projection
+    // 2..64 sequences: the gate/up projection quantizes its SiLU·up rows per 64-row group for the down
+    // projection (no separate quantization launch).  One sequence keeps the row code in both forms
+    // (its prologue-fused form and the separate-launch form stay bit-identical).
+    const bool grouped = B >= 2 && B <= kSkinnyTokens;
     GemmArgs down_pending{};                         // the previous layer's deferred down projection
     for (int l = 0; l < layers; ++l) {
       const FastLayer& f = fast[l];
@@ -328,8 +349,12 @@ struct qwen_hip_model {
           launch_norm_quant(w.att, QWEN_HIDDEN, B, QWEN_HIDDEN, f.post_ln, kNormDecode, w.xq, w.sx, w.sums, nullptr,
                             stream);
         }
+        GemmArgs gq{};
+        gq.xq_out = w.gxq;
+        gq.gsx_out = w.gsx;
+        gq.gcorr_out = w.gcorr;
         gemm(w, B, QWEN_HIDDEN, QWEN_INTERMEDIATE, f.gate, f.sw_gate, nullptr, w.s, QWEN_INTERMEDIATE, kEpiSiluMul,
-             f.up, f.sw_up, nullptr, 0, 0);
+             f.up, f.sw_up, nullptr, 0, 0, grouped ? &gq : nullptr);
       }
       const bool fuse_next = fused && l + 1 < layers;  // the next layer's input RMSNorm + quantize
       fn.norm_w = fuse_next ? fast[l + 1].ln : nullptr;
@@ -348,10 +373,18 @@ struct qwen_hip_model {
         if (!launch_gemm_i8_preq(da, sq, stream)) throw std::runtime_error("down with the quantization: bad shape");
         if (fuse_next) down_pending = da;
       } else {
-        launch_norm_quant(w.s, QWEN_INTERMEDIATE, B, QWEN_INTERMEDIATE, nullptr, kNormNone, w.xq, w.sx, w.sums,
-                          nullptr, stream);
-        gemm(w, B, QWEN_INTERMEDIATE, QWEN_HIDDEN, f.down, f.sw_down, nullptr, hidden, QWEN_HIDDEN, kEpiResidual,
-             nullptr, nullptr, w.att, round, 0, fuse_next ? &fn : nullptr);
+        if (!grouped)
+          launch_norm_quant(w.s, QWEN_INTERMEDIATE, B, QWEN_INTERMEDIATE, nullptr, kNormNone, w.xq, w.sx, w.sums,
+                            nullptr, stream);
+        GemmArgs da = args(w, B, QWEN_INTERMEDIATE, QWEN_HIDDEN, f.down, f.sw_down, nullptr, hidden, QWEN_HIDDEN,
+                           nullptr, nullptr, w.att, round, 0, fuse_next ? &fn : nullptr);
+        if (grouped) {  // the down partials carry the per-group offsets: the reduce step gets zero sums
+          da.xq = w.gxq;
+          da.gsx = w.gsx;
+          da.gcorr = w.gcorr;
+          da.sums = w.zero_sums;
+        }
+        launch_gemm_i8(da, kEpiResidual, stream);
       }
     }
     QWEN_HIP(hipGetLastError());
