@@ -1503,30 +1503,40 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
 #pragma unroll
     for (int d = 0; d < D; ++d) accH[r][d] = accL[r][d] = v4i{0, 0, 0, 0};
   float gacc[GRP ? RTW : 1][4] = {};  // GRP: sum over groups of scale * (exact group dot product)
+  v4i gprod[2][GRP ? RTW : 1][4];     // GRP: products of two chunks in flight
 #pragma unroll
   for (int c = 0; c < KC; ++c) {
     if constexpr (GRP) {
-      const uint8_t* xr = xs + ((kg * KC + c) * 16 + col) * 256;
-      const v4i bh1 = *reinterpret_cast<const v4i*>(xr + (((2 * g) ^ col) << 4));
-      const v4i bh2 = *reinterpret_cast<const v4i*>(xr + (((2 * g + 1) ^ col) << 4));
-      const v4i bl1 = *reinterpret_cast<const v4i*>(xr + (((8 + 2 * g) ^ col) << 4));
-      const v4i bl2 = *reinterpret_cast<const v4i*>(xr + (((9 + 2 * g) ^ col) << 4));
+      // chunk c+1's products are issued before chunk c's are consumed, so each conversion works on
+      // products that have already left the matrix cores
+      auto products = [&](int cc, v4i (&p)[RTW][4]) {
+        const uint8_t* xr = xs + ((kg * KC + cc) * 16 + col) * 256;
+        const v4i bh1 = *reinterpret_cast<const v4i*>(xr + (((2 * g) ^ col) << 4));
+        const v4i bh2 = *reinterpret_cast<const v4i*>(xr + (((2 * g + 1) ^ col) << 4));
+        const v4i bl1 = *reinterpret_cast<const v4i*>(xr + (((8 + 2 * g) ^ col) << 4));
+        const v4i bl2 = *reinterpret_cast<const v4i*>(xr + (((9 + 2 * g) ^ col) << 4));
 #pragma unroll
-      for (int r = 0; r < RTW; ++r) {
-        v4i a1, a2;
-        unpack16(wv[r][0][c], a1, a2);
-        const v4i z = v4i{0, 0, 0, 0};
-        const v4i h1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bh1, z, 0, 0, 0);  // group 2c: K 0..63
-        const v4i l1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bl1, z, 0, 0, 0);
-        const v4i h2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2, bh2, z, 0, 0, 0);  // group 2c+1: K 64..127
-        const v4i l2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2, bl2, z, 0, 0, 0);
+        for (int r = 0; r < RTW; ++r) {
+          v4i a1, a2;
+          unpack16(wv[r][0][cc], a1, a2);
+          const v4i z = v4i{0, 0, 0, 0};
+          p[r][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bh1, z, 0, 0, 0);  // group 2cc, H limbs
+          p[r][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bl1, z, 0, 0, 0);  // group 2cc, L limbs
+          p[r][2] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2, bh2, z, 0, 0, 0);  // group 2cc+1
+          p[r][3] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2, bl2, z, 0, 0, 0);
+        }
+      };
+      if (c == 0) products(0, gprod[0]);
+      if (c + 1 < KC) products(c + 1, gprod[(c + 1) & 1]);
+      const v4i (&p)[RTW][4] = gprod[c & 1];
+#pragma unroll
+      for (int r = 0; r < RTW; ++r)
 #pragma unroll
         for (int q = 0; q < 4; ++q)  // the group's integer dot product, exact in int32 (< 2^26), then fp32
-          gacc[r][q] += gsv[2 * c] * (float)(h1[q] * 256 + l1[q] - 8 * gcv[2 * c]) +
-                        gsv[2 * c + 1] * (float)(h2[q] * 256 + l2[q] - 8 * gcv[2 * c + 1]);
-      }
-      // each chunk's products are consumed before the next chunk's: without an accumulator chain the
-      // compiler would issue every chunk's MFMAs first and hold all their results
+          gacc[r][q] += gsv[2 * c] * (float)(p[r][0][q] * 256 + p[r][1][q] - 8 * gcv[2 * c]) +
+                        gsv[2 * c + 1] * (float)(p[r][2][q] * 256 + p[r][3][q] - 8 * gcv[2 * c + 1]);
+      // each chunk's products are consumed in its iteration: without an accumulator chain the compiler
+      // would issue every chunk's MFMAs first and hold all their results
 #pragma unroll
       for (int r = 0; r < RTW; ++r)
 #pragma unroll
