@@ -49,6 +49,27 @@ int qwen_hip_fast_quantize_rows(const float* x, int rows, int n, int8_t* xq, flo
 int qwen_hip_fast_project(const uint8_t* w, const float* sw, const float* bias, int out_dim, int in_dim,
                           const float* x, int tokens, int flags, float* y, void* stream);
 
+/* Grouped code of the decode of 2..64 sequences (no counterpart in the reference; for tests and callers
+ * that check that step on its own).  There the gate/up projection quantizes its SiLU·up rows not per
+ * row but per group of 64 rows g (the rows of row tiles 8(g/2) + 2j + g%2, j < 4: the K of one 16x16x64
+ * matrix-core product of the down projection), with that group's maximum: for each token t and group
+ * g of the 8960 rows, the two-limb code of the 64 values, scale gsx[t][g] = max / 32512 (1 for an
+ * all-zero group) and offset term gcorr[t][g] = 256 sum H + sum L, the limbs at the rows' places of
+ * xq [tokens][70][2][128].  qwen_hip_fast_silu_mul_grouped runs that projection (INT4 gate and up
+ * [8960][1536] in the reference layout with their row scales, on the two-limb code of x [tokens][1536],
+ * 1 <= tokens <= 64) twice on the same code: into y [tokens][8960] (fp32 SiLU(gate)·up) and into the
+ * grouped code (xq, gsx [tokens][140], gcorr [tokens][140]). */
+int qwen_hip_fast_silu_mul_grouped(const uint8_t* gate, const float* sw_gate, const uint8_t* up, const float* sw_up,
+                                   const float* x, int tokens, float* y, int8_t* xq, float* gsx, int32_t* gcorr,
+                                   void* stream);
+
+/* The down projection of a grouped code (as qwen_hip_fast_silu_mul_grouped writes it; tokens 1..64):
+ * y[t][o] = sw[o] * sum_g gsx[t][g] * (sum over the group's K of u X - 8 gcorr[t][g]) for the INT4 matrix w
+ * [out_dim][8960] (u = q + 8), out_dim a multiple of 64; each group's integer sum is exact, the sum over
+ * groups is fp32.  Allocates its own workspace and synchronizes `stream` before returning. */
+int qwen_hip_fast_project_grouped(const uint8_t* w, const float* sw, int out_dim, const int8_t* xq, const float* gsx,
+                                  const int32_t* gcorr, int tokens, float* y, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

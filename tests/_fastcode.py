@@ -44,3 +44,38 @@ def unpack_int4(packed: np.ndarray, out_dim: int, in_dim: int) -> np.ndarray:
     p = np.asarray(packed, dtype=np.uint8)
     nib = np.stack([p & 0xF, p >> 4], axis=1).reshape(-1)[: out_dim * in_dim].astype(np.int32)
     return np.where(nib >= 8, nib - 16, nib).reshape(out_dim, in_dim)
+
+
+GROUP = 64  # rows of one group of the grouped code (the K of one 16x16x64 matrix-core product)
+
+
+def group_rows(g: int) -> np.ndarray:
+    """Rows (down-projection K) of group g: row tiles 8(g//2) + 2j + g%2, j < 4, 16 rows each."""
+    tiles = 8 * (g // 2) + 2 * np.arange(4) + (g % 2)
+    return (16 * tiles[:, None] + np.arange(16)[None, :]).reshape(-1)
+
+
+def grouped_code(y: np.ndarray) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """Grouped two-limb code of rows y [tokens][n] (include/qwen_hip_ops.h): each group of 64 rows
+    (group_rows) of a token quantized with the group's own maximum, by two_limb_code's arithmetic.
+    Returns (xq int8 [tokens][n/128][2][128], gsx fp32 [tokens][n/64], gcorr int32 [tokens][n/64])."""
+    y = np.ascontiguousarray(y, dtype=np.float32)
+    tokens, n = y.shape
+    ng = n // GROUP
+    xq = np.zeros((tokens, n // CHUNK, 2, CHUNK), np.int8)
+    gsx = np.zeros((tokens, ng), np.float32)
+    gcorr = np.zeros((tokens, ng), np.int32)
+    for g in range(ng):
+        rows = group_rows(g)
+        v = y[:, rows]
+        amax = np.max(np.abs(v), axis=1)
+        with np.errstate(divide="ignore"):
+            inv = np.where(amax > 0, np.float32(QMAX) / amax, np.float32(0.0)).astype(np.float32)
+            gsx[:, g] = np.where(amax > 0, amax / np.float32(QMAX), np.float32(1.0)).astype(np.float32)
+        X = np.clip(np.rint((v * inv[:, None]).astype(np.float32)), -QMAX, QMAX).astype(np.int32)
+        H = (X + 128) >> 8
+        L = X - (H << 8)
+        xq[:, rows // CHUNK, 0, rows % CHUNK] = H.astype(np.int8)
+        xq[:, rows // CHUNK, 1, rows % CHUNK] = L.astype(np.int8)
+        gcorr[:, g] = 256 * H.sum(axis=1) + L.sum(axis=1)
+    return xq, gsx, gcorr

@@ -76,3 +76,29 @@ def test_layout_is_chunk_major():
 def test_unpack_int4_matches_the_reference_nibble_order():
     packed = np.array([0x21, 0xF8, 0x7E], np.uint8)  # flat 0,1 = 1,2; 2,3 = -8,-1; 4,5 = -2,7
     assert unpack_int4(packed, 1, 6).tolist() == [[1, 2, -8, -1, -2, 7]]
+
+
+def test_grouped_code_is_two_limb_code_per_group():
+    """The grouped code of a row is two_limb_code applied to each 64-row group on its own (padded with
+    zeros to a 128-wide row, which changes neither the maximum nor the sums), and the groups
+    partition the rows (each row's limbs come from exactly one group)."""
+    from _fastcode import GROUP, group_rows, grouped_code, two_limb_code
+
+    rng = np.random.default_rng(3)
+    n = 8960
+    y = np.stack([rng.standard_normal(n).astype(np.float32) * np.float32(s) for s in (1.0, 1e-3, 5e3)])
+    y[1, group_rows(5)] = 0.0  # an all-zero group: scale 1, zero limbs
+    xq, gsx, gcorr = grouped_code(y)
+    covered = np.zeros(n, bool)
+    for g in range(n // GROUP):
+        rows = group_rows(g)
+        assert not covered[rows].any()
+        covered[rows] = True
+        padded = np.concatenate([y[:, rows], np.zeros((y.shape[0], GROUP), np.float32)], axis=1)
+        rq, rsx, rsums, _ = two_limb_code(padded)
+        assert np.array_equal(xq[:, rows // 128, 0, rows % 128], rq[:, 0, 0, :GROUP])
+        assert np.array_equal(xq[:, rows // 128, 1, rows % 128], rq[:, 0, 1, :GROUP])
+        assert np.array_equal(gsx[:, g].view(np.uint32), rsx.view(np.uint32))
+        assert np.array_equal(gcorr[:, g], 256 * rsums[:, 0] + rsums[:, 1])
+    assert covered.all()
+    assert gsx[1, 5] == 1.0 and gcorr[1, 5] == 0

@@ -3,6 +3,11 @@
 * The two-limb activation code (limbs, the scale max|x| / 32512, the limb sums) of the device
   quantizer the FAST layers run before every projection equals tests/_fastcode.two_limb_code bit for
   bit, on rows of width 1536 and 8960 with ties, zero rows and extreme magnitudes.
+* The grouped code of the decode of 2..64 sequences (the gate/up projection's SiLU·up rows quantized
+  per 64-row group): the device's grouped code equals tests/_fastcode.grouped_code of the same
+  projection's fp32 output bit for bit, and the down projection of a grouped code with power-of-two
+  group scales equals the int64 sum over groups exactly (a group dequantized with another group's
+  scale, or rows of one group read into another, changes it).
 * Every kernel a FAST projection can take (the skinny decode GEMMs with one K group and with five
   K splits, the direct-load kernel with its in-block K split, the pipelined GEMM with and without a
   cross-block K split, the pipelined GEMM with two blocks per CU) accumulates the weight x activation
@@ -18,7 +23,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from _fastcode import QMAX, two_limb_code, unpack_int4
+from _fastcode import GROUP, QMAX, group_rows, grouped_code, two_limb_code, unpack_int4
 
 pytestmark = pytest.mark.gpu
 
@@ -171,3 +176,71 @@ def test_operator_argument_checks(lib):
     assert lib.qwen_hip_fast_project(p, p, None, 1024, 9088, p, 1, 0, p, None) == 1  # in > 8960
     assert lib.qwen_hip_fast_project(p, p, None, 1024, 1536, p, 0, 0, p, None) == 1  # no tokens
     assert lib.qwen_hip_fast_quantize_rows(p, 1, 100, p, p, p, None) == 1
+
+
+@pytest.mark.parametrize("tokens", [2, 17, 64])
+def test_grouped_silu_code_bitexact(torch, lib, tokens):
+    from work_llm_accelerator_amd import abi
+
+    print(f"grouped SiLU·up code: tokens={tokens}", flush=True)
+    rng = np.random.default_rng(tokens + 404)
+    out, inp = 8960, 1536
+    gate = rng.integers(0, 256, out * inp // 2, dtype=np.uint8)
+    up = rng.integers(0, 256, out * inp // 2, dtype=np.uint8)
+    swg = (rng.random(out, dtype=np.float32) * np.float32(0.02) + np.float32(1e-3)).astype(np.float32)
+    swu = (rng.random(out, dtype=np.float32) * np.float32(0.02) + np.float32(1e-3)).astype(np.float32)
+    x = rng.standard_normal((tokens, inp), dtype=np.float32)
+    d = [torch.from_numpy(v).cuda() for v in (gate, swg, up, swu, x)]
+    y = torch.zeros((tokens, out), dtype=torch.float32, device="cuda")
+    xq = torch.zeros(tokens * out * 2, dtype=torch.int8, device="cuda")
+    gsx = torch.zeros((tokens, out // GROUP), dtype=torch.float32, device="cuda")
+    gcorr = torch.zeros((tokens, out // GROUP), dtype=torch.int32, device="cuda")
+    st = lib.qwen_hip_fast_silu_mul_grouped(*[dptr(v) for v in d], tokens, dptr(y), dptr(xq), dptr(gsx), dptr(gcorr),
+                                            None)
+    assert st == 0, abi.last_error(lib)
+    rq, rsx, rcorr = grouped_code(y.cpu().numpy())
+    assert np.array_equal(xq.cpu().numpy(), rq.reshape(-1)), "limbs differ"
+    assert np.array_equal(gsx.cpu().numpy().view(np.uint32), rsx.view(np.uint32)), "group scales differ"
+    assert np.array_equal(gcorr.cpu().numpy(), rcorr), "group offset terms differ"
+
+
+@pytest.mark.parametrize("tokens", [2, 33, 64])
+def test_grouped_down_projection_exact(torch, lib, tokens):
+    from work_llm_accelerator_amd import abi
+
+    print(f"grouped down projection: tokens={tokens}", flush=True)
+    rng = np.random.default_rng(tokens + 505)
+    out, inp = 1536, 8960
+    ng = inp // GROUP
+    packed = rng.integers(0, 256, out * inp // 2, dtype=np.uint8)
+    q = unpack_int4(packed, out, inp).astype(np.int64)
+    X = rng.integers(-300, 301, (tokens, inp)).astype(np.int64)  # high limbs -1, 0 and 1
+    H = (X + 128) >> 8
+    L = X - 256 * H
+    xq = np.zeros((tokens, inp // 128, 2, 128), np.int8)
+    xq[:, np.arange(inp) // 128, 0, np.arange(inp) % 128] = H
+    xq[:, np.arange(inp) // 128, 1, np.arange(inp) % 128] = L
+    gsx = np.zeros((tokens, ng), np.float32)
+    gcorr = np.zeros((tokens, ng), np.int32)
+    ref = np.zeros((tokens, out), np.float64)
+    bound = np.zeros((tokens, out), np.float64)
+    for g in range(ng):
+        rows = group_rows(g)
+        gsx[:, g] = np.float32(2.0 ** (g % 3))
+        gcorr[:, g] = 256 * H[:, rows].sum(axis=1) + L[:, rows].sum(axis=1)
+        term = gsx[:, g:g + 1].astype(np.float64) * (X[:, rows] @ q[:, rows].T)
+        ref += term
+        bound += np.abs(term)
+    # every partial sum of the group terms is an integer below 2^24: any order of fp32 addition is exact
+    assert bound.max() < 2**24
+    sw = torch.ones(out, dtype=torch.float32, device="cuda")
+    d = [torch.from_numpy(v).cuda() for v in (packed, xq.reshape(-1), gsx, gcorr)]
+    y = torch.full((tokens, out), float("nan"), dtype=torch.float32, device="cuda")
+    st = lib.qwen_hip_fast_project_grouped(dptr(d[0]), dptr(sw), out, dptr(d[1]), dptr(d[2]), dptr(d[3]), tokens,
+                                           dptr(y), None)
+    assert st == 0, abi.last_error(lib)
+    got = y.cpu().numpy()
+    want = ref.astype(np.float32)
+    bad = np.nonzero(got.view(np.uint32) != want.view(np.uint32))
+    assert bad[0].size == 0, (f"{bad[0].size} outputs differ; first (t={bad[0][0]}, o={bad[1][0]}): "
+                              f"{got[bad[0][0], bad[1][0]]!r} vs {want[bad[0][0], bad[1][0]]!r}")

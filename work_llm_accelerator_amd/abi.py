@@ -85,6 +85,8 @@ EXTRA_SIGNATURES: dict[str, tuple[list, object]] = {
     # FAST operators (include/qwen_hip_ops.h)
     "qwen_hip_fast_quantize_rows": ([P, c_int, c_int, P, P, P, P], c_int),
     "qwen_hip_fast_project": ([P, P, P, c_int, c_int, P, c_int, c_int, P, P], c_int),
+    "qwen_hip_fast_silu_mul_grouped": ([P, P, P, P, P, c_int, P, P, P, P, P], c_int),
+    "qwen_hip_fast_project_grouped": ([P, P, c_int, P, P, P, c_int, P, P], c_int),
     # device-resident descriptor dispatch (include/qwen_hip_dispatch.h): descriptors on the host,
     # DDR images on the device
     "qwen_hip_decode_dispatch_layers": ([c_void_p, c_int, P, P, P, P, P, c_void_p], c_int),

@@ -98,4 +98,80 @@ int qwen_hip_fast_project(const uint8_t* w, const float* sw, const float* bias, 
   });
 }
 
+int qwen_hip_fast_silu_mul_grouped(const uint8_t* gate, const float* sw_gate, const uint8_t* up, const float* sw_up,
+                                   const float* x, int tokens, float* y, int8_t* xq, float* gsx, int32_t* gcorr,
+                                   void* stream) {
+  if (!gate || !sw_gate || !up || !sw_up || !x || !y || !xq || !gsx || !gcorr || tokens < 1 || tokens > kSkinnyTokens)
+    return op_invalid("invalid grouped SiLU·up arguments (1 to 64 tokens)");
+  return guarded_op([&]() -> int {
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    const int in = QWEN_HIDDEN, out = QWEN_INTERMEDIATE;
+    ScopedDev wg((size_t)out * in / 2), wu((size_t)out * in / 2);
+    ScopedDev xc(xq_bytes((size_t)tokens, (size_t)in));
+    ScopedDev sx((size_t)tokens * 4u);
+    ScopedDev sums((size_t)tokens * 8u);
+    launch_repack_int4(gate, out, in, wg.as<uint8_t>(), st);
+    launch_repack_int4(up, out, in, wu.as<uint8_t>(), st);
+    launch_norm_quant(x, (size_t)in, tokens, in, nullptr, kNormNone, xc.as<int8_t>(), sx.as<float>(), sums.as<int>(),
+                      nullptr, st);
+    GemmArgs a{};
+    a.wp = wg.as<uint8_t>();
+    a.wp2 = wu.as<uint8_t>();
+    a.sw = sw_gate;
+    a.sw2 = sw_up;
+    a.xq = xc.as<int8_t>();
+    a.sx = sx.as<float>();
+    a.sums = sums.as<int>();
+    a.tokens = tokens;
+    a.in_dim = in;
+    a.out_dim = out;
+    a.y = y;
+    a.y_stride = (size_t)out;
+    a.fuse = kFuseNone;
+    launch_gemm_i8(a, kEpiSiluMul, st);  // fp32 SiLU(gate)·up
+    a.xq_out = xq;
+    a.gsx_out = gsx;
+    a.gcorr_out = reinterpret_cast<int*>(gcorr);
+    launch_gemm_i8(a, kEpiSiluMul, st);  // the grouped code of the same values
+    QWEN_HIP(hipGetLastError());
+    QWEN_HIP(hipStreamSynchronize(st));
+    return QWEN_OK;
+  });
+}
+
+int qwen_hip_fast_project_grouped(const uint8_t* w, const float* sw, int out_dim, const int8_t* xq, const float* gsx,
+                                  const int32_t* gcorr, int tokens, float* y, void* stream) {
+  if (!w || !sw || !xq || !gsx || !gcorr || !y || out_dim <= 0 || out_dim % 64 != 0 || tokens < 1 ||
+      tokens > kSkinnyTokens)
+    return op_invalid("invalid grouped projection arguments (out_dim % 64, 1 to 64 tokens)");
+  return guarded_op([&]() -> int {
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    const int in = QWEN_INTERMEDIATE;
+    ScopedDev wp((size_t)out_dim * in / 2);
+    ScopedDev zero((size_t)tokens * 8u);  // limb sums of a code whose offsets are applied per group
+    ScopedDev part(splitk_bytes((size_t)out_dim));
+    launch_repack_int4(w, out_dim, in, wp.as<uint8_t>(), st);
+    launch_zero_u32(zero.as<unsigned>(), 2 * tokens, st);
+    GemmArgs a{};
+    a.wp = wp.as<uint8_t>();
+    a.sw = sw;
+    a.xq = xq;
+    a.sx = gsx;  // any finite per-token value: multiplied by the zero sums
+    a.sums = zero.as<int>();
+    a.gsx = gsx;
+    a.gcorr = reinterpret_cast<const int*>(gcorr);
+    a.tokens = tokens;
+    a.in_dim = in;
+    a.out_dim = out_dim;
+    a.y = y;
+    a.y_stride = (size_t)out_dim;
+    a.part = part.as<float>();
+    a.fuse = kFuseNone;
+    launch_gemm_i8(a, kEpiStore, st);
+    QWEN_HIP(hipGetLastError());
+    QWEN_HIP(hipStreamSynchronize(st));
+    return QWEN_OK;
+  });
+}
+
 }  // extern "C"
