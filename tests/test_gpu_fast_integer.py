@@ -178,7 +178,7 @@ def test_operator_argument_checks(lib):
     assert lib.qwen_hip_fast_quantize_rows(p, 1, 100, p, p, p, None) == 1
 
 
-@pytest.mark.parametrize("tokens", [2, 17, 64])
+@pytest.mark.parametrize("tokens", [1, 2, 17, 64])
 def test_grouped_silu_code_bitexact(torch, lib, tokens):
     from work_llm_accelerator_amd import abi
 
@@ -189,6 +189,7 @@ def test_grouped_silu_code_bitexact(torch, lib, tokens):
     up = rng.integers(0, 256, out * inp // 2, dtype=np.uint8)
     swg = (rng.random(out, dtype=np.float32) * np.float32(0.02) + np.float32(1e-3)).astype(np.float32)
     swu = (rng.random(out, dtype=np.float32) * np.float32(0.02) + np.float32(1e-3)).astype(np.float32)
+    swg[group_rows(5)] = 0.0  # an all-zero group: scale 1, zero limbs, zero offset term
     x = rng.standard_normal((tokens, inp), dtype=np.float32)
     d = [torch.from_numpy(v).cuda() for v in (gate, swg, up, swu, x)]
     y = torch.zeros((tokens, out), dtype=torch.float32, device="cuda")
@@ -202,9 +203,11 @@ def test_grouped_silu_code_bitexact(torch, lib, tokens):
     assert np.array_equal(xq.cpu().numpy(), rq.reshape(-1)), "limbs differ"
     assert np.array_equal(gsx.cpu().numpy().view(np.uint32), rsx.view(np.uint32)), "group scales differ"
     assert np.array_equal(gcorr.cpu().numpy(), rcorr), "group offset terms differ"
+    zr = group_rows(5)
+    assert np.all(rsx[:, 5] == 1.0) and not np.any(rq[:, zr // 128, :, zr % 128])  # the zero group was exercised
 
 
-@pytest.mark.parametrize("tokens", [2, 33, 64])
+@pytest.mark.parametrize("tokens", [1, 2, 33, 64])
 def test_grouped_down_projection_exact(torch, lib, tokens):
     from work_llm_accelerator_amd import abi
 

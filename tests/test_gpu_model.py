@@ -266,13 +266,15 @@ def test_synthetic_model_runs(torch):
         m.close()
 
 
-@pytest.mark.parametrize("batch", [20, 64, 100, 300])
+@pytest.mark.parametrize("batch", [2, 5, 20, 64, 100, 300])
 def test_model_decode_fast_batched(torch, layers2, batch):
     """Every sequence of the batch stays within the per-layer tolerance of the oracle, on each of
-    the batched paths: 17..64 sequences take the skinny GEMMs (activations staged in LDS, weights
+    the batched paths: 2..64 sequences take the skinny GEMMs (activations staged in LDS, weights
     in registers) with the RoPE/append and RMSNorm/quantization steps fused into their reduce
-    kernels; 65..256 the pipelined GEMMs split over K, with the same fused reduce steps; above 256
-    the unfused path (separate RMSNorm/quantization, RoPE and append launches)."""
+    kernels and the SiLU·up rows passed to the down projection as a grouped code (2..16: the Q/K/V
+    projection in one K wave group, 17..64 in two); 65..256 the pipelined GEMMs split over K, with
+    the same fused reduce steps; above 256 the unfused path (separate RMSNorm/quantization, RoPE and
+    append launches)."""
     from work_llm_accelerator_amd.model import FLAG_NO_BF16_ROUND, MODE_FAST, DeviceModel
 
     rng = np.random.default_rng(batch)
