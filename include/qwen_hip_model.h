@@ -113,6 +113,21 @@ int qwen_hip_model_prefill(qwen_hip_model* m, int mode, int batch, int seq_len, 
 int qwen_hip_model_prefill_chunk(qwen_hip_model* m, int mode, int batch, int seq_len, int past, float* hidden,
                                  float* k_cache, float* v_cache, uint64_t seq_stride, uint64_t layer_stride);
 
+/* The two step functions above over layers first_layer..first_layer+layer_count-1 only, with the same
+ * arguments and semantics; k_cache / v_cache hold the caches of those layers (layer first_layer+i at
+ * i*layer_stride floats).  hidden is the input of layer first_layer and receives the output of the
+ * range's last layer (bf16-rounded after every layer unless QWEN_FLAG_NO_BF16_ROUND).  Inside a range
+ * FAST fuses each layer boundary (the next layer's RMSNorm and quantization run in the down
+ * projection's reduce step); at the range's ends they run as steps of their own.  A caller can inspect
+ * or replace the hidden state between layers, e.g. to compare two modes layer by layer on the same
+ * inputs. */
+int qwen_hip_model_decode_layers(qwen_hip_model* m, int mode, int first_layer, int layer_count, int batch,
+                                 float* hidden, const int* positions, int max_keys, float* k_cache, float* v_cache,
+                                 uint64_t seq_stride, uint64_t layer_stride);
+int qwen_hip_model_prefill_layers(qwen_hip_model* m, int mode, int first_layer, int layer_count, int batch,
+                                  int seq_len, int past, float* hidden, float* k_cache, float* v_cache,
+                                  uint64_t seq_stride, uint64_t layer_stride);
+
 /* Embedding lookup from the model's bf16 table: hidden[i] = fp32(table[token_ids[i]]) (ids outside
  * [0, vocab) read row 0).  token_ids and hidden are device pointers. */
 int qwen_hip_model_embed(qwen_hip_model* m, const int* token_ids, int count, float* hidden);
@@ -138,7 +153,8 @@ int qwen_hip_model_logits(qwen_hip_model* m, const float* hidden, int count, flo
 int qwen_hip_model_greedy(qwen_hip_model* m, const float* hidden, int count, int* token_ids);
 
 /* Re-runs one kernel of the most recent decode/prefill call `reps` times in isolation, on the
- * model's stream between two HIP events, with that call's shapes and the weights of `layer`;
+ * model's stream between two HIP events, with that call's shapes and the weights of `layer` (one of
+ * that call's layers);
  * *avg_ms receives the mean duration of one launch (the decode attention takes the layers' caches in
  * turn from `layer` on, so that no launch re-reads rows a recent launch left in the last-level cache,
  * as in a decode step).  The re-run reads that call's positions and K/V

@@ -12,9 +12,11 @@
   sum).
 * 28-layer greedy generation, batch 1, a 512-token prompt then 128 decode steps (synthetic model seed
   2): layer 0 of the prefill and of the first decode step against the oracle (ORDERED bit for bit,
-  FAST within FAST_TOL); the head of the first step against the oracle; every greedy id equal to the
-  argmax of the same mode's logits; FAST fed ORDERED's token trajectory (teacher forcing), with and
-  without the driver's bf16 rounding between layers.
+  FAST within FAST_TOL); the head of the first step against the oracle; greedy loops of both modes
+  (each step embeds the id the run chose at the step before, on the device) and runs fed a fixed
+  sequence of uniform random ids; every id equal to the argmax of the same run's logits; FAST against
+  ORDERED end to end over the random ids, with and without the driver's bf16 rounding between layers.
+  Every layer of these workloads is checked on its own, teacher-forced, in tests/test_gpu_layerwise.py.
 
 Tolerances:
   FAST_TOL = 1e-3 (max |y - y_ref| / max |y_ref| per tensor): one layer, fp32 output (no bf16
@@ -250,7 +252,8 @@ def test_greedy_28_layers_prompt512_128_steps(torch):
     from work_llm_accelerator_amd.model import (FLAG_NO_BF16_ROUND, MODE_FAST, MODE_ORDERED, DeviceModel,
                                                 KvCache)
 
-    print("greedy 28 layers (seed 2): 512-token prompt + 128 teacher-forced steps, FAST vs ORDERED", flush=True)
+    print("greedy 28 layers (seed 2): 512-token prompt + 128 steps (greedy loops, and fixed random ids), FAST vs ORDERED",
+          flush=True)
     m = DeviceModel(28, synthetic_seed=2)
     vocab = m.vocab
     positions = PROMPT3 + STEPS3 + 1
@@ -269,11 +272,14 @@ def test_greedy_28_layers_prompt512_128_steps(torch):
         x_pert[0, 0, 7] = x_pert[0, 0, 7] * (1.0 + 2.0 ** -7)  # one element of the first prompt token, one ulp
         x_pert2 = x0.clone()
         x_pert2[0, 0, 1000] = x_pert2[0, 0, 1000] * (1.0 + 2.0 ** -7)
+        # a fixed sequence of uniform random ids, fed to every "rand" run (teacher forcing with varying ids)
+        rand_ids = torch.from_numpy(np.random.default_rng(2).integers(0, vocab, STEPS3).astype(np.int32)).cuda()
         NR = FLAG_NO_BF16_ROUND
-        for name, mode, x in (("ordered", MODE_ORDERED, x0), ("fast", MODE_FAST, x0), ("pert", MODE_ORDERED, x_pert),
-                              ("pert2", MODE_ORDERED, x_pert2), ("ordered_nr", MODE_ORDERED | NR, x0),
-                              ("fast_nr", MODE_FAST | NR, x0), ("pert_nr", MODE_ORDERED | NR, x_pert),
-                              ("pert2_nr", MODE_ORDERED | NR, x_pert2)):
+        for name, mode, x in (("ordered", MODE_ORDERED, x0), ("fast", MODE_FAST, x0),
+                              ("ordered_rand", MODE_ORDERED, x0), ("fast_rand", MODE_FAST, x0),
+                              ("pert_rand", MODE_ORDERED, x_pert), ("pert2_rand", MODE_ORDERED, x_pert2),
+                              ("ordered_rand_nr", MODE_ORDERED | NR, x0), ("fast_rand_nr", MODE_FAST | NR, x0),
+                              ("pert_rand_nr", MODE_ORDERED | NR, x_pert), ("pert2_rand_nr", MODE_ORDERED | NR, x_pert2)):
             cache = KvCache.allocate(28, 1, positions)
             hp = x.clone()
             m.prefill(mode, hp, cache)
@@ -282,12 +288,16 @@ def test_greedy_28_layers_prompt512_128_steps(torch):
             first = torch.empty(1, dtype=torch.int32, device="cuda")
             h = torch.empty(1, HIDDEN, dtype=torch.float32, device="cuda")
             m.greedy(hp[0, PROMPT3 - 1:], first)  # the prompt's next token starts the loop
-            # teacher forcing: every other run is fed ORDERED's tokens (step i embeds the id ORDERED chose at
-            # step i-1); every operation below is queued on the model's stream, in order
-            src_first = first if name == "ordered" else runs["ordered"]["first"]
-            src_ids = ids if name == "ordered" else runs["ordered"]["ids"]
+            # "ordered" and "fast" are greedy loops (step i embeds the id the same run chose at step i-1, on the
+            # device); the "rand" runs embed rand_ids[i] at step i; every operation is queued on the model's
+            # stream, in order
+            rand = "rand" in name
             for i in range(STEPS3):
-                m.embed(src_first if i == 0 else src_ids[i - 1:i], h, order=False)
+                if rand:
+                    src = rand_ids[i:i + 1]
+                else:
+                    src = first if i == 0 else ids[i - 1:i]
+                m.embed(src, h, order=False)
                 m.decode(mode, h, pos_all[i:i + 1], positions, cache, order=False)
                 m.logits(h, logits[i:i + 1], order=False)
                 m.greedy(h, ids[i:i + 1], order=False)
@@ -336,25 +346,25 @@ def test_greedy_28_layers_prompt512_128_steps(torch):
                     assert rel_err(g1, out0) <= FAST_TOL, rel_err(g1, out0)
         finally:
             m1.close()
-        # first decode step, layer 0: K/V row 512 from the embedded first generated token
-        tok = runs["ordered"]["first"]
-        e = torch.empty(1, HIDDEN, dtype=torch.float32, device="cuda")
-        m.embed(tok, e)
-        m.synchronize()
-        kd = np.zeros((PROMPT3 + 1) * KV_WIDTH, np.float32)
-        vd = np.zeros((PROMPT3 + 1) * KV_WIDTH, np.float32)
-        kd[:PROMPT3 * KV_WIDTH] = kc
-        vd[:PROMPT3 * KV_WIDTH] = vc
-        outd = np.zeros(HIDDEN, np.float32)
-        assert o.oracle_decode_layer_block(e.cpu().numpy().reshape(-1), PROMPT3, w0, s0, kd, vd, outd) == 0
+        # first decode step, layer 0: K/V row 512 from each greedy loop's own first generated token (the new
+        # row depends only on the embedded token)
         for name, r in ((n, runs[n]) for n in ("ordered", "fast")):
+            e = torch.empty(1, HIDDEN, dtype=torch.float32, device="cuda")
+            m.embed(r["first"], e)
+            m.synchronize()
+            kd = np.zeros((PROMPT3 + 1) * KV_WIDTH, np.float32)
+            vd = np.zeros((PROMPT3 + 1) * KV_WIDTH, np.float32)
+            kd[:PROMPT3 * KV_WIDTH] = kc
+            vd[:PROMPT3 * KV_WIDTH] = vc
+            outd = np.zeros(HIDDEN, np.float32)
+            assert o.oracle_decode_layer_block(e.cpu().numpy().reshape(-1), PROMPT3, w0, s0, kd, vd, outd) == 0
             gk = r["cache"].k[0, 0, PROMPT3].cpu().numpy()
             gv = r["cache"].v[0, 0, PROMPT3].cpu().numpy()
             rk, rv = kd[PROMPT3 * KV_WIDTH:], vd[PROMPT3 * KV_WIDTH:]
             if name == "ordered":
                 assert bits_equal(gk, rk) and bits_equal(gv, rv), "ORDERED layer-0 decode K/V row 512"
             else:
-                assert rel_err(gk, rk) <= FAST_TOL and rel_err(gv, rv) <= FAST_TOL
+                assert rel_err(gk, rk) <= FAST_TOL and rel_err(gv, rv) <= FAST_TOL, (rel_err(gk, rk), rel_err(gv, rv))
 
         # the head of the first step against the oracle (final RMSNorm + tied bf16 lm_head over the vocab)
         embed = np.zeros((vocab, HIDDEN), np.uint16)
@@ -368,28 +378,28 @@ def test_greedy_28_layers_prompt512_128_steps(torch):
         assert not np.any((ulp > 1) & (np.abs(got0 - ref_logits[0]) > floor)), "head logits of step 0"
         assert np.mean(ulp == 0) >= 0.99
 
-        # FAST against ORDERED (same tokens), against ORDERED's own one-ulp sensitivity, with the driver's
-        # bf16 rounding between layers and without it; where the ids differ, ORDERED's logits of the two ids
-        # are closer than the logit difference (a near-tie)
+        # FAST against ORDERED end to end over the same fixed random ids, against ORDERED's own one-ulp
+        # sensitivity, with the driver's bf16 rounding between layers and without it.  The random-init model
+        # is chaotic over 28 layers, so this bounds the whole chain only loosely; every layer is checked on
+        # its own by tests/test_gpu_layerwise.py.
         for suffix, what in (("", "with the driver's bf16 rounding"), ("_nr", "without rounding")):
-            lo = runs["ordered" + suffix]["logits"].cpu().numpy().astype(np.float64)
-            io = runs["ordered" + suffix]["ids"].cpu().numpy()
+            lo = runs["ordered_rand" + suffix]["logits"].cpu().numpy().astype(np.float64)
+            io = runs["ordered_rand" + suffix]["ids"].cpu().numpy()
 
             def logit_dev(name):
                 lx = runs[name + suffix]["logits"].cpu().numpy().astype(np.float64)
-                dl = np.max(np.abs(lx - lo), axis=1)
-                return dl, float(np.max(dl / np.max(np.abs(lo), axis=1)))
+                return float(np.max(np.max(np.abs(lx - lo), axis=1) / np.max(np.abs(lo), axis=1)))
 
-            dl, worst = logit_dev("fast")
-            cond = max(logit_dev("pert")[1], logit_dev("pert2")[1])
-            jf = runs["fast" + suffix]["ids"].cpu().numpy()
-            diff = np.nonzero(io != jf)[0]
-            for i in diff:
-                gap = lo[i, io[i]] - lo[i, jf[i]]
-                assert gap <= 2.0 * dl[i], f"step {i}: ids {io[i]} vs {jf[i]}: ORDERED gap {gap:.4g} > 2 x {dl[i]:.4g}"
-            print(f"  {what}: logits FAST vs ORDERED worst {worst:.3g} of max; ORDERED vs one-ulp-perturbed ORDERED "
-                  f"{cond:.3g}; ids equal at {STEPS3 - diff.size}/{STEPS3} steps (the rest are near-ties); "
-                  f"{len(set(io.tolist()))} distinct ORDERED ids", flush=True)
+            worst = logit_dev("fast_rand")
+            cond = max(logit_dev("pert_rand"), logit_dev("pert2_rand"))
+            same = int(np.sum(io == runs["fast_rand" + suffix]["ids"].cpu().numpy()))
+            print(f"  {what}, {len(set(rand_ids.cpu().numpy().tolist()))} distinct random ids fed: logits FAST vs "
+                  f"ORDERED worst {worst:.3g} of max; ORDERED vs one-ulp-perturbed ORDERED {cond:.3g}; argmax ids "
+                  f"equal at {same}/{STEPS3} steps", flush=True)
             assert worst <= COND_FACTOR * cond, (what, worst, cond)
+        for name in ("ordered", "fast"):
+            gi = runs[name]["ids"].cpu().numpy()
+            print(f"  {name} greedy loop (own ids fed back): {len(set(gi.tolist()))} distinct ids over {STEPS3} steps",
+                  flush=True)
     finally:
         m.close()

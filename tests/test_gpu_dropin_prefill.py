@@ -64,9 +64,16 @@ def test_attention_mlp_glue_bitexact(lib, layer):
     assert bits_equal(out_glue, out_layer) and bits_equal(kc_glue, kc_layer) and bits_equal(vc_glue, vc_layer)
 
 
-def test_top_wrapper_bitexact_with_scratch(lib, layer):
-    S = 16
-    x = random_hidden(88, S)
+@pytest.mark.parametrize("S", [16, 128])
+def test_top_wrapper_bitexact_with_scratch(lib, layer, S):
+    """The top wrapper (qwen_prefill_host_wrapper.cpp:639-705): S = 16 on the module's layer, and the
+    128-token one-layer prefill workload (seed-1 weights N(0, 0.02) with unit norms, N(0, 1) hidden
+    states, positions 0..127) through the entry it names."""
+    if S == 128:
+        layer = random_layer(seed=1, unit_norms=True)
+        x = random_hidden(1, S)
+    else:
+        x = random_hidden(88, S)
     act = np.zeros(S * HIDDEN * 3, np.float32)
     act[:S * HIDDEN] = x
     kv = np.zeros(S * KV_WIDTH * 2, np.float32)

@@ -70,6 +70,8 @@ EXTRA_SIGNATURES: dict[str, tuple[list, object]] = {
     "qwen_hip_model_decode": ([P, c_int, c_int, P, P, c_int, P, P, c_u64, c_u64], c_int),
     "qwen_hip_model_prefill": ([P, c_int, c_int, c_int, P, P, P, c_u64, c_u64], c_int),
     "qwen_hip_model_prefill_chunk": ([P, c_int, c_int, c_int, c_int, P, P, P, c_u64, c_u64], c_int),
+    "qwen_hip_model_decode_layers": ([P, c_int, c_int, c_int, c_int, P, P, c_int, P, P, c_u64, c_u64], c_int),
+    "qwen_hip_model_prefill_layers": ([P, c_int, c_int, c_int, c_int, c_int, c_int, P, P, P, c_u64, c_u64], c_int),
     "qwen_hip_model_embed": ([P, P, c_int, P], c_int),
     "qwen_hip_model_set_head": ([P, c_int, P, P], c_int),
     "qwen_hip_model_vocab": ([P], c_int),

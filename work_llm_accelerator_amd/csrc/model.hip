@@ -54,6 +54,7 @@ struct DevBuf {
 struct LastCall {
   int kind = 0;  // 0 none, 1 decode, 2 prefill
   int mode = 0, batch = 0, seq_len = 0, max_keys = 0, past = 0;
+  int first = 0, count = 0;  // layers first..first+count-1; their caches start at k_cache / v_cache
   const int* positions = nullptr;
   float *k_cache = nullptr, *v_cache = nullptr;
   uint64_t seq_stride = 0, layer_stride = 0;
@@ -271,8 +272,9 @@ struct qwen_hip_model {
     return g;
   }
 
-  void decode_fast(int B, float* hidden, const int* pos, int max_keys, float* kc0, float* vc0, uint64_t ss,
-                   uint64_t ls, int round, bool pre_reduce = true) {
+  // Layers first..first+count-1; the caches of layer first+i start at kc0/vc0 + i*ls.
+  void decode_fast(int first, int count, int B, float* hidden, const int* pos, int max_keys, float* kc0, float* vc0,
+                   uint64_t ss, uint64_t ls, int round, bool pre_reduce = true) {
     const AttnDecodePlan plan = plan_attn_decode(B, max_keys);
     const Ws w = carve(B, B, plan.nsplit);
     const bool fused = B <= kSplitTokens;
@@ -282,13 +284,14 @@ struct qwen_hip_model {
     // (its prologue-fused form and the separate-launch form stay bit-identical).
     const bool grouped = B >= 2 && B <= kSkinnyTokens;
     GemmArgs down_pending{};                         // the previous layer's deferred down projection
-    for (int l = 0; l < layers; ++l) {
+    for (int i = 0; i < count; ++i) {
+      const int l = first + i;
       const FastLayer& f = fast[l];
-      float* kc = kc0 + (size_t)l * ls;
-      float* vc = vc0 + (size_t)l * ls;
+      float* kc = kc0 + (size_t)i * ls;
+      float* vc = vc0 + (size_t)i * ls;
       // With at most kSplitTokens sequences, RoPE + KV append and the two RMSNorm + quantize steps
       // run inside the split-K reduce kernels of the QKV, O and down projections.
-      if (l == 0 || !fused)
+      if (i == 0 || !fused)
         launch_norm_quant(hidden, QWEN_HIDDEN, B, QWEN_HIDDEN, f.ln, kNormDecode, w.xq, w.sx, w.sums, nullptr,
                           stream);
       if (fused) {
@@ -300,7 +303,7 @@ struct qwen_hip_model {
         fq.v_cache = vc;
         fq.seq_stride = ss;
         fq.limit = max_keys;
-        if (one && l > 0) {
+        if (one && i > 0) {
           // the previous layer's down projection left its K-split partials: every block of this
           // projection finishes that row (residual, bf16 rounding, this layer's RMSNorm, quantization)
           const GemmArgs qa = args(w, B, QWEN_HIDDEN, (int)kQkvRows, f.qkv, f.sw_qkv, f.b_qkv, w.qkv, kQkvRows,
@@ -356,7 +359,7 @@ struct qwen_hip_model {
         gemm(w, B, QWEN_HIDDEN, QWEN_INTERMEDIATE, f.gate, f.sw_gate, nullptr, w.s, QWEN_INTERMEDIATE, kEpiSiluMul,
              f.up, f.sw_up, nullptr, 0, 0, grouped ? &gq : nullptr);
       }
-      const bool fuse_next = fused && l + 1 < layers;  // the next layer's input RMSNorm + quantize
+      const bool fuse_next = fused && i + 1 < count;  // the next layer's input RMSNorm + quantize
       fn.norm_w = fuse_next ? fast[l + 1].ln : nullptr;
       if (one) {
         // the SiLU·up row is quantized by every block of the down projection for its own K chunks;
@@ -392,14 +395,14 @@ struct qwen_hip_model {
 
   // FAST prefill of S new tokens per sequence at positions past..past+S-1 (cache rows 0..past-1 hold
   // the earlier tokens of each sequence).
-  void prefill_fast(int B, int S, int past, float* hidden, float* kc0, float* vc0, uint64_t ss, uint64_t ls,
-                    int round) {
+  void prefill_fast(int first, int count, int B, int S, int past, float* hidden, float* kc0, float* vc0, uint64_t ss,
+                    uint64_t ls, int round) {
     const int T = B * S;
     const Ws w = carve(T, 1, 1, attn_prefill_workspace_bytes(past + S, B));
-    for (int l = 0; l < layers; ++l) {
-      const FastLayer& f = fast[l];
-      float* kc = kc0 + (size_t)l * ls;
-      float* vc = vc0 + (size_t)l * ls;
+    for (int i = 0; i < count; ++i) {
+      const FastLayer& f = fast[first + i];
+      float* kc = kc0 + (size_t)i * ls;
+      float* vc = vc0 + (size_t)i * ls;
       launch_norm_quant(hidden, QWEN_HIDDEN, T, QWEN_HIDDEN, f.ln, kNormPrefill, w.xq, w.sx, w.sums, nullptr,
                         stream);
       if (T > kSplitTokens) {
@@ -434,14 +437,14 @@ struct qwen_hip_model {
     QWEN_HIP(hipGetLastError());
   }
 
-  void decode_ordered(int B, float* hidden, const int* pos, int max_keys, float* kc0, float* vc0, uint64_t ss,
-                      uint64_t ls, int round) {
+  void decode_ordered(int first, int count, int B, float* hidden, const int* pos, int max_keys, float* kc0,
+                      float* vc0, uint64_t ss, uint64_t ls, int round) {
     float* att = scratch((size_t)B * QWEN_HIDDEN * 4u);
-    for (int l = 0; l < layers; ++l) {
-      const DevLayer d = dev_layer(l);
+    for (int i = 0; i < count; ++i) {
+      const DevLayer d = dev_layer(first + i);
       arena.reset();
       arena.reserve(decode_workspace_bytes(B));
-      DecodeBatch b{B, pos, rope_decode, false, kc0 + (size_t)l * ls, vc0 + (size_t)l * ls, (size_t)ss, max_keys};
+      DecodeBatch b{B, pos, rope_decode, false, kc0 + (size_t)i * ls, vc0 + (size_t)i * ls, (size_t)ss, max_keys};
       run_decode_attention(d, hidden, b, att, arena, stream);
       run_decode_mlp(d, att, B, hidden, arena, stream);
       if (round) launch_round_bf16(hidden, (size_t)B * QWEN_HIDDEN, stream);
@@ -450,17 +453,17 @@ struct qwen_hip_model {
     QWEN_HIP(hipGetLastError());
   }
 
-  void prefill_ordered(int B, int S, int past, float* hidden, float* kc0, float* vc0, uint64_t ss, uint64_t ls,
-                       int round) {
+  void prefill_ordered(int first, int count, int B, int S, int past, float* hidden, float* kc0, float* vc0,
+                       uint64_t ss, uint64_t ls, int round) {
     float* att = scratch((size_t)S * QWEN_HIDDEN * 4u);
-    for (int l = 0; l < layers; ++l) {
-      const DevLayer d = dev_layer(l);
+    for (int i = 0; i < count; ++i) {
+      const DevLayer d = dev_layer(first + i);
       for (int b = 0; b < B; ++b) {
         float* x = hidden + (size_t)b * S * QWEN_HIDDEN;
         arena.reset();
         arena.reserve(prefill_workspace_bytes(S));
-        run_prefill_attention(d, x, S, past, rope_prefill, kc0 + (size_t)l * ls + (size_t)b * ss,
-                              vc0 + (size_t)l * ls + (size_t)b * ss, att, arena, stream);
+        run_prefill_attention(d, x, S, past, rope_prefill, kc0 + (size_t)i * ls + (size_t)b * ss,
+                              vc0 + (size_t)i * ls + (size_t)b * ss, att, arena, stream);
         run_prefill_mlp(d, att, S, x, arena, stream);
       }
       if (round) launch_round_bf16(hidden, (size_t)B * S * QWEN_HIDDEN, stream);
@@ -615,9 +618,11 @@ int qwen_hip_model_synchronize(qwen_hip_model* m) {
   });
 }
 
-int qwen_hip_model_decode(qwen_hip_model* m, int mode, int batch, float* hidden, const int* positions, int max_keys,
-                          float* k_cache, float* v_cache, uint64_t seq_stride, uint64_t layer_stride) {
+int qwen_hip_model_decode_layers(qwen_hip_model* m, int mode, int first_layer, int layer_count, int batch,
+                                 float* hidden, const int* positions, int max_keys, float* k_cache, float* v_cache,
+                                 uint64_t seq_stride, uint64_t layer_stride) {
   if (!m || !hidden || !positions || !k_cache || !v_cache) return invalid("null argument");
+  if (first_layer < 0 || layer_count <= 0 || first_layer > m->layers - layer_count) return invalid("invalid layer range");
   const int round = (mode & QWEN_FLAG_NO_BF16_ROUND) ? 0 : 1;
   const bool pre_reduce = (mode & QWEN_FLAG_SEPARATE_REDUCE) == 0;
   mode &= ~(QWEN_FLAG_NO_BF16_ROUND | QWEN_FLAG_SEPARATE_REDUCE);
@@ -625,7 +630,7 @@ int qwen_hip_model_decode(qwen_hip_model* m, int mode, int batch, float* hidden,
     return invalid("invalid decode shape or mode");
   if (mode == QWEN_MODE_FAST && (size_t)batch > kMaxArrivals) return invalid("FAST decode batch above 4096 sequences");
   if (seq_stride < (uint64_t)max_keys * QWEN_KV_WIDTH || (batch > 1 && layer_stride < (uint64_t)batch * seq_stride) ||
-      (m->layers > 1 && layer_stride == 0))
+      (layer_count > 1 && layer_stride == 0))
     return invalid("KV strides too small for max_keys / batch");
   std::lock_guard<std::mutex> lock(m->mu);
   return guarded_model([&]() -> int {
@@ -636,18 +641,29 @@ int qwen_hip_model_decode(qwen_hip_model* m, int mode, int batch, float* hidden,
     if (mode == QWEN_MODE_FAST && sp && std::atoi(sp) > 0)
       throw std::runtime_error("QWEN_SPLIT_CUS: the CU-masked split decode was removed");
     if (mode == QWEN_MODE_FAST)
-      m->decode_fast(batch, hidden, positions, max_keys, k_cache, v_cache, seq_stride, layer_stride, round,
-                     pre_reduce);
+      m->decode_fast(first_layer, layer_count, batch, hidden, positions, max_keys, k_cache, v_cache, seq_stride,
+                     layer_stride, round, pre_reduce);
     else
-      m->decode_ordered(batch, hidden, positions, max_keys, k_cache, v_cache, seq_stride, layer_stride, round);
-    m->last = LastCall{1, mode, batch, 1, max_keys, 0, positions, k_cache, v_cache, seq_stride, layer_stride};
+      m->decode_ordered(first_layer, layer_count, batch, hidden, positions, max_keys, k_cache, v_cache, seq_stride,
+                        layer_stride, round);
+    m->last = LastCall{1, mode, batch, 1, max_keys, 0, first_layer, layer_count, positions, k_cache, v_cache,
+                       seq_stride, layer_stride};
     return QWEN_OK;
   });
 }
 
-int qwen_hip_model_prefill_chunk(qwen_hip_model* m, int mode, int batch, int seq_len, int past, float* hidden,
-                                 float* k_cache, float* v_cache, uint64_t seq_stride, uint64_t layer_stride) {
+int qwen_hip_model_decode(qwen_hip_model* m, int mode, int batch, float* hidden, const int* positions, int max_keys,
+                          float* k_cache, float* v_cache, uint64_t seq_stride, uint64_t layer_stride) {
+  if (!m) return invalid("null argument");
+  return qwen_hip_model_decode_layers(m, mode, 0, m->layers, batch, hidden, positions, max_keys, k_cache, v_cache,
+                                      seq_stride, layer_stride);
+}
+
+int qwen_hip_model_prefill_layers(qwen_hip_model* m, int mode, int first_layer, int layer_count, int batch,
+                                  int seq_len, int past, float* hidden, float* k_cache, float* v_cache,
+                                  uint64_t seq_stride, uint64_t layer_stride) {
   if (!m || !hidden || !k_cache || !v_cache) return invalid("null argument");
+  if (first_layer < 0 || layer_count <= 0 || first_layer > m->layers - layer_count) return invalid("invalid layer range");
   const int round = (mode & QWEN_FLAG_NO_BF16_ROUND) ? 0 : 1;
   mode &= ~QWEN_FLAG_NO_BF16_ROUND;
   if (batch <= 0 || seq_len <= 0 || past < 0 || past > QWEN_MAX_SEQ - seq_len || seq_len > QWEN_MAX_SEQ ||
@@ -655,18 +671,27 @@ int qwen_hip_model_prefill_chunk(qwen_hip_model* m, int mode, int batch, int seq
     return invalid("invalid prefill shape, past length or mode");
   const uint64_t rows = (uint64_t)past + (uint64_t)seq_len;
   if (seq_stride < rows * QWEN_KV_WIDTH || (batch > 1 && layer_stride < (uint64_t)batch * seq_stride) ||
-      (m->layers > 1 && layer_stride == 0))
+      (layer_count > 1 && layer_stride == 0))
     return invalid("KV strides too small for past + seq_len / batch");
   std::lock_guard<std::mutex> lock(m->mu);
   return guarded_model([&]() -> int {
     if (mode == QWEN_MODE_FAST)
-      m->prefill_fast(batch, seq_len, past, hidden, k_cache, v_cache, seq_stride, layer_stride, round);
+      m->prefill_fast(first_layer, layer_count, batch, seq_len, past, hidden, k_cache, v_cache, seq_stride,
+                      layer_stride, round);
     else
-      m->prefill_ordered(batch, seq_len, past, hidden, k_cache, v_cache, seq_stride, layer_stride, round);
-    m->last = LastCall{2, mode, batch, seq_len, past + seq_len, past, nullptr, k_cache, v_cache, seq_stride,
-                       layer_stride};
+      m->prefill_ordered(first_layer, layer_count, batch, seq_len, past, hidden, k_cache, v_cache, seq_stride,
+                         layer_stride, round);
+    m->last = LastCall{2, mode, batch, seq_len, past + seq_len, past, first_layer, layer_count, nullptr, k_cache,
+                       v_cache, seq_stride, layer_stride};
     return QWEN_OK;
   });
+}
+
+int qwen_hip_model_prefill_chunk(qwen_hip_model* m, int mode, int batch, int seq_len, int past, float* hidden,
+                                 float* k_cache, float* v_cache, uint64_t seq_stride, uint64_t layer_stride) {
+  if (!m) return invalid("null argument");
+  return qwen_hip_model_prefill_layers(m, mode, 0, m->layers, batch, seq_len, past, hidden, k_cache, v_cache,
+                                       seq_stride, layer_stride);
 }
 
 int qwen_hip_model_prefill(qwen_hip_model* m, int mode, int batch, int seq_len, float* hidden, float* k_cache,
@@ -738,20 +763,21 @@ int qwen_hip_model_time_kernel(qwen_hip_model* m, int kernel, int layer, int rep
   const bool decode = c.kind == 1;
   if ((kernel == QWEN_KERNEL_ATTN_DECODE && !decode) || (kernel == QWEN_KERNEL_ATTN_PREFILL && decode))
     return invalid("kernel does not belong to the last call");
+  if (layer < c.first || layer >= c.first + c.count) return invalid("layer outside the last call's layer range");
   return guarded_model([&]() -> int {
     const int T = c.batch * c.seq_len;
     const AttnDecodePlan plan = plan_attn_decode(decode ? c.batch : 1, c.max_keys);
     const qwen_hip_model::Ws w = m->carve(T, decode ? c.batch : 1, decode ? plan.nsplit : 1,
                                           decode ? 0 : attn_prefill_workspace_bytes(c.max_keys, c.batch));
     const FastLayer& f = m->fast[layer];
-    float* kc = c.k_cache + (size_t)layer * c.layer_stride;
-    float* vc = c.v_cache + (size_t)layer * c.layer_stride;
+    float* kc = c.k_cache + (size_t)(layer - c.first) * c.layer_stride;
+    float* vc = c.v_cache + (size_t)(layer - c.first) * c.layer_stride;
     int rep = 0;
     auto once = [&]() {
-      // the decode attention reads layer (layer + rep) % layers: each launch streams KV rows that no recent
-      // launch has read, as in a decode step (re-reading one layer's rows would be served partly from the
-      // 256 MB last-level cache)
-      const size_t la = (size_t)((layer + rep++) % m->layers) * c.layer_stride;
+      // the decode attention reads the caches of the call's layers in turn, starting at `layer`: each launch
+      // streams KV rows that no recent launch has read, as in a decode step (re-reading one layer's rows would
+      // be served partly from the 256 MB last-level cache)
+      const size_t la = (size_t)((layer - c.first + rep++) % c.count) * c.layer_stride;
       switch (kernel) {
         case QWEN_KERNEL_ATTN_DECODE:
           launch_attn_decode(w.qkv, (int)kQkvRows, c.k_cache + la, c.v_cache + la, c.seq_stride, c.positions,

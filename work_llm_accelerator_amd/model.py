@@ -113,24 +113,47 @@ class DeviceModel:
         ev.record(torch.cuda.current_stream())
         self.stream.wait_event(ev)
 
-    def decode(self, mode: int, hidden, positions, max_keys: int, cache: KvCache, order: bool = True) -> None:
-        """hidden [B,1536] fp32 (in/out), positions [B] int32 on the GPU."""
+    def _range(self, cache: KvCache, layers) -> tuple[int, int, int]:
+        """(first layer, layer count, cache offset in floats) of a `layers` range: None for every layer,
+        an int for one layer, or (first, count).  A cache of fewer layers than the model holds the
+        range's own layers from its layer 0; a whole-model cache holds every layer."""
+        if layers is None:
+            first, count = 0, self.layers
+        elif isinstance(layers, int):
+            first, count = layers, 1
+        else:
+            first, count = int(layers[0]), int(layers[1])
+        if cache.layers == self.layers:
+            return first, count, first * cache.layer_stride
+        if cache.layers < count:
+            raise ValueError(f"cache holds {cache.layers} layers, the range {count}")
+        return first, count, 0
+
+    def decode(self, mode: int, hidden, positions, max_keys: int, cache: KvCache, order: bool = True,
+               layers=None) -> None:
+        """hidden [B,1536] fp32 (in/out), positions [B] int32 on the GPU; `layers` as in _range."""
         if order:
             self._enter()
         B = hidden.shape[0]
-        st = self.lib.qwen_hip_model_decode(self.handle, mode, B, _ptr(hidden), _ptr(positions), int(max_keys),
-                                            _ptr(cache.k), _ptr(cache.v), cache.seq_stride, cache.layer_stride)
-        _check(self.lib, st, "qwen_hip_model_decode")
+        first, count, off = self._range(cache, layers)
+        st = self.lib.qwen_hip_model_decode_layers(self.handle, mode, first, count, B, _ptr(hidden), _ptr(positions),
+                                                   int(max_keys), ctypes.c_void_p(cache.k.data_ptr() + 4 * off),
+                                                   ctypes.c_void_p(cache.v.data_ptr() + 4 * off), cache.seq_stride,
+                                                   cache.layer_stride)
+        _check(self.lib, st, "qwen_hip_model_decode_layers")
 
-    def prefill(self, mode: int, hidden, cache: KvCache, order: bool = True, past: int = 0) -> None:
+    def prefill(self, mode: int, hidden, cache: KvCache, order: bool = True, past: int = 0, layers=None) -> None:
         """hidden [B,S,1536] fp32 (in/out) at positions past..past+S-1; cache rows past..past+S-1 of
-        sequences 0..B-1 are written (rows 0..past-1 hold the earlier tokens)."""
+        sequences 0..B-1 are written (rows 0..past-1 hold the earlier tokens); `layers` as in _range."""
         if order:
             self._enter()
         B, S = hidden.shape[0], hidden.shape[1]
-        st = self.lib.qwen_hip_model_prefill_chunk(self.handle, mode, B, S, int(past), _ptr(hidden), _ptr(cache.k),
-                                                   _ptr(cache.v), cache.seq_stride, cache.layer_stride)
-        _check(self.lib, st, "qwen_hip_model_prefill_chunk")
+        first, count, off = self._range(cache, layers)
+        st = self.lib.qwen_hip_model_prefill_layers(self.handle, mode, first, count, B, S, int(past), _ptr(hidden),
+                                                    ctypes.c_void_p(cache.k.data_ptr() + 4 * off),
+                                                    ctypes.c_void_p(cache.v.data_ptr() + 4 * off), cache.seq_stride,
+                                                    cache.layer_stride)
+        _check(self.lib, st, "qwen_hip_model_prefill_layers")
 
     def embed(self, token_ids, hidden, order: bool = True) -> None:
         if order:
