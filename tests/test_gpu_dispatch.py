@@ -310,3 +310,47 @@ def test_device_prefill_dispatch(torch, lib, images):
     kv_r, act_r = np.zeros(2 * S * KV_WIDTH, np.float32), prefill_act()
     assert run_oracle_prefill([d], w, s, kv_r, act_r) == 1
     assert bits_equal(kvd.cpu().numpy(), kv_r) and bits_equal(actd.cpu().numpy(), act_r)
+
+
+def test_device_decode_dispatch_past_beyond_32768(torch, lib, images):
+    """A position past 32,767 (the length of the model API's decode RoPE table): the reference builds
+    each RoPE row from libm at the position (qwen_decode_attention_kernel.cpp:29-42) and sets no bound,
+    so both device dispatch entry points (the allocating one and qwen_hip_decode_dispatch_layers_noalloc)
+    take per-descriptor host rows too.  Layers 0 and 1 at past 33,000 and 6: both entry points return
+    (0, 2) and equal the reference top wrapper bit for bit."""
+    w, s = images
+    big = 33000
+    k, v = quantized_kv_history(901, big + 1)
+    k[big * KV_WIDTH:] = 0.0
+    v[big * KV_WIDTH:] = 0.0
+    kv_h = np.zeros(2 * (big + 1) * KV_WIDTH + 2 * (PAST + 1) * KV_WIDTH, np.float32)
+    kv_h[:k.size] = k
+    kv_h[k.size:2 * k.size] = v
+    k2, v2 = quantized_kv_history(902, PAST + 1)
+    k2[PAST * KV_WIDTH:] = 0.0
+    v2[PAST * KV_WIDTH:] = 0.0
+    o2 = 2 * k.size
+    kv_h[o2:o2 + k2.size] = k2
+    kv_h[o2 + k2.size:] = v2
+    d0 = replace(L.build_decode_descriptors(big, 0, 0, 0, 0, 0)[0], k_cache_base_addr=0,
+                 v_cache_base_addr=k.size * 4)
+    d1 = replace(L.build_decode_descriptors(PAST, 0, 0, 0, 0, 0)[1], k_cache_base_addr=o2 * 4,
+                 v_cache_base_addr=(o2 + k2.size) * 4)
+    descs = [d0, d1]
+    print(f"device decode dispatch at past {big} and {PAST}: allocating and allocation-free entry points", flush=True)
+    act_h = decode_inputs()
+    kv_r, act_r = kv_h.copy(), act_h.copy()
+    assert run_reference_decode(descs, w, s, kv_r, act_r) == 0
+    wd, sd = torch.from_numpy(w).cuda(), torch.from_numpy(s).cuda()
+    arr = L.to_c_decode(descs)
+    for fn in (lib.qwen_hip_decode_dispatch_layers, lib.qwen_hip_decode_dispatch_layers_noalloc):
+        kvd, actd = torch.from_numpy(kv_h).cuda(), torch.from_numpy(act_h).cuda()
+        torch.cuda.synchronize()
+        done = ctypes.c_int(-1)
+        st = fn(ctypes.cast(arr, ctypes.c_void_p), 2, dptr(wd), dptr(sd), dptr(kvd), dptr(actd), None,
+                ctypes.byref(done))
+        torch.cuda.synchronize()  # the allocation-free entry point returns without synchronizing
+        assert (st, done.value) == (0, 2), abi.last_error(lib)
+        act_g, kv_g = actd.cpu().numpy(), kvd.cpu().numpy()
+        assert bits_equal(act_g, act_r), first_mismatch(act_g, act_r)
+        assert bits_equal(kv_g, kv_r), first_mismatch(kv_g, kv_r)

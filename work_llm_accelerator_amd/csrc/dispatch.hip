@@ -101,20 +101,23 @@ int qwen_hip_decode_dispatch_layers(const qwen_decode_descriptor* dsc, int n, co
   std::lock_guard<std::mutex> lock(rt.mu);
   return guarded_dispatch([&]() -> int {
     const hipStream_t st = static_cast<hipStream_t>(stream);
-    // RoPE rows and arena sized once, before the first launch (growing either frees memory that
-    // queued layers still read)
-    int max_past = 0;
-    for (int i = 0; i < n && decode_descriptor_status(dsc[i]) == QWEN_OK; ++i)
-      max_past = dsc[i].past_seq_len > max_past ? dsc[i].past_seq_len : max_past;
-    if (max_past >= QWEN_MAX_SEQ) throw std::runtime_error("past_seq_len beyond the 32768-position RoPE table");
-    const float* rope = rt.decode_rope(max_past + 1);
+    // Every runnable descriptor's position and RoPE row (host libm, qwen_decode_attention_kernel.cpp:29-42,
+    // as the drop-in top wrapper and the allocation-free entry build them: no table, so no bound on the
+    // position) staged before the first launch; the arena is sized once (growing it would free memory that
+    // queued layers still read), and the layers' intermediates then reuse one workspace in stream order.
+    int runnable = 0;
+    while (runnable < n && decode_descriptor_status(dsc[runnable]) == QWEN_OK) ++runnable;
+    const size_t rows = runnable > 0 ? (size_t)runnable : 1u;
     rt.arena.reset();
-    rt.arena.reserve(decode_workspace_bytes(1) + 4u * QWEN_HIDDEN + 4u * (size_t)n + 8192u);
-    // every descriptor's position staged before the first launch; the layers' intermediates then
-    // reuse one workspace in stream order
-    std::vector<int> pasts((size_t)n);
-    for (int i = 0; i < n; ++i) pasts[i] = dsc[i].past_seq_len;
-    const int* pos_all = stage_in(rt.arena, pasts.data(), (size_t)n, st);
+    rt.arena.reserve(decode_workspace_bytes(1) + 4u * QWEN_HIDDEN + 4u * rows + 512u * rows + 8192u);
+    std::vector<int> pasts(rows, 0);
+    std::vector<float> rope_rows(rows * 128u, 0.0f);
+    for (int i = 0; i < runnable; ++i) {
+      pasts[i] = dsc[i].past_seq_len;
+      decode_rope_row_host(dsc[i].past_seq_len, &rope_rows[(size_t)i * 128u]);
+    }
+    const int* pos_all = stage_in(rt.arena, pasts.data(), rows, st);
+    const float* rope_all = stage_in(rt.arena, rope_rows.data(), rope_rows.size(), st);
     float* att = rt.arena.alloc_n<float>(QWEN_HIDDEN);
     const size_t layer_mark = rt.arena.mark();
     int status = QWEN_OK, done = 0;
@@ -129,7 +132,8 @@ int qwen_hip_decode_dispatch_layers(const qwen_decode_descriptor* dsc, int n, co
       rt.arena.rewind(layer_mark);
       const int* pos_d = pos_all + done;
       const DevLayer L = device_layer(wd, sd, d.layer_weights_base_addr, d.layer_scales_base_addr);
-      DecodeBatch b{1, pos_d, rope, false, kv + d.k_cache_base_addr / 4, kv + d.v_cache_base_addr / 4, 0, past + 1};
+      DecodeBatch b{1, pos_d, rope_all + (size_t)done * 128u, true, kv + d.k_cache_base_addr / 4,
+                    kv + d.v_cache_base_addr / 4, 0, past + 1};
       run_decode_attention(L, act + d.input_token_addr / 4, b, att, rt.arena, st);
       run_decode_mlp(L, att, 1, act + d.output_token_addr / 4, rt.arena, st);
     }

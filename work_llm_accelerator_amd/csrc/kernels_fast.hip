@@ -2799,6 +2799,8 @@ static void launch_gemm_pipe_t(const GemmArgs& a, int splits, hipStream_t st) {
 
 template <int RTW, bool DUAL, int EPI, int NKC, bool ROPE, int KSW = 1, bool GRP = false>
 static void launch_skinny_t(const GemmArgs& a, int rg_count, int splits, hipStream_t st) {
+  // the grouped code's per-group sums are only finished by the split-K partial epilogue
+  if (GRP && splits <= 1) throw std::runtime_error("grouped-code GEMM needs the split-K partial epilogue");
   const int tt = (a.tokens + 15) / 16;
   const int groups = rg_count * splits;
   const int blocks = 8 * tt * ((groups + 7) / 8);
@@ -2855,6 +2857,21 @@ template <int EPI, bool DUAL>
 static void launch_gemm_epi(const GemmArgs& a, hipStream_t st) {
   const int nkc = a.in_dim / kKChunk;
   const int row_tiles = a.out_dim / 16;
+  // The grouped SiLU·up code (gsx/gcorr read by the down projection, gsx_out/gcorr_out written by
+  // gate/up) exists only in the skinny kernels: any other kernel would ignore it, reading the zero
+  // limb sums or leaving the code stale.  Such a call either takes the skinny kernel or fails.
+  const bool grouped_in = a.gsx != nullptr || a.gcorr != nullptr;
+  const bool grouped_out = a.gsx_out != nullptr || a.gcorr_out != nullptr;
+  if (grouped_in || grouped_out) {
+    const bool in_ok = !grouped_in || (!DUAL && a.gsx && a.gcorr && a.in_dim == QWEN_INTERMEDIATE && a.part &&
+                                       a.fuse != kFuseQkvRope);
+    const bool out_ok = !grouped_out || (DUAL && EPI == kEpiSiluMul && a.gsx_out && a.gcorr_out && a.xq_out &&
+                                         a.in_dim == QWEN_HIDDEN);
+    if (!in_ok || !out_ok || !launch_skinny<EPI, DUAL>(a, st))
+      throw std::runtime_error("grouped SiLU·up code outside the skinny GEMM shapes (<= 64 tokens, out_dim a "
+                               "multiple of 64, gate/up writing it or the split-K down projection reading it)");
+    return;
+  }
   if (launch_skinny<EPI, DUAL>(a, st)) return;
   if (a.tokens <= 16) {
     launch_gemm_t<1, 4, EPI, DUAL>(a, st);

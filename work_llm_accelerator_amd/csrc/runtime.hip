@@ -155,23 +155,16 @@ DevLayer stage_layer(Arena& a, const HostLayer& h, hipStream_t st) {
 // ---------------------------------------------------------------------------------------------
 // Executors.  Intermediates come from the arena; sizes in floats per token:
 //   xn 1536, q 1536, k 256, v 256, ctx 1536 (attention);  pn 1536, g/u/s 3*8960 (MLP).
-size_t decode_workspace_bytes(int tokens) { return 2u * decode_workspace_floats(tokens) * sizeof(float) + 16u * 256u; }
-size_t prefill_workspace_bytes(int tokens) { return decode_workspace_bytes(tokens); }
+// The attention and MLP executors each take their own part, so one token's layer needs the sum.
+namespace {
+size_t up64(size_t n) { return (n + 63u) & ~size_t(63u); }
+size_t decode_attention_floats(size_t T) { return 3u * up64(T * QWEN_HIDDEN) + 2u * up64(T * QWEN_KV_WIDTH); }
+size_t decode_mlp_floats(size_t T) { return up64(T * QWEN_HIDDEN) + 3u * up64(T * QWEN_INTERMEDIATE); }
 
-size_t decode_workspace_floats(int tokens) {
-  const size_t T = (size_t)tokens;
-  auto up = [](size_t n) { return (n + 63u) & ~size_t(63u); };
-  return 5u * up(T * QWEN_HIDDEN) + 2u * up(T * QWEN_KV_WIDTH) + 3u * up(T * QWEN_INTERMEDIATE);
-}
-
-DecodeWorkspace carve_decode_workspace(float* base, int tokens) {
-  const size_t T = (size_t)tokens;
-  auto up = [](size_t n) { return (n + 63u) & ~size_t(63u); };
-  DecodeWorkspace w;
-  float* p = base;
+void carve_attention_part(DecodeWorkspace& w, float* p, size_t T) {
   auto take = [&](size_t n) {
     float* r = p;
-    p += up(n);
+    p += up64(n);
     return r;
   };
   w.xn = take(T * QWEN_HIDDEN);
@@ -179,10 +172,38 @@ DecodeWorkspace carve_decode_workspace(float* base, int tokens) {
   w.k = take(T * QWEN_KV_WIDTH);
   w.v = take(T * QWEN_KV_WIDTH);
   w.ctx = take(T * QWEN_HIDDEN);
+}
+
+void carve_mlp_part(DecodeWorkspace& w, float* p, size_t T) {
+  auto take = [&](size_t n) {
+    float* r = p;
+    p += up64(n);
+    return r;
+  };
   w.pn = take(T * QWEN_HIDDEN);
   w.g = take(T * QWEN_INTERMEDIATE);
   w.u = take(T * QWEN_INTERMEDIATE);
   w.s = take(T * QWEN_INTERMEDIATE);
+}
+}  // namespace
+
+// Two arena allocations (attention part, MLP part), each aligned to 256 bytes.
+size_t decode_workspace_bytes(int tokens) { return decode_workspace_floats(tokens) * sizeof(float) + 2u * 256u; }
+// run_prefill_attention's xn, q, ctx and run_prefill_mlp's pn, g, u, s: seven allocations.
+size_t prefill_workspace_bytes(int tokens) {
+  const size_t T = (size_t)tokens;
+  return (4u * T * QWEN_HIDDEN + 3u * T * QWEN_INTERMEDIATE) * sizeof(float) + 7u * 256u;
+}
+
+size_t decode_workspace_floats(int tokens) {
+  return decode_attention_floats((size_t)tokens) + decode_mlp_floats((size_t)tokens);
+}
+
+DecodeWorkspace carve_decode_workspace(float* base, int tokens) {
+  const size_t T = (size_t)tokens;
+  DecodeWorkspace w;
+  carve_attention_part(w, base, T);
+  carve_mlp_part(w, base + decode_attention_floats(T), T);
   return w;
 }
 
@@ -212,12 +233,14 @@ void run_decode_mlp_ws(const DevLayer& L, const float* att, int T, float* out, c
 
 void run_decode_attention(const DevLayer& L, const float* x, const DecodeBatch& b, float* att, Arena& a,
                           hipStream_t st) {
-  const DecodeWorkspace w = carve_decode_workspace(a.alloc_n<float>(decode_workspace_floats(b.tokens)), b.tokens);
+  DecodeWorkspace w{};
+  carve_attention_part(w, a.alloc_n<float>(decode_attention_floats((size_t)b.tokens)), (size_t)b.tokens);
   run_decode_attention_ws(L, x, b, att, w, st);
 }
 
 void run_decode_mlp(const DevLayer& L, const float* att, int T, float* out, Arena& a, hipStream_t st) {
-  const DecodeWorkspace w = carve_decode_workspace(a.alloc_n<float>(decode_workspace_floats(T)), T);
+  DecodeWorkspace w{};
+  carve_mlp_part(w, a.alloc_n<float>(decode_mlp_floats((size_t)T)), (size_t)T);
   run_decode_mlp_ws(L, att, T, out, w, st);
 }
 
