@@ -151,6 +151,8 @@ def cpu_model() -> str:
 
 # ---------------------------------------------------------------------------------------------
 TRAFFIC_PROFILE = ROOT / "profiles" / "attn_decode_b64_kv4096_hbm_traffic.json"
+GREEDY_TRAFFIC = ROOT / "profiles" / "greedy_b1_prompt512_hbm_traffic.json"
+PREFILL_TRAFFIC = ROOT / "profiles" / "prefill_8x2048_hbm_traffic.json"
 
 
 def measured_traffic(batch: int, history: int):
@@ -160,6 +162,14 @@ def measured_traffic(batch: int, history: int):
     if (batch, history) != (64, 4096) or not TRAFFIC_PROFILE.exists():
         return None
     return json.loads(TRAFFIC_PROFILE.read_text())["traffic_bytes_per_launch"]
+
+
+def profiled_traffic(profile: Path, step: str):
+    """HBM bytes per launch of one step of a workload, from its committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (copy-calibrated like measured_traffic); None when the summary is absent."""
+    if not profile.exists():
+        return None
+    return json.loads(profile.read_text())["kernels"][step]["traffic_bytes_per_launch"]
 
 
 def copy_bandwidth(torch, nbytes: int = 1 << 30, reps: int = 5) -> dict:
@@ -317,7 +327,8 @@ def bench_greedy(args, torch, prompt: int, seed: int) -> dict:
     head_bytes = table_bytes + 1536 * 4 + 1536 * 2
     res["roofline"] = {"bound": "hbm", "kernel": "lm_head_row_kernel (with head_norm_kernel and argmax_finalize_kernel)",
                        "achieved": head_bytes / (head_ms * 1e-3) / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                       "frac": head_bytes / (head_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "traffic": None,
+                       "frac": head_bytes / (head_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                       "traffic": profiled_traffic(GREEDY_TRAFFIC, "lm_head (bf16 table)"),
                        "avg_launch_us": head_ms * 1e3, "algorithmic_bytes_per_launch": head_bytes}
     model.close()
     del cache
@@ -365,7 +376,8 @@ def bench_prefill(args, torch, batch: int, seq: int, seed: int) -> dict:
         res["roofline"] = {"bound": "mfma", "kernel": "gemm_i8_pipe_kernel (gate/up + SiLU·up)",
                            "achieved": gu_ops / (gu_ms * 1e-3) / 1e12, "peak": INT8_PEAK_TOPS,
                            "unit": "TOP/s (int8 dense)", "frac": gu_ops / (gu_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS,
-                           "traffic": None, "avg_launch_us": gu_ms * 1e3,
+                           "traffic": profiled_traffic(PREFILL_TRAFFIC, "gate/up + SiLU·up"),
+                           "avg_launch_us": gu_ms * 1e3,
                            "issued_frac": 2 * gu_ops / (gu_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS,
                            "note": "algorithmic ops; the two-limb code issues 2 int8 MFMA products per weight x "
                                    "activation product (issued_frac); MFMA busy cycles from counters in "
