@@ -18,6 +18,7 @@
 #include <hip/hip_runtime.h>
 
 #include <stdexcept>
+#include <type_traits>
 
 #include "kernels.hpp"
 #include "qwen_device_math.hpp"
@@ -73,7 +74,10 @@ __device__ __forceinline__ float silu_prefill_fast(float v) {
   const float s = -v;
   const float t6 = 1.0f + s * (1.0f + s * (0.5f + s * (1.0f / 6.0f + s * (1.0f / 24.0f + s * (1.0f / 120.0f +
                                                                                             s * (1.0f / 720.0f))))));
-  const float e = s < -1.0f ? __expf(s) : t6;
+  // both forms are evaluated and one is selected, so the lanes of a wave do not branch apart (the
+  // hardware exp of the other form is finite or +inf and discarded)
+  const float ex = __expf(s);
+  const float e = s < -1.0f ? ex : t6;
   return v * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
@@ -691,6 +695,18 @@ __device__ __forceinline__ void reg_tie(v4i& r) { asm volatile("" : "+v"(r)); }
 
 constexpr int kRasterGroup = 8;  // token tiles per raster group of the pipelined GEMM
 
+// Epilogue forms of the pipelined GEMM, fixed per kernel instance by the launcher.
+//   kEfPrefillSilu: the SiLU of the gate/up epilogue is the prefill one (silu_prefill_fast); otherwise
+//                   the decode one (silu_decode).
+//   kEfIntSum:      the two limb sums and their zero-point terms are combined in 32-bit integers,
+//                   256 (sum uH - 8 sum H) + (sum uL - 8 sum L) = sum q X, then converted once.  The
+//                   result is exact for in_dim <= kIntSumMaxK (|q X| <= 8 * 32512 per term, so the sum fits
+//                   in int32 and the modular intermediates do not matter), and its one rounding equals
+//                   that of the fp32 form, whose two limb terms are exact before the one fma rounds.
+constexpr int kEfPrefillSilu = 1;
+constexpr int kEfIntSum = 2;
+constexpr int kIntSumMaxK = 8192;
+
 // OWN (one token group of 4 tiles, TW = 1, NT = 4): the token tile a wave loads itself (tile wv) is
 // its accumulator slot 0, and the wave runs half of that slot's MFMAs before the chunk's barrier (its
 // own loads have landed by its own wait), so waves that reach the barrier late are absorbed by matrix
@@ -699,7 +715,8 @@ constexpr int kRasterGroup = 8;  // token tiles per raster group of the pipeline
 // 16 row tiles) holds row tiles h*8 + 2*(w & 1) + {0, 1} and the same + 4 of head h = w >> 1, so that
 // tiles r and r + 2 hold the rotation pairs (p, p + 64) of one head and the epilogue rotates q and k and
 // appends K/V to the cache, as rope_qkv_kernel does after a plain store.
-template <int NT, int RTW, int NBUF, int EPI, bool DUAL, int TW, int WPE = 1, bool OWN = false, bool ROPE = false>
+template <int NT, int RTW, int NBUF, int EPI, bool DUAL, int TW, int WPE = 1, bool OWN = false, bool ROPE = false,
+          int EF = 0>
 __global__ void __launch_bounds__(256 * TW) __attribute__((amdgpu_waves_per_eu(WPE))) gemm_i8_pipe_kernel(GemmArgs a) {
   static_assert(!OWN || (TW == 1 && NT == 4), "own tile first: each of the 4 waves loads one token tile");
   static_assert(!ROPE || (RTW == 4 && TW == 1 && !DUAL && EPI == kEpiStore), "prefill RoPE: 2 heads per block");
@@ -961,6 +978,24 @@ __global__ void __launch_bounds__(256 * TW) __attribute__((amdgpu_waves_per_eu(W
       }
       return;
     }
+    // zero-point term of the int32 form: 256 * (8 sum H) + 8 sum L per token, modulo 2^32
+    uint32_t c8[NT];
+#pragma unroll
+    for (int n = 0; n < NT; ++n) c8[n] = ((uint32_t)sh8[n] << 8) + (uint32_t)sl8[n];
+    auto dequant = [&](int d, int r, int n, int q) -> float {
+      if constexpr ((EF & kEfIntSum) != 0) {
+        const uint32_t x = ((uint32_t)accH[d][r][n][q] << 8) + (uint32_t)accL[d][r][n][q] - c8[n];
+        return (float)(int32_t)x;
+      } else {
+        // fp32 dequantization: the int32 sums are exact; fp32 adds ~2^-24 relative, far inside the
+        // FAST tolerance, at a quarter of the cost of the fp64 form
+        return (float)(accH[d][r][n][q] - sh8[n]) * 256.0f + (float)(accL[d][r][n][q] - sl8[n]);
+      }
+    };
+    // the lane's output rows start at yrow[n] + row0 (one 64-bit product per token, not per store)
+    float* yrow[NT];
+#pragma unroll
+    for (int n = 0; n < NT; ++n) yrow[n] = a.y + (size_t)min(tok[n], a.tokens - 1) * a.y_stride;
 #pragma unroll
     for (int r = 0; r < RTW; ++r) {
       if (rt0 + r >= row_tiles) continue;
@@ -985,15 +1020,10 @@ __global__ void __launch_bounds__(256 * TW) __attribute__((amdgpu_waves_per_eu(W
         }
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          // fp32 dequantization: the int32 sums are exact; fp32 adds ~2^-24 relative, far inside the
-          // FAST tolerance, at a quarter of the cost of the fp64 form
-          const float tot = (float)(accH[0][r][n][q] - sh8[n]) * 256.0f + (float)(accL[0][r][n][q] - sl8[n]);
-          const float v = tot * sxv[n] * sw[r][q];
+          const float v = dequant(0, r, n, q) * sxv[n] * sw[r][q];
           if (EPI == kEpiSiluMul) {
-            const float tot2 =
-                (float)(accH[D - 1][r][n][q] - sh8[n]) * 256.0f + (float)(accL[D - 1][r][n][q] - sl8[n]);
-            const float u = tot2 * sxv[n] * sw2[r][q];
-            const float sg = a.prefill_silu ? silu_prefill_fast(v) : silu_decode(v);
+            const float u = dequant(D - 1, r, n, q) * sxv[n] * sw2[r][q];
+            const float sg = (EF & kEfPrefillSilu) != 0 ? silu_prefill_fast(v) : silu_decode(v);
             out[q] = sg * u;
           } else if (EPI == kEpiResidual) {
             out[q] = (&res[n].x)[q] + v;
@@ -1008,8 +1038,7 @@ __global__ void __launch_bounds__(256 * TW) __attribute__((amdgpu_waves_per_eu(W
         if (EPI == kEpiResidual && a.round_bf16)
 #pragma unroll
           for (int q = 0; q < 4; ++q) out[q] = round_bf16(out[q]);
-        *reinterpret_cast<float4*>(a.y + (size_t)tok[n] * a.y_stride + row0) =
-            make_float4(out[0], out[1], out[2], out[3]);
+        *reinterpret_cast<float4*>(yrow[n] + row0) = make_float4(out[0], out[1], out[2], out[3]);
       }
     }
   };
@@ -2787,8 +2816,23 @@ static void launch_gemm_pipe_t(const GemmArgs& a, int splits, hipStream_t st) {
   const int row_tiles = a.out_dim / 16;
   const int nblk = ((a.tokens + 16 * NT * TW - 1) / (16 * NT * TW)) * ((row_tiles + 4 * RTW - 1) / (4 * RTW));
   const dim3 grid(8 * ((nblk + 7) / 8), 1, splits);
-  hipLaunchKernelGGL((gemm_i8_pipe_kernel<NT, RTW, NBUF, EPI, DUAL, TW, WPE, OWN, ROPE>), grid, dim3(256 * TW), 0, st,
-                     a);
+  // epilogue form: the int32 limb combination where in_dim allows it, and the SiLU the call asks for
+  const bool int_sum = a.in_dim <= kIntSumMaxK;
+  auto go = [&](auto ef) {
+    hipLaunchKernelGGL((gemm_i8_pipe_kernel<NT, RTW, NBUF, EPI, DUAL, TW, WPE, OWN, ROPE, decltype(ef)::value>), grid,
+                       dim3(256 * TW), 0, st, a);
+  };
+  if constexpr (EPI == kEpiSiluMul) {
+    if (a.prefill_silu)
+      int_sum ? go(std::integral_constant<int, kEfPrefillSilu | kEfIntSum>{})
+              : go(std::integral_constant<int, kEfPrefillSilu>{});
+    else
+      int_sum ? go(std::integral_constant<int, kEfIntSum>{}) : go(std::integral_constant<int, 0>{});
+  } else if constexpr (ROPE) {
+    go(std::integral_constant<int, 0>{});  // the RoPE epilogue has its own dequantization
+  } else {
+    int_sum ? go(std::integral_constant<int, kEfIntSum>{}) : go(std::integral_constant<int, 0>{});
+  }
   // K splits, or an epilogue fused into the reduce step, finish in the reduce kernel; the prefill RoPE
   // epilogue is complete in the GEMM itself
   if (!DUAL && !ROPE && (splits > 1 || a.fuse != kFuseNone)) launch_reduce<EPI>(a, splits, st);
