@@ -50,6 +50,11 @@ typedef struct qwen_hip_model qwen_hip_model;
  * reduce + next RMSNorm + quantization (fused into the next layer's Q/K/V).  Same arithmetic, same
  * results; it exists to check the fused forms. */
 #define QWEN_FLAG_SEPARATE_REDUCE 0x200
+/* OR-ed into `mode` (FAST decode of one sequence with at most 1536 keys): run the decode attention as
+ * a launch of its own rather than in the blocks of the Q/K/V projection (the fused form attends over
+ * the history keys there and adds the new key's term in the O projection's merge).  The two forms
+ * round differently; both are within the FAST tolerance.  QWEN_FLAG_SEPARATE_REDUCE implies it. */
+#define QWEN_FLAG_SEPARATE_ATTN 0x400
 
 /* Kernels that qwen_hip_model_time_kernel can re-run in isolation. */
 #define QWEN_KERNEL_ATTN_DECODE 1   /* split-KV decode attention partials (FAST) */

@@ -390,7 +390,7 @@ def test_model_decode_o_reduce_in_gate_up(torch, layers2, model2, past):
     forms must give exactly the same hidden row and K/V cache, over both layers with the driver's
     bf16 rounding, for two calls in a row.  1500 keys: 24 attention splits, so the O blocks' merge
     loads its partials in two batches (16 + 8); its first call is also checked against the oracle."""
-    from work_llm_accelerator_amd.model import FLAG_SEPARATE_REDUCE, MODE_FAST
+    from work_llm_accelerator_amd.model import FLAG_SEPARATE_ATTN, FLAG_SEPARATE_REDUCE, MODE_FAST
 
     print(f"model decode fast O reduce in gate/up past={past}", flush=True)
     if past > 1000:
@@ -404,7 +404,9 @@ def test_model_decode_o_reduce_in_gate_up(torch, layers2, model2, past):
         ref = oracle_decode(layers2, x[0], past, kl, vl)
         assert rel_err(hidden.cpu().numpy()[0], ref) <= FAST_TOL_ROUNDED
     outs = []
-    for flag in (0, FLAG_SEPARATE_REDUCE):
+    # the attention runs as its own launch in both forms (its fusion into Q/K/V rounds differently,
+    # checked by test_model_decode_fused_attention)
+    for flag in (FLAG_SEPARATE_ATTN, FLAG_SEPARATE_REDUCE):
         cache, _, x = decode_setup(torch, 2, [past], max(48, past + 1), seed=61)
         hidden = torch.from_numpy(x).cuda()
         pos = torch.tensor([past], dtype=torch.int32, device="cuda")
@@ -414,3 +416,62 @@ def test_model_decode_o_reduce_in_gate_up(torch, layers2, model2, past):
         outs.append((hidden.cpu().numpy(), cache.k.cpu().numpy(), cache.v.cpu().numpy()))
     for a, b in zip(outs[0], outs[1]):
         assert bits_equal(a.reshape(-1), b.reshape(-1)), first_mismatch(a.reshape(-1), b.reshape(-1))
+
+
+# The two attention forms: |y_fused - y_sep| <= 5e-4 * max|y_sep|.  The context rows differ in the last
+# fp32 bits, which moves a few elements of its two-limb code by one step, so the forms differ by about
+# the code's own rounding (measured on MI355X: up to 9.5e-5, against 1.1e-4 for either vs the oracle).
+FUSED_VS_SEPARATE_TOL = 5e-4
+
+
+@pytest.mark.parametrize("past", [0, 1, 15, 63, 64, 65, 300, 1279])
+def test_model_decode_fused_attention(torch, layers2, model2, past):
+    """One sequence with at most 1280 keys: the decode attention over the history keys runs in the
+    blocks of the Q/K/V projection (one block per query head and 64-key split, its K/V rows staged in
+    LDS) and the O projection's merge adds the new key's term.  Checked against the oracle (one layer
+    without rounding: FAST_TOL; two layers with the driver's rounding, the second layer's Q/K/V blocks
+    also finishing the first layer's down projection: FAST_TOL_ROUNDED) and against the separate
+    attention launch (QWEN_FLAG_SEPARATE_ATTN), which rounds differently: within
+    FUSED_VS_SEPARATE_TOL, with layer 0's new K/V row bit-identical.  The pasts cover no history
+    (0), a partial first split, exact split boundaries (63, 64, 65: the new key opens a split in the
+    separate form) and 20 splits (1279: the most the fused form takes)."""
+    from work_llm_accelerator_amd.model import DeviceModel, FLAG_NO_BF16_ROUND, FLAG_SEPARATE_ATTN, MODE_FAST
+
+    print(f"model decode fused attention past={past}", flush=True)
+    pos = torch.tensor([past], dtype=torch.int32, device="cuda")
+    m1 = DeviceModel(1, layers2[0].weight_ddr, layers2[0].scale_ddr)
+    try:
+        got = {}
+        for flag in (0, FLAG_SEPARATE_ATTN):
+            cache, hist, x = decode_setup(torch, 1, [past], past + 1, seed=71)
+            h = torch.from_numpy(x).cuda()
+            m1.decode(MODE_FAST | FLAG_NO_BF16_ROUND | flag, h, pos, past + 1, cache)
+            m1.synchronize()
+            got[flag] = (h.cpu().numpy()[0], cache.k[0, 0, past].cpu().numpy(), cache.v[0, 0, past].cpu().numpy())
+        kl, vl = [hist[(0, 0)][0].copy()], [hist[(0, 0)][1].copy()]
+        ref = oracle_decode(layers2[:1], x[0], past, kl, vl, rounding=False)
+        e_f, e_s = rel_err(got[0][0], ref), rel_err(got[FLAG_SEPARATE_ATTN][0], ref)
+        d = rel_err(got[0][0], got[FLAG_SEPARATE_ATTN][0])
+        print(f"  one layer: fused {e_f:.3g}, separate {e_s:.3g} of max vs the oracle; fused vs separate {d:.3g}",
+              flush=True)
+        assert e_f <= FAST_TOL and e_s <= FAST_TOL
+        assert d <= FUSED_VS_SEPARATE_TOL
+        for i in (1, 2):
+            assert bits_equal(got[0][i], got[FLAG_SEPARATE_ATTN][i]), first_mismatch(got[0][i], got[FLAG_SEPARATE_ATTN][i])
+    finally:
+        m1.close()
+    got2 = {}
+    for flag in (0, FLAG_SEPARATE_ATTN):
+        cache, hist, x = decode_setup(torch, 2, [past], past + 1, seed=73)
+        h = torch.from_numpy(x).cuda()
+        model2.decode(MODE_FAST | flag, h, pos, past + 1, cache)
+        model2.synchronize()
+        got2[flag] = (h.cpu().numpy()[0], cache.k[0, 0, past].cpu().numpy(), cache.v[0, 0, past].cpu().numpy())
+    kl = [hist[(l, 0)][0].copy() for l in range(2)]
+    vl = [hist[(l, 0)][1].copy() for l in range(2)]
+    ref = oracle_decode(layers2, x[0], past, kl, vl)
+    e_f, e_s = rel_err(got2[0][0], ref), rel_err(got2[FLAG_SEPARATE_ATTN][0], ref)
+    print(f"  two layers: fused {e_f:.3g}, separate {e_s:.3g} of max vs the oracle", flush=True)
+    assert e_f <= FAST_TOL_ROUNDED and e_s <= FAST_TOL_ROUNDED
+    for i in (1, 2):
+        assert bits_equal(got2[0][i], got2[FLAG_SEPARATE_ATTN][i])

@@ -50,7 +50,23 @@ struct AttnMergeArgs {
   int nsplit, chunk, max_keys;
   float* sx_out;  // scale and limb sums of the quantized context row (block 0 writes them)
   int* sums_out;
+  // With the attention fused into the Q/K/V projection (AttnFuseArgs), the partials cover the history
+  // keys only (keys 0..pos-1 when 0 <= pos < max_keys) and the merge adds the new key's own term from
+  // qkv_new, the token's rotated [q | k | v] row (q unscaled; k at + 1536, v at + 1792).
+  const float* qkv_new = nullptr;
 };
+
+// The decode attention of one sequence fused into its Q/K/V projection: block (query head h, split c)
+// computes the head's q row and the attention over history keys [c*chunk, min(end, (c+1)*chunk)),
+// end = pos when 0 <= pos < max_keys (the new key is the O projection's merge's own term), else
+// min(max(pos, 0) + 1, max_keys), written as partials part[h][c][128], pml[h][c] = (m, l).
+struct AttnFuseArgs {
+  float* part = nullptr;
+  float2* pml = nullptr;
+  int nsplit = 0, chunk = 0, max_keys = 0;
+};
+constexpr int kFusedAttnChunk = 64;      // keys per block of the fused attention (its K/V rows sit in LDS)
+constexpr int kFusedAttnMaxSplits = 20;  // at most 248 blocks: one launch wave at one block per CU
 
 struct GemmArgs {
   const uint8_t* wp;    // repacked weights (tile layout)
@@ -126,6 +142,15 @@ bool launch_gemm_i8_preq(const GemmArgs& a, const GemmArgs& pre, hipStream_t st)
 // into its own slice; block 0 writes the row's scale and limb sums to am.sx_out / am.sums_out (= a.sx,
 // a.sums), followed by the reduce step unless a.defer_reduce.  Returns false for other shapes.
 bool launch_gemm_i8_prea(const GemmArgs& a, const AttnMergeArgs& am, hipStream_t st);
+// The fused [q | k | v] projection + RoPE + K/V append of one token (a.fuse == kFuseQkvRope) with the
+// decode attention over the history keys fused in (AttnFuseArgs; af.chunk == kFusedAttnChunk, at most
+// kFusedAttnMaxSplits splits): its partials are merged, with the new key's term, by the O projection
+// (launch_gemm_i8_prea with am.qkv_new set).  _pre: the activation row is `pre`'s unfinished down-projection
+// reduce step (as launch_gemm_i8_pre with kEpiResidual); otherwise a.xq holds the quantized row.
+// Returns false (nothing launched) for other shapes.
+bool launch_gemm_i8_attn(const GemmArgs& a, const AttnFuseArgs& af, hipStream_t st);
+bool launch_gemm_i8_pre_attn(const GemmArgs& a, const GemmArgs& pre, int pre_splits, const AttnFuseArgs& af,
+                             hipStream_t st);
 // Decode (pos given): token t is sequence t at position pos[t].  Prefill (pos null): token t is
 // sequence t / seq_len at position past + t % seq_len.  Positions outside [0, limit) are skipped.
 void launch_rope_qkv(float* qkv, int qkv_stride, const int* pos, int seq_len, int past, int limit, int tokens,

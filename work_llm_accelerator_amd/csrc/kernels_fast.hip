@@ -1188,7 +1188,10 @@ __device__ __forceinline__ void quant_row_slice(const float* __restrict__ x, int
 // weighted sum, then the weighted sum of the split partial rows), followed by quantize_row_lds's
 // quantization of the context row (from registers) into token 0's row of a skinny-GEMM slice (K chunk c at xs + c * chunk_stride).  The
 // partials come from the previous launch, so plain loads see them.  256 threads.
-template <class Issue>
+// NEWKEY (the attention fused into the Q/K/V projection): the partials cover the history keys and the
+// new key is a term of its own, read from am.qkv_new: score s = (q / sqrt(128)) . k, weight exp(s - M)
+// with M the maximum over the splits and s, added to the sum with l = 1 and to the row with v.
+template <bool NEWKEY = false, class Issue>
 __device__ __forceinline__ void attn_merge_quant_slice(const AttnMergeArgs& am, uint8_t* xs, int chunk_stride,
                                                        float* sx_lds, int* sums_lds, bool write_global,
                                                        Issue&& issue) {
@@ -1224,6 +1227,18 @@ __device__ __forceinline__ void attn_merge_quant_slice(const AttnMergeArgs& am, 
     const int i = min((int)threadIdx.x + 256 * u, QWEN_Q_HEADS * nsplit - 1);
     mlv[u] = am.pml[i];  // pml[h][sp] at h * nsplit + sp
   }
+  // NEWKEY: the thread's q, k and v float4s of the new key (head f >> 5, KV head (f >> 5) / 6)
+  float4 nq[2], nk[2], nv[2];
+  if constexpr (NEWKEY) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int f = min((int)threadIdx.x + 256 * u, QWEN_HIDDEN / 4 - 1);
+      const int d4 = 4 * (f & 31), kvo = ((f >> 5) / QWEN_GROUPS) * QWEN_HEAD_DIM + d4;
+      nq[u] = *reinterpret_cast<const float4*>(am.qkv_new + (f >> 5) * QWEN_HEAD_DIM + d4);
+      nk[u] = *reinterpret_cast<const float4*>(am.qkv_new + QWEN_HIDDEN + kvo);
+      nv[u] = *reinterpret_cast<const float4*>(am.qkv_new + QWEN_HIDDEN + QWEN_KV_WIDTH + kvo);
+    }
+  }
   __builtin_amdgcn_sched_barrier(0);
   issue();  // the caller's loads queue behind the partials
   __builtin_amdgcn_sched_barrier(0);
@@ -1237,20 +1252,43 @@ __device__ __forceinline__ void attn_merge_quant_slice(const AttnMergeArgs& am, 
     }
   }
   const int n = min(max(p0, 0) + 1, am.max_keys);
-  const int nc = (n + am.chunk - 1) / am.chunk;  // splits that hold keys (the rest hold stale values)
+  // NEWKEY: the history keys end at p0 when the new key is one of the n keys
+  const bool has_new = NEWKEY && p0 >= 0 && p0 < am.max_keys;
+  const int hist = has_new ? p0 : n;
+  const int nc = (hist + am.chunk - 1) / am.chunk;  // splits that hold keys (the rest hold stale values)
+  __shared__ float s_new[QWEN_Q_HEADS];  // NEWKEY: the new key's score per head, then its merge weight
+  if constexpr (NEWKEY) {
+    constexpr float kScale = 0.08838834764831845f;  // 1/sqrt(128), the scale of the split partials' q
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      if (u == 1 && threadIdx.x >= QWEN_HIDDEN / 4 - 256) break;  // wave-uniform: waves 2, 3 own one float4
+      float sc = (nq[u].x * kScale) * nk[u].x + (nq[u].y * kScale) * nk[u].y + (nq[u].z * kScale) * nk[u].z +
+                 (nq[u].w * kScale) * nk[u].w;
+#pragma unroll
+      for (int o = 1; o < 32; o <<= 1) sc += __shfl_xor(sc, o, 64);  // over the head's 32 lanes
+      if ((threadIdx.x & 31) == 0) s_new[(threadIdx.x + 256 * u) >> 5] = sc;
+    }
+  }
   __syncthreads();
   if (threadIdx.x < QWEN_Q_HEADS) {
     float* mh = ml + threadIdx.x * kAttnMaxSplits * 2;
     float M = -INFINITY;
     for (int sp = 0; sp < nc; ++sp) M = fmaxf(M, mh[2 * sp]);
+    if (has_new) M = fmaxf(M, s_new[threadIdx.x]);
     float L = 0.0f;
     for (int sp = 0; sp < nc; ++sp) {
       const float f = __expf(mh[2 * sp] - M);
       mh[2 * sp] = f;
       L += mh[2 * sp + 1] * f;
     }
+    float fn = 0.0f;
+    if (has_new) {
+      fn = __expf(s_new[threadIdx.x] - M);
+      L += fn;
+    }
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
     for (int sp = 0; sp < nc; ++sp) mh[2 * sp] *= inv;  // merge weight of split sp
+    if (NEWKEY) s_new[threadIdx.x] = fn * inv;         // merge weight of the new key (0 without one)
   }
   __syncthreads();
   float4 out[2] = {make_float4(0.0f, 0.0f, 0.0f, 0.0f), make_float4(0.0f, 0.0f, 0.0f, 0.0f)};
@@ -1269,6 +1307,19 @@ __device__ __forceinline__ void attn_merge_quant_slice(const AttnMergeArgs& am, 
             out[u].z += pv[u][j].z * w;
             out[u].w += pv[u][j].w * w;
           }
+      }
+    }
+  }
+  if constexpr (NEWKEY) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int f = threadIdx.x + 256 * u;
+      if (f < QWEN_HIDDEN / 4) {
+        const float w = s_new[f >> 5];
+        out[u].x += nv[u].x * w;
+        out[u].y += nv[u].y * w;
+        out[u].z += nv[u].z * w;
+        out[u].w += nv[u].w * w;
       }
     }
   }
@@ -1326,12 +1377,23 @@ __device__ __forceinline__ void attn_merge_quant_slice(const AttnMergeArgs& am, 
 // own K chunks; block 0 writes the row's scale and limb sums to pre.sx_out / pre.sums_out.  PRE_ATTN
 // (one token, KSW = 1, the 1536-wide context row): every block merges the decode attention's split
 // partials (am) and quantizes the row into the slice; block 0 writes its scale and limb sums.
+//
+// ATTN (one token, the fused [q | k | v] projection with RoPE, RTW = 2): the decode attention over the
+// history keys runs in the same launch (AttnFuseArgs).  Blocks 0..3 are the k and v heads (rows
+// 1536..2047: RoPE, K/V append); from block 8 on, block (query head h, key split c) computes head h's
+// rows, rotates them and attends over keys [c*chunk, min(pos, (c+1)*chunk)), whose K/V rows it loads
+// into LDS with its weights.  Its partial (m, l, acc[128]) goes to af.part / af.pml; split 0 also stores
+// the q row, which the O projection's merge needs for the new key's term.
 template <int RTW, bool DUAL, int EPI, int NKC, bool ROPE, int KSW, bool PRE, int PRE_EPI = kEpiStore,
-          bool PRE_QUANT = false, bool PRE_ATTN = false, bool GRP = false>
+          bool PRE_QUANT = false, bool PRE_ATTN = false, bool GRP = false, bool ATTN = false, bool NEWKEY = false>
 __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count, int rg_count, int splits,
                                                  const GemmArgs& pre, int pre_splits,
-                                                 const AttnMergeArgs& am = AttnMergeArgs{}) {
+                                                 const AttnMergeArgs& am = AttnMergeArgs{},
+                                                 const AttnFuseArgs& af = AttnFuseArgs{}) {
   constexpr int D = DUAL ? 2 : 1;
+  static_assert(!ATTN || (RTW == 2 && !DUAL && ROPE && KSW == 1 && EPI == kEpiStore && !PRE_QUANT && !PRE_ATTN &&
+                          !GRP && NKC * kKChunk == QWEN_HIDDEN),
+                "ATTN: the one-token [q | k | v] projection with RoPE");
   static_assert(!PRE || (KSW == 1 && NKC * kKChunk == QWEN_HIDDEN), "PRE: one K group over a 1536-wide row");
   static_assert(!PRE_QUANT || (KSW == 1 && !PRE), "PRE_QUANT: one K group");
   static_assert(!PRE_ATTN || (KSW == 1 && !PRE && !PRE_QUANT && NKC * kKChunk == QWEN_HIDDEN),
@@ -1344,19 +1406,52 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   constexpr int KC = NKC / KSW;  // K chunks per wave group
   static_assert(NKC % KSW == 0, "K chunks split evenly over the wave groups");
   static_assert(RTW * D * 8 * 1024 <= NKC * 16 * 256 || KSW == 1, "K-group reduction fits the slice buffer");
-  __shared__ __align__(16) uint8_t xs[NKC * 16 * 256];
+  // The activation slice: K chunk c's 16 token rows of 256 bytes at xs + (16 c + row) * 256 (row r's
+  // 16-byte segments swizzled by ^ r).  ATTN keeps token 0's row alone (chunk c at xs + c * 256): the
+  // MFMAs read it for every column, and the columns of the absent tokens are not stored.
+  constexpr int kXsRows = ATTN ? 1 : 16;
+  constexpr int kXsChunk = kXsRows * 256;
+  __shared__ __align__(16) uint8_t xs[NKC * kXsChunk];
+  // ATTN: the split's K rows (16-byte chunks of key row r at slot chunk ^ (r & 7), so that the score
+  // reads of 8 consecutive lanes, 8 rows at one chunk, fall in 8 distinct bank groups), then its V rows
+  constexpr int kKvRows = ATTN ? kFusedAttnChunk : 1;
+  __shared__ __align__(16) float kv_lds[2 * kKvRows * QWEN_HEAD_DIM];
+  __shared__ __align__(16) float q_lds[ATTN ? QWEN_HEAD_DIM : 4];  // the head's rotated q row x 1/sqrt(128)
+  __shared__ __align__(16) float wacc[ATTN ? 4 * QWEN_HEAD_DIM : 4];  // per wave: acc[128], then m and l
+  __shared__ float wml[ATTN ? 8 : 2];
   const int lane = threadIdx.x & 63;
   const int wave = (threadIdx.x >> 6) & 3;  // row position of the wave
   const int kg = threadIdx.x >> 8;                                  // K group of the wave
   const int g = lane >> 4;
   const int col = lane & 15;
-  const int xcd = blockIdx.x & 7;
-  const int j = blockIdx.x >> 3;
-  const int tt = j % tt_count;
-  const int grp = (j / tt_count) * 8 + xcd;
-  if (grp >= rg_count * splits) return;  // block-uniform: ids past the last group
-  const int rg = grp % rg_count;
-  const int z = grp / rg_count;
+  int rg_b, z_b, tt_b, ks = -1;  // ks: key split of an ATTN query-head block (-1: none)
+  if constexpr (ATTN) {
+    // ids 0..3: the k and v heads; 4..7: none; from 8 on, the six query heads of one (KV head, key split)
+    // pair at ids 8 + 8 (6 (pair / 8) + j) + pair % 8, so that the blocks reading the same K/V rows share
+    // an XCD (block ids are dealt to the 8 XCDs round robin)
+    const int b = blockIdx.x;
+    if (b < 8) {
+      if (b >= 2 * QWEN_KV_HEADS) return;  // block-uniform
+      rg_b = QWEN_Q_HEADS + b;
+    } else {
+      const int id = b - 8, kq = id >> 3;
+      const int pair = (kq / QWEN_GROUPS) * 8 + (id & 7);
+      if (pair >= QWEN_KV_HEADS * af.nsplit) return;  // block-uniform: ids past the last pair
+      ks = pair / QWEN_KV_HEADS;
+      rg_b = (pair % QWEN_KV_HEADS) * QWEN_GROUPS + kq % QWEN_GROUPS;
+    }
+    z_b = 0;
+    tt_b = 0;
+  } else {
+    const int xcd = blockIdx.x & 7;
+    const int j = blockIdx.x >> 3;
+    tt_b = j % tt_count;
+    const int grp = (j / tt_count) * 8 + xcd;
+    if (grp >= rg_count * splits) return;  // block-uniform: ids past the last group
+    rg_b = grp % rg_count;
+    z_b = grp / rg_count;
+  }
+  const int rg = rg_b, z = z_b, tt = tt_b;
   const int nkc_all = a.in_dim / kKChunk;
   const int kc0 = z * NKC;
   const int tok0 = tt * 16;
@@ -1364,7 +1459,18 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   const size_t row_stride_x = (size_t)a.in_dim * 2u;
 
   // activation slice -> LDS: chunk c, rows 4q..4q+3 per load (1 KiB), wave w takes chunks w, w+4KSW, ..
+  // (ATTN: token 0's row of chunks 4j..4j+3 per load, wave w takes j = w, w+4, ..)
   auto issue_slice = [&]() {
+    if constexpr (ATTN) {
+      static_assert(NKC % 4 == 0, "four 256-byte chunk rows per load");
+      for (int j = threadIdx.x >> 6; j < NKC / 4; j += 4) {
+        const uint8_t* src =
+            reinterpret_cast<const uint8_t*>(a.xq) + (size_t)(kc0 + 4 * j + (lane >> 4)) * 256u + (lane & 15) * 16;
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src),
+                                         (__attribute__((address_space(3))) void*)(xs + 4 * j * 256), 16, 0, 0);
+      }
+      return;
+    }
     for (int c = threadIdx.x >> 6; c < NKC; c += 4 * KSW) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -1381,6 +1487,39 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   };
   // decode position of this lane's token (RoPE epilogue), loaded with the weights
   const int P = ROPE ? a.pos[min(tok0 + col, a.tokens - 1)] : 0;
+  // ATTN: end of the history keys (the new key at P joins in the O projection's merge when it is a key
+  // of this step, 0 <= P < max_keys; otherwise the keys are min(max(P, 0) + 1, max_keys) cache rows)
+  auto hist_end = [&]() {
+    const int pu = __builtin_amdgcn_readfirstlane(P);
+    return pu >= 0 && pu < af.max_keys ? pu : min(max(pu, 0) + 1, af.max_keys);
+  };
+  // ATTN: the split's K/V rows of the head's KV head -> LDS, 16 rows per wave, two rows per load.  Every
+  // block issues the same number of loads (the k and v heads and empty splits load row 0, which nobody
+  // reads), so the wave's load counts stay exact; keys past the split's last one reload it (masked).
+  constexpr int kKvLoads = ATTN ? 2 * (kFusedAttnChunk / 4) / 2 : 0;  // per wave: 8 of K, 8 of V
+  auto issue_kv = [&]() {
+    if constexpr (ATTN) {
+      const int t0 = ks * kFusedAttnChunk;
+      const int t1 = min(hist_end(), t0 + kFusedAttnChunk);
+      const bool live = ks >= 0 && t1 > t0;
+      const size_t hoff = (size_t)(ks >= 0 ? rg / QWEN_GROUPS : 0) * QWEN_HEAD_DIM;
+      const int sl = lane & 31;
+#pragma unroll
+      for (int i = 0; i < kFusedAttnChunk / 8; ++i) {
+        const int r0 = 16 * wave + 2 * i;  // LDS rows r0, r0 + 1 (keys t0 + r0, t0 + r0 + 1)
+        const int r = r0 + (lane >> 5);
+        const int key = live ? min(t0 + r, t1 - 1) : 0;
+        const float* krow = a.k_cache + (size_t)key * QWEN_KV_WIDTH + hoff;
+        const float* vrow = a.v_cache + (size_t)key * QWEN_KV_WIDTH + hoff;
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(krow + 4 * (sl ^ (r & 7))),
+                                         (__attribute__((address_space(3))) void*)(kv_lds + r0 * QWEN_HEAD_DIM), 16,
+                                         0, 0);
+        __builtin_amdgcn_global_load_lds(
+            reinterpret_cast<const void*>(vrow + 4 * sl),
+            (__attribute__((address_space(3))) void*)(kv_lds + (kKvRows + r0) * QWEN_HEAD_DIM), 16, 0, 0);
+      }
+    }
+  };
   uint4 wv[RTW][D][KC];
   bool ok[RTW];
   // Row tile of the wave's tile r: rg*4*RTW + wave + 4r.  A gate/up block writing the grouped code
@@ -1477,10 +1616,12 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   auto issue_loads = [&]() {
     issue_weights();
     issue_scalars();
+    issue_kv();
   };
   __shared__ float pre_sx;
   __shared__ int pre_sums[2];
-  if constexpr (PRE_ATTN) attn_merge_quant_slice(am, xs, 16 * 256, &pre_sx, pre_sums, blockIdx.x == 0, issue_loads);
+  if constexpr (PRE_ATTN)
+    attn_merge_quant_slice<NEWKEY>(am, xs, kXsChunk, &pre_sx, pre_sums, blockIdx.x == 0, issue_loads);
   if constexpr (PRE_QUANT) {
     // token 0's row of the slice: K chunks kc0 .. kc0 + NKC - 1 (row 0 of each chunk, unswizzled)
     quant_row_slice<kQuantVecs>(pre.y, pre.in_dim, kc0, NKC, xs, 16 * 256, &pre_sx, pre_sums,
@@ -1491,7 +1632,7 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
     if (threadIdx.x < 64)
       // the O projection's one K group (store epilogue) or the down projection's five splits (residual)
       reduce_norm_quant_row_zb<PRE_EPI, PRE_EPI == kEpiResidual ? 5 : 1>(
-          pre, pre_splits, 0, reinterpret_cast<int8_t*>(xs), 16 * 256, &pre_sx, pre_sums, blockIdx.x == 0, issue_loads);
+          pre, pre_splits, 0, reinterpret_cast<int8_t*>(xs), kXsChunk, &pre_sx, pre_sums, blockIdx.x == 0, issue_loads);
     else
       issue_loads();
   }
@@ -1507,8 +1648,9 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
     issue_scalars();
     issue_slice();
     issue_weights();
+    issue_kv();
     __builtin_amdgcn_sched_barrier(0);  // every load above is in flight before any use
-    wait_vmcnt<RTW * D * KC>();
+    wait_vmcnt<RTW * D * KC + kKvLoads>();
     if (kTab && threadIdx.x < 32) exp_tab[threadIdx.x] = tab_v;
     if (kTab) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the table store lands before the barrier
     __builtin_amdgcn_s_barrier();
@@ -1573,11 +1715,12 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
       __builtin_amdgcn_sched_barrier(0);
       continue;
     }
-    const uint8_t* xr = xs + ((kg * KC + c) * 16 + col) * 256;
-    const v4i bh1 = *reinterpret_cast<const v4i*>(xr + (((2 * g) ^ col) << 4));
-    const v4i bh2 = *reinterpret_cast<const v4i*>(xr + (((2 * g + 1) ^ col) << 4));
-    const v4i bl1 = *reinterpret_cast<const v4i*>(xr + (((8 + 2 * g) ^ col) << 4));
-    const v4i bl2 = *reinterpret_cast<const v4i*>(xr + (((9 + 2 * g) ^ col) << 4));
+    const int colr = ATTN ? 0 : col;  // ATTN: every column reads token 0's row
+    const uint8_t* xr = xs + ((kg * KC + c) * kXsRows + colr) * 256;
+    const v4i bh1 = *reinterpret_cast<const v4i*>(xr + (((2 * g) ^ colr) << 4));
+    const v4i bh2 = *reinterpret_cast<const v4i*>(xr + (((2 * g + 1) ^ colr) << 4));
+    const v4i bl1 = *reinterpret_cast<const v4i*>(xr + (((8 + 2 * g) ^ colr) << 4));
+    const v4i bl2 = *reinterpret_cast<const v4i*>(xr + (((9 + 2 * g) ^ colr) << 4));
 #pragma unroll
     for (int r = 0; r < RTW; ++r)
 #pragma unroll
@@ -1688,7 +1831,7 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
 
   // epilogue: lane holds rows 16*rt + 4g + q (q < 4) of token tok0 + col
   const int tok = tok0 + col;
-  if (tok >= a.tokens) return;
+  if (!ATTN && tok >= a.tokens) return;  // ATTN: every lane goes on to the attention (stores guarded)
   const double sx = (double)(kMade ? pre_sx : sx_l);
   const bool partial = splits > 1 || (!DUAL && !ROPE && a.fuse != kFuseNone);
   if (partial) {
@@ -1755,9 +1898,87 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
                 ? a.k_cache + cache_row + (head - QWEN_Q_HEADS) * QWEN_HEAD_DIM + p0
                 : a.v_cache + cache_row + (head - QWEN_Q_HEADS - QWEN_KV_HEADS) * QWEN_HEAD_DIM + p0;
     }
+    if constexpr (ATTN) {
+      if (head < QWEN_Q_HEADS && tok < a.tokens) {
+        constexpr float kScale = 0.08838834764831845f;  // 1/sqrt(128), as attn_decode_kernel scales q
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          q_lds[p0 + q] = lo[q] * kScale;
+          q_lds[p0 + 64 + q] = hi[q] * kScale;
+        }
+      }
+      if (tok >= a.tokens || ks > 0) dst = nullptr;  // split 0 stores the q row (the merge's new-key term)
+      if (head >= QWEN_Q_HEADS && tok < a.tokens) {  // the k and v rows also go to the token's row
+        float* yr = a.y + (size_t)tok * a.y_stride + head * QWEN_HEAD_DIM + p0;
+        *reinterpret_cast<float4*>(yr) = make_float4(lo[0], lo[1], lo[2], lo[3]);
+        *reinterpret_cast<float4*>(yr + 64) = make_float4(hi[0], hi[1], hi[2], hi[3]);
+      }
+    }
     if (dst) {
       *reinterpret_cast<float4*>(dst) = make_float4(lo[0], lo[1], lo[2], lo[3]);
       *reinterpret_cast<float4*>(dst + 64) = make_float4(hi[0], hi[1], hi[2], hi[3]);
+    }
+    if constexpr (ATTN) {
+      // The attention of query head rg over history keys [t0, t1) of this split (the new key joins in
+      // the O projection's merge).  Wave w takes keys t0 + 16w .. + 15: lane (key k = lane & 15, dim
+      // quarter lane >> 4) forms a quarter of the score, the quarters meet by shuffles; then the wave's
+      // online-softmax state over its 16 keys and P.V for dims 2 lane, 2 lane + 1.
+      // every wave waits for its K/V loads into LDS before it ends, the blocks without keys included
+      wait_vmcnt<0>();
+      if (ks < 0) return;  // the k and v heads
+      const int t0 = ks * kFusedAttnChunk;
+      const int t1 = min(hist_end(), t0 + kFusedAttnChunk);
+      if (t1 <= t0) return;  // block-uniform: no history key in this split
+      __syncthreads();       // every wave's K/V rows and the q row are visible
+      const int kk = lane & 15, qd = lane >> 4;
+      const int r = 16 * wave + kk;
+      const float* krow = kv_lds + r * QWEN_HEAD_DIM;
+      float sc = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int jc = qd * 8 + i;  // 16-byte chunk: dims 4 jc .. 4 jc + 3
+        const float4 k4 = *reinterpret_cast<const float4*>(krow + 4 * (jc ^ (r & 7)));
+        const float4 q4 = *reinterpret_cast<const float4*>(q_lds + 4 * jc);
+        sc += q4.x * k4.x + q4.y * k4.y + q4.z * k4.z + q4.w * k4.w;
+      }
+      sc += __shfl_xor(sc, 16, 64);
+      sc += __shfl_xor(sc, 32, 64);
+      if (t0 + r >= t1) sc = -INFINITY;
+      float m = sc;
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+      const float pr = m == -INFINITY ? 0.0f : __expf(sc - m);  // a wave without keys: weight 0
+      float l = pr;
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) l += __shfl_xor(l, o, 64);
+      float a0 = 0.0f, a1 = 0.0f;
+      const float* vb = kv_lds + (kKvRows + 16 * wave) * QWEN_HEAD_DIM + 2 * lane;
+#pragma unroll
+      for (int k2 = 0; k2 < 16; ++k2) {
+        const float pk = __shfl(pr, k2, 64);  // lane k2 holds key k2's weight
+        const float2 v2 = *reinterpret_cast<const float2*>(vb + k2 * QWEN_HEAD_DIM);
+        a0 += pk * v2.x;
+        a1 += pk * v2.y;
+      }
+      *reinterpret_cast<float2*>(wacc + wave * QWEN_HEAD_DIM + 2 * lane) = make_float2(a0, a1);
+      if (lane == 0) {
+        wml[2 * wave] = m;
+        wml[2 * wave + 1] = l;
+      }
+      __syncthreads();
+      if (threadIdx.x < QWEN_HEAD_DIM) {
+        const int d = threadIdx.x;
+        const float M = fmaxf(fmaxf(wml[0], wml[2]), fmaxf(wml[4], wml[6]));  // finite: key t0 is in wave 0
+        float L = 0.0f, A = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const float f = wml[2 * w] == -INFINITY ? 0.0f : __expf(wml[2 * w] - M);
+          L += wml[2 * w + 1] * f;
+          A += wacc[w * QWEN_HEAD_DIM + d] * f;
+        }
+        af.part[((size_t)rg * af.nsplit + ks) * QWEN_HEAD_DIM + d] = A;
+        if (d == 0) af.pml[(size_t)rg * af.nsplit + ks] = make_float2(M, L);
+      }
     }
   } else {
 #pragma unroll
@@ -1789,10 +2010,25 @@ __global__ void __launch_bounds__(256) gemm_skinny_preq_kernel(GemmArgs a, int r
 }
 
 // One token whose activation row is the decode attention's context: every block merges the split
-// partials and quantizes the row (see PRE_ATTN above).
-template <int RTW, int EPI, int NKC>
+// partials and quantizes the row (see PRE_ATTN above; NEWKEY: with the new key's own term).
+template <int RTW, int EPI, int NKC, bool NEWKEY>
 __global__ void __launch_bounds__(256) gemm_skinny_prea_kernel(GemmArgs a, int rg_count, AttnMergeArgs am) {
-  gemm_skinny_body<RTW, false, EPI, NKC, false, 1, false, kEpiStore, false, true>(a, 1, rg_count, 1, a, 0, am);
+  gemm_skinny_body<RTW, false, EPI, NKC, false, 1, false, kEpiStore, false, true, false, false, NEWKEY>(
+      a, 1, rg_count, 1, a, 0, am);
+}
+
+// One token's fused [q | k | v] projection + RoPE + K/V append with the decode attention over the
+// history keys (see ATTN above); _pre: its activation row is the previous layer's unfinished down
+// projection (see PRE above).
+__global__ void __launch_bounds__(256) gemm_skinny_attn_kernel(GemmArgs a, AttnFuseArgs af) {
+  gemm_skinny_body<2, false, kEpiStore, 12, true, 1, false, kEpiStore, false, false, false, true>(
+      a, 1, QWEN_QKV_ROWS / 128, 1, a, 0, AttnMergeArgs{}, af);
+}
+
+__global__ void __launch_bounds__(256) gemm_skinny_pre_attn_kernel(GemmArgs a, GemmArgs pre, int pre_splits,
+                                                                   AttnFuseArgs af) {
+  gemm_skinny_body<2, false, kEpiStore, 12, true, 1, true, kEpiResidual, false, false, false, true>(
+      a, 1, QWEN_QKV_ROWS / 128, 1, pre, pre_splits, AttnMergeArgs{}, af);
 }
 
 // One token, with the previous projection's reduce step redone by every block (see PRE above).
@@ -2987,9 +3223,42 @@ bool launch_gemm_i8_prea(const GemmArgs& a, const AttnMergeArgs& am, hipStream_t
       am.nsplit > kAttnMaxSplits || am.chunk < 1)
     return false;
   const int rg_count = a.out_dim / 64;
-  hipLaunchKernelGGL((gemm_skinny_prea_kernel<1, kEpiStore, 12>), dim3(8 * ((rg_count + 7) / 8)), dim3(256), 0, st, a,
-                     rg_count, am);
+  if (am.qkv_new)
+    hipLaunchKernelGGL((gemm_skinny_prea_kernel<1, kEpiStore, 12, true>), dim3(8 * ((rg_count + 7) / 8)), dim3(256), 0,
+                       st, a, rg_count, am);
+  else
+    hipLaunchKernelGGL((gemm_skinny_prea_kernel<1, kEpiStore, 12, false>), dim3(8 * ((rg_count + 7) / 8)), dim3(256),
+                       0, st, a, rg_count, am);
   if (!a.defer_reduce) launch_reduce<kEpiStore>(a, 1, st);
+  return true;
+}
+
+// Blocks of the fused Q/K/V + attention launch: ids 0..7 (the four k and v heads, four idle), then 8
+// per six-head group of 8 (KV head, key split) pairs.
+static int fused_attn_blocks(int nsplit) {
+  return 8 + 8 * QWEN_GROUPS * ((QWEN_KV_HEADS * nsplit + 7) / 8);
+}
+
+static bool fused_attn_ok(const GemmArgs& a, const AttnFuseArgs& af) {
+  return a.tokens == 1 && a.in_dim == QWEN_HIDDEN && a.out_dim == QWEN_QKV_ROWS && !a.wp2 &&
+         a.fuse == kFuseQkvRope && a.pos && a.rope && a.k_cache && a.v_cache && a.y && af.part && af.pml &&
+         af.chunk == kFusedAttnChunk && af.nsplit >= 1 && af.nsplit <= kFusedAttnMaxSplits && af.max_keys >= 1 &&
+         af.max_keys <= af.nsplit * af.chunk && a.limit >= 1;
+}
+
+bool launch_gemm_i8_attn(const GemmArgs& a, const AttnFuseArgs& af, hipStream_t st) {
+  if (!fused_attn_ok(a, af) || !a.xq) return false;
+  hipLaunchKernelGGL(gemm_skinny_attn_kernel, dim3(fused_attn_blocks(af.nsplit)), dim3(256), 0, st, a, af);
+  return true;
+}
+
+bool launch_gemm_i8_pre_attn(const GemmArgs& a, const GemmArgs& pre, int pre_splits, const AttnFuseArgs& af,
+                             hipStream_t st) {
+  if (!fused_attn_ok(a, af) || pre.out_dim != QWEN_HIDDEN || pre.fuse != kFuseNormQuant || pre.tokens != 1 ||
+      pre_splits < 1 || pre_splits > kMaxSplits)
+    return false;
+  hipLaunchKernelGGL(gemm_skinny_pre_attn_kernel, dim3(fused_attn_blocks(af.nsplit)), dim3(256), 0, st, a, pre,
+                     pre_splits, af);
   return true;
 }
 

@@ -274,11 +274,21 @@ struct qwen_hip_model {
 
   // Layers first..first+count-1; the caches of layer first+i start at kc0/vc0 + i*ls.
   void decode_fast(int first, int count, int B, float* hidden, const int* pos, int max_keys, float* kc0, float* vc0,
-                   uint64_t ss, uint64_t ls, int round, bool pre_reduce = true) {
+                   uint64_t ss, uint64_t ls, int round, bool pre_reduce = true, bool sep_attn = false) {
     const AttnDecodePlan plan = plan_attn_decode(B, max_keys);
     const Ws w = carve(B, B, plan.nsplit);
     const bool fused = B <= kSplitTokens;
     const bool one = fused && B == 1 && pre_reduce;  // one sequence: reduce steps in the next projection
+    // one sequence with 64-key splits (at most 1536 keys): the attention over the history keys runs in
+    // the Q/K/V projection's blocks, and the O projection's merge adds the new key's term
+    const bool fuse_attn =
+        one && !sep_attn && plan.chunk == kFusedAttnChunk && plan.nsplit <= kFusedAttnMaxSplits;
+    AttnFuseArgs af{};
+    af.part = w.part;
+    af.pml = w.pml;
+    af.nsplit = plan.nsplit;
+    af.chunk = plan.chunk;
+    af.max_keys = max_keys;
     // 2..64 sequences: the gate/up projection quantizes its SiLU·up rows per 64-row group for the down
     // projection (no separate quantization launch).  One sequence keeps the row code in both forms
     // (its prologue-fused form and the separate-launch form stay bit-identical).
@@ -308,8 +318,13 @@ struct qwen_hip_model {
           // projection finishes that row (residual, bf16 rounding, this layer's RMSNorm, quantization)
           const GemmArgs qa = args(w, B, QWEN_HIDDEN, (int)kQkvRows, f.qkv, f.sw_qkv, f.b_qkv, w.qkv, kQkvRows,
                                    nullptr, nullptr, nullptr, 0, 0, &fq);
-          if (!launch_gemm_i8_pre(qa, down_pending, kEpiResidual, 5, stream))
+          if (fuse_attn ? !launch_gemm_i8_pre_attn(qa, down_pending, 5, af, stream)
+                        : !launch_gemm_i8_pre(qa, down_pending, kEpiResidual, 5, stream))
             throw std::runtime_error("Q/K/V with the down reduce: bad shape");
+        } else if (fuse_attn) {
+          const GemmArgs qa = args(w, B, QWEN_HIDDEN, (int)kQkvRows, f.qkv, f.sw_qkv, f.b_qkv, w.qkv, kQkvRows,
+                                   nullptr, nullptr, nullptr, 0, 0, &fq);
+          if (!launch_gemm_i8_attn(qa, af, stream)) throw std::runtime_error("Q/K/V with the attention: bad shape");
         } else {
           gemm(w, B, QWEN_HIDDEN, (int)kQkvRows, f.qkv, f.sw_qkv, f.b_qkv, w.qkv, kQkvRows, kEpiStore, nullptr,
                nullptr, nullptr, 0, 0, &fq);
@@ -319,8 +334,9 @@ struct qwen_hip_model {
         launch_rope_qkv(w.qkv, (int)kQkvRows, pos, 1, 0, max_keys, B, rope_decode, kc, vc, ss, stream);
       }
       // one sequence: the attention leaves its split partials, merged by every block of the O projection
-      launch_attn_decode(w.qkv, (int)kQkvRows, kc, vc, ss, pos, B, max_keys, plan, w.part, w.pml, w.arrivals,
-                         nullptr, one ? nullptr : w.xq, w.sx, w.sums, stream);
+      if (!fuse_attn)
+        launch_attn_decode(w.qkv, (int)kQkvRows, kc, vc, ss, pos, B, max_keys, plan, w.part, w.pml, w.arrivals,
+                           nullptr, one ? nullptr : w.xq, w.sx, w.sums, stream);
       GemmArgs fn{};
       fn.fuse = kFuseNormQuant;
       fn.norm = kNormDecode;
@@ -336,7 +352,8 @@ struct qwen_hip_model {
         const GemmArgs oa = args(w, B, QWEN_HIDDEN, QWEN_HIDDEN, f.o, f.sw_o, nullptr, w.att, QWEN_HIDDEN, nullptr,
                                  nullptr, nullptr, 0, 0, &fn);
         fn.defer_reduce = 0;
-        const AttnMergeArgs am{w.part, w.pml, pos, plan.nsplit, plan.chunk, max_keys, w.sx, w.sums};
+        const AttnMergeArgs am{w.part, w.pml, pos, plan.nsplit, plan.chunk, max_keys, w.sx, w.sums,
+                               fuse_attn ? w.qkv : nullptr};
         if (!launch_gemm_i8_prea(oa, am, stream)) throw std::runtime_error("O with the attention merge: bad shape");
         const GemmArgs ga = args(w, B, QWEN_HIDDEN, QWEN_INTERMEDIATE, f.gate, f.sw_gate, nullptr, w.s,
                                  QWEN_INTERMEDIATE, f.up, f.sw_up);
@@ -625,7 +642,8 @@ int qwen_hip_model_decode_layers(qwen_hip_model* m, int mode, int first_layer, i
   if (first_layer < 0 || layer_count <= 0 || first_layer > m->layers - layer_count) return invalid("invalid layer range");
   const int round = (mode & QWEN_FLAG_NO_BF16_ROUND) ? 0 : 1;
   const bool pre_reduce = (mode & QWEN_FLAG_SEPARATE_REDUCE) == 0;
-  mode &= ~(QWEN_FLAG_NO_BF16_ROUND | QWEN_FLAG_SEPARATE_REDUCE);
+  const bool sep_attn = (mode & QWEN_FLAG_SEPARATE_ATTN) != 0;
+  mode &= ~(QWEN_FLAG_NO_BF16_ROUND | QWEN_FLAG_SEPARATE_REDUCE | QWEN_FLAG_SEPARATE_ATTN);
   if (batch <= 0 || max_keys <= 0 || max_keys > QWEN_MAX_SEQ || (mode != QWEN_MODE_ORDERED && mode != QWEN_MODE_FAST))
     return invalid("invalid decode shape or mode");
   if (mode == QWEN_MODE_FAST && (size_t)batch > kMaxArrivals) return invalid("FAST decode batch above 4096 sequences");
@@ -642,7 +660,7 @@ int qwen_hip_model_decode_layers(qwen_hip_model* m, int mode, int first_layer, i
       throw std::runtime_error("QWEN_SPLIT_CUS: the CU-masked split decode was removed");
     if (mode == QWEN_MODE_FAST)
       m->decode_fast(first_layer, layer_count, batch, hidden, positions, max_keys, k_cache, v_cache, seq_stride,
-                     layer_stride, round, pre_reduce);
+                     layer_stride, round, pre_reduce, sep_attn);
     else
       m->decode_ordered(first_layer, layer_count, batch, hidden, positions, max_keys, k_cache, v_cache, seq_stride,
                         layer_stride, round);

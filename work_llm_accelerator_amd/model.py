@@ -21,6 +21,7 @@ MODE_ORDERED = 0
 MODE_FAST = 1
 FLAG_NO_BF16_ROUND = 0x100  # skip the driver's bf16 rounding between layers
 FLAG_SEPARATE_REDUCE = 0x200  # FAST decode of one sequence: the row steps fused into projections as own launches
+FLAG_SEPARATE_ATTN = 0x400  # FAST decode of one sequence: the attention as its own launch (not in the Q/K/V blocks)
 
 KERNEL_ATTN_DECODE = 1
 KERNEL_GEMM_GATE_UP = 2
