@@ -675,6 +675,14 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((VMCNT & 0xF) | (0x7 << 4) | (0xF << 8) | ((VMCNT >> 4) << 14));
 }
 
+// A uniform int read through the scalar cache, waited for with lgkmcnt (the vector loads in flight
+// are not waited for).  p must be uniform across the wave.
+__device__ __forceinline__ int load_uniform_i32(const int* p) {
+  int v;
+  asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p));
+  return v;
+}
+
 // LDS byte address of a pointer into a __shared__ array.
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
@@ -1408,10 +1416,12 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   static_assert(RTW * D * 8 * 1024 <= NKC * 16 * 256 || KSW == 1, "K-group reduction fits the slice buffer");
   // The activation slice: K chunk c's 16 token rows of 256 bytes at xs + (16 c + row) * 256 (row r's
   // 16-byte segments swizzled by ^ r).  ATTN keeps token 0's row alone (chunk c at xs + c * 256): the
-  // MFMAs read it for every column, and the columns of the absent tokens are not stored.
+  // MFMAs read it for every column, and the columns of the absent tokens are not stored.  (Its four
+  // spare chunk slots take wave 3's load, so that every wave issues one: a load under a wave-dependent
+  // branch made the compiler wait for every load in flight at the branch's join.)
   constexpr int kXsRows = ATTN ? 1 : 16;
   constexpr int kXsChunk = kXsRows * 256;
-  __shared__ __align__(16) uint8_t xs[NKC * kXsChunk];
+  __shared__ __align__(16) uint8_t xs[(ATTN ? NKC + 4 : NKC) * kXsChunk];
   // ATTN: the split's K rows (16-byte chunks of key row r at slot chunk ^ (r & 7), so that the score
   // reads of 8 consecutive lanes, 8 rows at one chunk, fall in 8 distinct bank groups), then its V rows
   constexpr int kKvRows = ATTN ? kFusedAttnChunk : 1;
@@ -1462,13 +1472,12 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   // (ATTN: token 0's row of chunks 4j..4j+3 per load, wave w takes j = w, w+4, ..)
   auto issue_slice = [&]() {
     if constexpr (ATTN) {
-      static_assert(NKC % 4 == 0, "four 256-byte chunk rows per load");
-      for (int j = threadIdx.x >> 6; j < NKC / 4; j += 4) {
-        const uint8_t* src =
-            reinterpret_cast<const uint8_t*>(a.xq) + (size_t)(kc0 + 4 * j + (lane >> 4)) * 256u + (lane & 15) * 16;
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src),
-                                         (__attribute__((address_space(3))) void*)(xs + 4 * j * 256), 16, 0, 0);
-      }
+      static_assert(NKC == 12, "three waves of four 256-byte chunk rows, wave 3 into the spare slots");
+      const int j = wave;  // chunks 4j .. 4j + 3 (wave 3: a valid source, the spare slots)
+      const uint8_t* src = reinterpret_cast<const uint8_t*>(a.xq) +
+                           (size_t)(kc0 + min(4 * j + (lane >> 4), NKC - 1)) * 256u + (lane & 15) * 16;
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src),
+                                       (__attribute__((address_space(3))) void*)(xs + 4 * j * 256), 16, 0, 0);
       return;
     }
     for (int c = threadIdx.x >> 6; c < NKC; c += 4 * KSW) {
@@ -1486,7 +1495,17 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
     }
   };
   // decode position of this lane's token (RoPE epilogue), loaded with the weights
-  const int P = ROPE ? a.pos[min(tok0 + col, a.tokens - 1)] : 0;
+  // (ATTN, one token: read through the scalar cache once the weights are in flight, in issue_kv: a
+  // vector load here made the compiler wait for every load in flight before its first use)
+  int P = ROPE && !ATTN ? a.pos[min(tok0 + col, a.tokens - 1)] : 0;
+  // RoPE cos/sin of pairs p = 16*wave + 4g + q, q < 4, at position P (ATTN: loaded in issue_kv, ahead
+  // of the K/V rows; otherwise after the slice barrier, in flight during the MFMAs)
+  float4 rc = make_float4(1.0f, 1.0f, 1.0f, 1.0f), rs = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  auto load_rope = [&]() {
+    const float* rr = a.rope + (size_t)min(max(P, 0), a.limit - 1) * 128 + 16 * wave + 4 * g;
+    rc = *reinterpret_cast<const float4*>(rr);
+    rs = *reinterpret_cast<const float4*>(rr + 64);
+  };
   // ATTN: end of the history keys (the new key at P joins in the O projection's merge when it is a key
   // of this step, 0 <= P < max_keys; otherwise the keys are min(max(P, 0) + 1, max_keys) cache rows)
   auto hist_end = [&]() {
@@ -1499,6 +1518,10 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   constexpr int kKvLoads = ATTN ? 2 * (kFusedAttnChunk / 4) / 2 : 0;  // per wave: 8 of K, 8 of V
   auto issue_kv = [&]() {
     if constexpr (ATTN) {
+      // after every other load of the wave: the addresses wait for the position
+      __builtin_amdgcn_sched_barrier(0);
+      P = load_uniform_i32(a.pos);
+      load_rope();
       const int t0 = ks * kFusedAttnChunk;
       const int t1 = min(hist_end(), t0 + kFusedAttnChunk);
       const bool live = ks >= 0 && t1 > t0;
@@ -1638,7 +1661,7 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   }
   if constexpr (kMade) {
     __builtin_amdgcn_sched_barrier(0);  // every load above is in flight before any use
-    wait_vmcnt<0>();
+    wait_vmcnt<kKvLoads>();  // ATTN: the K/V rows (the wave's last loads) land during the MFMAs
     __syncthreads();
   } else {
     // Scalars, then the activation slice, then the weights in chunk order.  A wave's loads return in
@@ -1650,7 +1673,7 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
     issue_weights();
     issue_kv();
     __builtin_amdgcn_sched_barrier(0);  // every load above is in flight before any use
-    wait_vmcnt<RTW * D * KC + kKvLoads>();
+    wait_vmcnt<RTW * D * KC + (ATTN ? 2 : 0) + kKvLoads>();
     if (kTab && threadIdx.x < 32) exp_tab[threadIdx.x] = tab_v;
     if (kTab) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the table store lands before the barrier
     __builtin_amdgcn_s_barrier();
@@ -1662,12 +1685,7 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   // condition the load is a branch, whose join waited for every load in flight, the weight stream
   // included, before the first MFMA.
   const bool rope_in = ROPE && P >= 0 && P < a.limit;
-  float4 rc = make_float4(1.0f, 1.0f, 1.0f, 1.0f), rs = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-  if constexpr (ROPE) {
-    const float* rr = a.rope + (size_t)min(max(P, 0), a.limit - 1) * 128 + 16 * wave + 4 * g;
-    rc = *reinterpret_cast<const float4*>(rr);
-    rs = *reinterpret_cast<const float4*>(rr + 64);
-  }
+  if constexpr (ROPE && !ATTN) load_rope();
   v4i accH[RTW][D], accL[RTW][D];
 #pragma unroll
   for (int r = 0; r < RTW; ++r)
