@@ -1393,7 +1393,8 @@ __device__ __forceinline__ void attn_merge_quant_slice(const AttnMergeArgs& am, 
 // into LDS with its weights.  Its partial (m, l, acc[128]) goes to af.part / af.pml; split 0 also stores
 // the q row, which the O projection's merge needs for the new key's term.
 template <int RTW, bool DUAL, int EPI, int NKC, bool ROPE, int KSW, bool PRE, int PRE_EPI = kEpiStore,
-          bool PRE_QUANT = false, bool PRE_ATTN = false, bool GRP = false, bool ATTN = false, bool NEWKEY = false>
+          bool PRE_QUANT = false, bool PRE_ATTN = false, bool GRP = false, bool ATTN = false, bool NEWKEY = false,
+          bool KW = false>
 __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count, int rg_count, int splits,
                                                  const GemmArgs& pre, int pre_splits,
                                                  const AttnMergeArgs& am = AttnMergeArgs{},
@@ -1411,9 +1412,15 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   // one MFMA of a K chunk, is dequantized with its own scale, so the block's partials are fp32 sums
   // over groups that already carry the offset correction
   static_assert(!GRP || (!DUAL && !ROPE && KSW == 1 && !kMade), "grouped code: the skinny down projection");
-  constexpr int KC = NKC / KSW;  // K chunks per wave group
-  static_assert(NKC % KSW == 0, "K chunks split evenly over the wave groups");
-  static_assert(RTW * D * 8 * 1024 <= NKC * 16 * 256 || KSW == 1, "K-group reduction fits the slice buffer");
+  // KW (one token, a made slice): the block's four waves split the K chunks of the same RTW row tiles
+  // instead of taking four row tiles each: a quarter of the weight bytes per block, four times the
+  // blocks (a CU streams a few tens of KB at a time; a block's 96 KB of weights was its critical path)
+  static_assert(!KW || (KSW == 1 && kMade && !ROPE && !ATTN), "KW: the one-token projections without RoPE");
+  constexpr int KG = KW ? 4 : KSW;  // K groups: KSW groups of four waves, or (KW) four groups of one wave
+  constexpr int KC = NKC / KG;      // K chunks per wave
+  static_assert(NKC % KG == 0, "K chunks split evenly over the wave groups");
+  static_assert((KG - 1) * RTW * D * 8 * 256 * (KW ? 1 : 4) <= NKC * 16 * 256 || KG == 1,
+                "K-group reduction fits the slice buffer");
   // The activation slice: K chunk c's 16 token rows of 256 bytes at xs + (16 c + row) * 256 (row r's
   // 16-byte segments swizzled by ^ r).  ATTN keeps token 0's row alone (chunk c at xs + c * 256): the
   // MFMAs read it for every column, and the columns of the absent tokens are not stored.  (Its four
@@ -1430,8 +1437,8 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   __shared__ __align__(16) float wacc[ATTN ? 4 * QWEN_HEAD_DIM : 4];  // per wave: acc[128], then m and l
   __shared__ float wml[ATTN ? 8 : 2];
   const int lane = threadIdx.x & 63;
-  const int wave = (threadIdx.x >> 6) & 3;  // row position of the wave
-  const int kg = threadIdx.x >> 8;                                  // K group of the wave
+  const int wave = KW ? 0 : ((threadIdx.x >> 6) & 3);        // row position of the wave
+  const int kg = KW ? (threadIdx.x >> 6) : (threadIdx.x >> 8);  // K group of the wave
   const int g = lane >> 4;
   const int col = lane & 15;
   int rg_b, z_b, tt_b, ks = -1;  // ks: key split of an ATTN query-head block (-1: none)
@@ -1551,7 +1558,9 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   // (one product) and 8c + {1,3,5,7} (the other), so block rg takes tiles 8(rg/2) + 2 wave + rg%2 and
   // its 64 rows are exactly group rg.
   const bool gmap = EPI == kEpiSiluMul && DUAL && !kMade && KSW == 1 && RTW == 1 && a.gsx_out != nullptr;
-  auto row_tile = [&](int r) { return gmap ? 8 * (rg >> 1) + 2 * wave + (rg & 1) : rg * 4 * RTW + wave + 4 * r; };
+  auto row_tile = [&](int r) {
+    return KW ? rg * RTW + r : gmap ? 8 * (rg >> 1) + 2 * wave + (rg & 1) : rg * 4 * RTW + wave + 4 * r;
+  };
   float swv[RTW][4], sw2v[RTW][4], biasv[RTW][4];
   const int tok_l = min(tok0 + col, a.tokens - 1);
   float sx_l = 0.0f;
@@ -1752,32 +1761,39 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
       }
   }
 
-  if constexpr (KSW > 1) {
-    // K group 1 hands its exact int32 sums to K group 0 through LDS (the slice buffer, now read).
+  if constexpr (KG > 1) {
+    // K groups 1.. hand their exact int32 sums to K group 0 through LDS (the slice buffer, now read):
+    // region (row wave, or with KW the K group's) of RTW * D * 8 * 64 ints each.
     __syncthreads();
-    int* red = reinterpret_cast<int*>(xs) + (wave * RTW * D * 8) * 64 + lane;
-    if (kg == 1) {
+    constexpr int kRegion = RTW * D * 8 * 64;
+    int* red = reinterpret_cast<int*>(xs) + lane;
+    if (kg > 0) {
+      int* mine = red + (KW ? kg - 1 : wave) * kRegion;
 #pragma unroll
       for (int r = 0; r < RTW; ++r)
 #pragma unroll
         for (int d = 0; d < D; ++d)
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
-            red[((r * D + d) * 8 + q) * 64] = accH[r][d][q];
-            red[((r * D + d) * 8 + 4 + q) * 64] = accL[r][d][q];
+            mine[((r * D + d) * 8 + q) * 64] = accH[r][d][q];
+            mine[((r * D + d) * 8 + 4 + q) * 64] = accL[r][d][q];
           }
     }
     __syncthreads();
-    if (kg == 1) return;
+    if (kg > 0) return;
 #pragma unroll
-    for (int r = 0; r < RTW; ++r)
+    for (int j = 1; j < KG; ++j) {
+      const int* theirs = red + (KW ? j - 1 : wave) * kRegion;
 #pragma unroll
-      for (int d = 0; d < D; ++d)
+      for (int r = 0; r < RTW; ++r)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          accH[r][d][q] += red[((r * D + d) * 8 + q) * 64];
-          accL[r][d][q] += red[((r * D + d) * 8 + 4 + q) * 64];
-        }
+        for (int d = 0; d < D; ++d)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            accH[r][d][q] += theirs[((r * D + d) * 8 + q) * 64];
+            accL[r][d][q] += theirs[((r * D + d) * 8 + 4 + q) * 64];
+          }
+    }
   }
 
   if constexpr (EPI == kEpiSiluMul && DUAL && !kMade && KSW == 1 && RTW == 1) {
@@ -2029,9 +2045,9 @@ __global__ void __launch_bounds__(256) gemm_skinny_preq_kernel(GemmArgs a, int r
 
 // One token whose activation row is the decode attention's context: every block merges the split
 // partials and quantizes the row (see PRE_ATTN above; NEWKEY: with the new key's own term).
-template <int RTW, int EPI, int NKC, bool NEWKEY>
+template <int RTW, int EPI, int NKC, bool NEWKEY, bool KW = false>
 __global__ void __launch_bounds__(256) gemm_skinny_prea_kernel(GemmArgs a, int rg_count, AttnMergeArgs am) {
-  gemm_skinny_body<RTW, false, EPI, NKC, false, 1, false, kEpiStore, false, true, false, false, NEWKEY>(
+  gemm_skinny_body<RTW, false, EPI, NKC, false, 1, false, kEpiStore, false, true, false, false, NEWKEY, KW>(
       a, 1, rg_count, 1, a, 0, am);
 }
 
@@ -2053,6 +2069,14 @@ __global__ void __launch_bounds__(256) gemm_skinny_pre_attn_kernel(GemmArgs a, G
 template <int RTW, bool DUAL, int EPI, int NKC, bool ROPE, int PRE_EPI>
 __global__ void __launch_bounds__(256) gemm_skinny_pre_kernel(GemmArgs a, int rg_count, GemmArgs pre, int pre_splits) {
   gemm_skinny_body<RTW, DUAL, EPI, NKC, ROPE, 1, true, PRE_EPI>(a, 1, rg_count, 1, pre, pre_splits);
+}
+
+// The same with the block's four waves splitting K (KW above), three blocks per CU.
+template <int RTW, bool DUAL, int EPI, int NKC, int PRE_EPI>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
+gemm_skinny_pre_kw_kernel(GemmArgs a, int rg_count, GemmArgs pre, int pre_splits) {
+  gemm_skinny_body<RTW, DUAL, EPI, NKC, false, 1, true, PRE_EPI, false, false, false, false, false, true>(
+      a, 1, rg_count, 1, pre, pre_splits);
 }
 
 // Sum over z < splits of part[z * zstride + off .. + 3] in z order.  The loads of 8 splits are all
@@ -2373,6 +2397,7 @@ __device__ __forceinline__ void reduce_norm_quant_row_zb(const GemmArgs& a, int 
     sums_out[1] = sl;
   }
 }
+
 
 // One split (the O projection's single K group) or up to five (the down projection's) in one batch.
 template <int EPI, class Issue>
@@ -3220,8 +3245,9 @@ bool launch_gemm_i8_pre(const GemmArgs& a, const GemmArgs& pre, int pre_epi, int
       pre.tokens != 1 || pre_splits < 1 || pre_splits > kMaxSplits)
     return false;
   if (a.wp2 && a.out_dim % 64 == 0 && pre_epi == kEpiStore) {  // gate/up after the O projection
-    const int rg_count = a.out_dim / 64;
-    hipLaunchKernelGGL((gemm_skinny_pre_kernel<1, true, kEpiSiluMul, 12, false, kEpiStore>),
+    // one 16-row tile of both matrices per block, K split over its four waves
+    const int rg_count = a.out_dim / 16;
+    hipLaunchKernelGGL((gemm_skinny_pre_kw_kernel<1, true, kEpiSiluMul, 12, kEpiStore>),
                        dim3(8 * ((rg_count + 7) / 8)), dim3(256), 0, st, a, rg_count, pre, pre_splits);
     return true;
   }
@@ -3240,13 +3266,14 @@ bool launch_gemm_i8_prea(const GemmArgs& a, const AttnMergeArgs& am, hipStream_t
       a.fuse != kFuseNormQuant || !am.part || !am.pml || !am.pos || !am.sx_out || !am.sums_out || am.nsplit < 1 ||
       am.nsplit > kAttnMaxSplits || am.chunk < 1)
     return false;
-  const int rg_count = a.out_dim / 64;
+  // one 16-row tile per block, K split over its four waves
+  const int rg_count = a.out_dim / 16;
   if (am.qkv_new)
-    hipLaunchKernelGGL((gemm_skinny_prea_kernel<1, kEpiStore, 12, true>), dim3(8 * ((rg_count + 7) / 8)), dim3(256), 0,
-                       st, a, rg_count, am);
+    hipLaunchKernelGGL((gemm_skinny_prea_kernel<1, kEpiStore, 12, true, true>), dim3(8 * ((rg_count + 7) / 8)),
+                       dim3(256), 0, st, a, rg_count, am);
   else
-    hipLaunchKernelGGL((gemm_skinny_prea_kernel<1, kEpiStore, 12, false>), dim3(8 * ((rg_count + 7) / 8)), dim3(256),
-                       0, st, a, rg_count, am);
+    hipLaunchKernelGGL((gemm_skinny_prea_kernel<1, kEpiStore, 12, false, true>), dim3(8 * ((rg_count + 7) / 8)),
+                       dim3(256), 0, st, a, rg_count, am);
   if (!a.defer_reduce) launch_reduce<kEpiStore>(a, 1, st);
   return true;
 }
