@@ -1417,8 +1417,10 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   // blocks (a CU streams a few tens of KB at a time; a block's 96 KB of weights was its critical path)
   static_assert(!KW || (KSW == 1 && kMade && !ROPE && !ATTN), "KW: the one-token projections without RoPE");
   constexpr int KG = KW ? 4 : KSW;  // K groups: KSW groups of four waves, or (KW) four groups of one wave
-  constexpr int KC = NKC / KG;      // K chunks per wave
-  static_assert(NKC % KG == 0, "K chunks split evenly over the wave groups");
+  // K chunks per wave (KW with NKC not a multiple of 4: the last waves take fewer, the wave's chunks
+  // past NKC load chunk NKC - 1 again and skip their products)
+  constexpr int KC = (NKC + KG - 1) / KG;
+  static_assert(KW || NKC % KG == 0, "K chunks split evenly over the wave groups");
   static_assert((KG - 1) * RTW * D * 8 * 256 * (KW ? 1 : 4) <= NKC * 16 * 256 || KG == 1,
                 "K-group reduction fits the slice buffer");
   // The activation slice: K chunk c's 16 token rows of 256 bytes at xs + (16 c + row) * 256 (row r's
@@ -1585,12 +1587,12 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
 #pragma unroll
       for (int r = 0; r < RTW; ++r) {
         const int rt = row_tile(r);
-        const size_t base = ((size_t)(ok[r] ? rt : 0) * nkc_all + kc0 + kg * KC) * 64u + lane;
+        const size_t base = ((size_t)(ok[r] ? rt : 0) * nkc_all + kc0) * 64u + lane;
 #pragma unroll
         for (int d = 0; d < D; ++d) {
           const uint4* wp = reinterpret_cast<const uint4*>(d ? a.wp2 : a.wp) + base;
 #pragma unroll
-          for (int c = 0; c < KC; ++c) wv[r][d][c] = wp[(size_t)c * 64u];
+          for (int c = 0; c < KC; ++c) wv[r][d][c] = wp[(size_t)min(kg * KC + c, NKC - 1) * 64u];
         }
       }
     } else {
@@ -1742,6 +1744,7 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
       __builtin_amdgcn_sched_barrier(0);
       continue;
     }
+    if (KW && NKC % KG != 0 && kg * KC + c >= NKC) break;  // wave-uniform: the wave's chunks past NKC
     const int colr = ATTN ? 0 : col;  // ATTN: every column reads token 0's row
     const uint8_t* xr = xs + ((kg * KC + c) * kXsRows + colr) * 256;
     const v4i bh1 = *reinterpret_cast<const v4i*>(xr + (((2 * g) ^ colr) << 4));
@@ -2037,10 +2040,12 @@ gemm_skinny_kernel(GemmArgs a, int tt_count, int rg_count, int splits) {
                                                                                       a, 0);
 }
 
-// One token, the activation row quantized by every block for its own K chunks (see PRE_QUANT above).
-template <int RTW, int EPI, int NKC>
+// One token, the activation row quantized by every block for its own K chunks (see PRE_QUANT above;
+// KW: the block's waves split K).
+template <int RTW, int EPI, int NKC, bool KW = false>
 __global__ void __launch_bounds__(256) gemm_skinny_preq_kernel(GemmArgs a, int rg_count, int splits, GemmArgs pre) {
-  gemm_skinny_body<RTW, false, EPI, NKC, false, 1, false, kEpiStore, true>(a, 1, rg_count, splits, pre, 0);
+  gemm_skinny_body<RTW, false, EPI, NKC, false, 1, false, kEpiStore, true, false, false, false, false, KW>(
+      a, 1, rg_count, splits, pre, 0);
 }
 
 // One token whose activation row is the decode attention's context: every block merges the split
@@ -3312,8 +3317,9 @@ bool launch_gemm_i8_preq(const GemmArgs& a, const GemmArgs& pre, hipStream_t st)
       pre.in_dim != a.in_dim || !pre.y || !pre.sx_out || !pre.sums_out)
     return false;
   constexpr int kSplits = 5;  // 14 K chunks each, as the separate-quantization path
-  const int rg_count = a.out_dim / 64;
-  hipLaunchKernelGGL((gemm_skinny_preq_kernel<1, kEpiResidual, 14>), dim3(8 * ((rg_count * kSplits + 7) / 8)),
+  // one 16-row tile per block, its 14 K chunks split over the block's four waves (4, 4, 3, 3)
+  const int rg_count = a.out_dim / 16;
+  hipLaunchKernelGGL((gemm_skinny_preq_kernel<1, kEpiResidual, 14, true>), dim3(8 * ((rg_count * kSplits + 7) / 8)),
                      dim3(256), 0, st, a, rg_count, kSplits, pre);
   if (!(a.defer_reduce && a.fuse == kFuseNormQuant)) launch_reduce<kEpiResidual>(a, kSplits, st);
   return true;
