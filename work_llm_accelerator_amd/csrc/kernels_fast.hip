@@ -1121,6 +1121,10 @@ template <int EPI, int ZB, class Issue, int W = 1>
 __device__ __forceinline__ void reduce_norm_quant_row_zb(const GemmArgs& a, int splits, int tok, int8_t* xq_row,
                                                          int chunk_stride, float* sx_out, int* sums_out, bool write_y,
                                                          Issue&& issue);
+template <int EPI, int ZB, class Issue>
+__device__ __forceinline__ void reduce_norm_quant_row_w4(const GemmArgs& a, int splits, int8_t* xq_row,
+                                                         int chunk_stride, float* sx_out, int* sums_out, bool write_y,
+                                                         Issue&& issue);
 
 // Two-limb quantization of one fp32 row x[0, n) (n % 4 == 0, n <= NV * 1024) by a 256-thread block
 // with norm_quant_row's arithmetic and thread mapping (float4 k = t + 256 j): the code of K chunks
@@ -1376,10 +1380,10 @@ __device__ __forceinline__ void attn_merge_quant_slice(const AttnMergeArgs& am, 
   }
 }
 
-// PRE (one token, KSW = 1): the activation slice is not loaded but made by the block: wave 0 redoes
-// the reduce step of the previous projection (`pre` with epilogue PRE_EPI, pre_splits K splits,
-// kFuseNormQuant on a 1536-wide row) for token 0 straight into the slice, once the block's weight
-// loads are in flight; block 0 alone writes the finished row (pre.y, pre.y_raw).  K chunk c of the
+// PRE (one token, KSW = 1): the activation slice is not loaded but made by the block: its four waves
+// redo the reduce step of the previous projection (`pre` with epilogue PRE_EPI, pre_splits K splits,
+// kFuseNormQuant on a 1536-wide row) for token 0 straight into the slice, each wave's weight loads
+// issued right after its loads of the row; block 0 alone writes the finished row (pre.y, pre.y_raw).  K chunk c of the
 // slice is the token's row c.  PRE_QUANT (one token, KSW = 1): the slice is the two-limb code of the
 // fp32 row pre.y (pre.in_dim wide, as norm_quant_kernel without a norm), made by every block for its
 // own K chunks; block 0 writes the row's scale and limb sums to pre.sx_out / pre.sums_out.  PRE_ATTN
@@ -1662,13 +1666,12 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
                                 blockIdx.x == 0 ? pre.sx_out : nullptr, pre.sums_out, issue_loads);
   }
   if constexpr (PRE) {
-    // token 0's row of the slice: K chunk c at xs + c * 16 * 256 (row 0 of the chunk, unswizzled)
-    if (threadIdx.x < 64)
-      // the O projection's one K group (store epilogue) or the down projection's five splits (residual)
-      reduce_norm_quant_row_zb<PRE_EPI, PRE_EPI == kEpiResidual ? 5 : 1>(
-          pre, pre_splits, 0, reinterpret_cast<int8_t*>(xs), kXsChunk, &pre_sx, pre_sums, blockIdx.x == 0, issue_loads);
-    else
-      issue_loads();
+    // token 0's row of the slice (K chunk c at xs + c * kXsChunk, row 0 of the chunk, unswizzled), made
+    // by the block's four waves together (three block barriers): the O projection's one K group (store
+    // epilogue) or the down projection's five splits (residual).  (One wave alone, with the other
+    // three issuing their loads, took 2.2 us of arithmetic on the launch's critical path.)
+    reduce_norm_quant_row_w4<PRE_EPI, PRE_EPI == kEpiResidual ? 5 : 1>(
+        pre, pre_splits, reinterpret_cast<int8_t*>(xs), kXsChunk, &pre_sx, pre_sums, blockIdx.x == 0, issue_loads);
   }
   if constexpr (kMade) {
     __builtin_amdgcn_sched_barrier(0);  // every load above is in flight before any use
@@ -2400,6 +2403,137 @@ __device__ __forceinline__ void reduce_norm_quant_row_zb(const GemmArgs& a, int 
     *sx_out = amax > 0.0f ? amax / (float)kQuantMax : 1.0f;
     sums_out[0] = sh;
     sums_out[1] = sl;
+  }
+}
+
+// reduce_norm_quant_row_zb's arithmetic for token 0's 1536-wide row (decode norm or none) by the four
+// waves of a 256-thread block: thread t owns float4 t and, for t < 128 (waves 0 and 1), float4 t + 256.
+// The sum of squares, the maximum and the limb sums are each a wave reduction (wave_sum's order) and
+// one exchange of the four waves' values through LDS: three barriers in all.  Every wave calls `issue`
+// once, right after its loads of the row.
+template <int EPI, int ZB, class Issue>
+__device__ __forceinline__ void reduce_norm_quant_row_w4(const GemmArgs& a, int splits, int8_t* xq_row,
+                                                         int chunk_stride, float* sx_out, int* sums_out, bool write_y,
+                                                         Issue&& issue) {
+  __shared__ double w_ss[4];
+  __shared__ float w_max[4];
+  __shared__ int w_sums[8];
+  constexpr int kF = QWEN_HIDDEN / 4;  // float4s of the row
+  const int t = threadIdx.x, wv = t >> 6;
+  const bool two = t < kF - 256;  // wave-uniform
+  const int f[2] = {t, min(t + 256, kF - 1)};
+  const size_t zstride4 = (size_t)a.tokens * kF;
+  const float4* pt = reinterpret_cast<const float4*>(a.part);
+  const float4* sw4 = reinterpret_cast<const float4*>(a.sw);
+  const bool has_add = EPI == kEpiResidual || a.bias != nullptr;
+  const bool has_w = a.norm != kNormNone;
+  const float4* r4 = EPI == kEpiResidual ? reinterpret_cast<const float4*>(a.resid)
+                                         : (a.bias ? reinterpret_cast<const float4*>(a.bias) : sw4);
+  const float4* w4 = has_w ? reinterpret_cast<const float4*>(a.norm_w) : sw4;
+  const int sum_h = a.sums[0], sum_l = a.sums[1];
+  const float sx_tok = a.sx[0];
+  float4 acc[2], sw[2], ad[2], wn[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    sw[j] = sw4[f[j]];
+    ad[j] = r4[f[j]];
+    wn[j] = w4[f[j]];
+    acc[j] = make_float4(0, 0, 0, 0);
+  }
+  for (int z0 = 0; z0 < splits; z0 += ZB) {
+    float4 pz[ZB][2];
+#pragma unroll
+    for (int u = 0; u < ZB; ++u)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) pz[u][j] = pt[(size_t)min(z0 + u, splits - 1) * zstride4 + f[j]];
+    if (z0 == 0) {
+      __builtin_amdgcn_sched_barrier(0);
+      issue();
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int u = 0; u < ZB; ++u)
+      if (z0 + u < splits)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          acc[j].x += pz[u][j].x;
+          acc[j].y += pz[u][j].y;
+          acc[j].z += pz[u][j].z;
+          acc[j].w += pz[u][j].w;
+        }
+  }
+  if (splits < 1) issue();
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    if (!has_add) ad[j] = make_float4(0, 0, 0, 0);
+    if (!has_w) wn[j] = make_float4(0, 0, 0, 0);
+  }
+  const double corr = -8.0 * (256.0 * (double)sum_h + (double)sum_l) * (double)sx_tok;
+  float4 v[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+    v[j] = rnq_combine<EPI>(a, 0, 4 * f[j], acc[j], sw[j], ad[j], corr, write_y && (j == 0 || two));
+  if (a.norm == kNormDecode) {
+    double ss = rnq_sq4(v[0]);
+    if (two) ss += rnq_sq4(v[1]);
+    ss = wave_sum_d(ss);
+    if ((t & 63) == 0) w_ss[wv] = ss;
+    __syncthreads();
+    ss = (w_ss[0] + w_ss[1]) + (w_ss[2] + w_ss[3]);
+    const double inv = 1.0 / sqrt(ss / (double)QWEN_HIDDEN + (double)QWEN_RMS_EPS);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) v[j] = rnq_norm4(v[j], inv, wn[j]);
+  } else if (a.norm == kNormPrefill) {
+    float ss = v[0].x * v[0].x + v[0].y * v[0].y + v[0].z * v[0].z + v[0].w * v[0].w;
+    if (two) ss += v[1].x * v[1].x + v[1].y * v[1].y + v[1].z * v[1].z + v[1].w * v[1].w;
+    ss = wave_sum(ss);
+    if ((t & 63) == 0) w_ss[wv] = ss;
+    __syncthreads();
+    ss = (float)((w_ss[0] + w_ss[1]) + (w_ss[2] + w_ss[3]));
+    const float inv = 1.0f / approx_sqrt((float)ss / (float)QWEN_HIDDEN + QWEN_RMS_EPS);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      v[j] = make_float4(v[j].x * inv * wn[j].x, v[j].y * inv * wn[j].y, v[j].z * inv * wn[j].z, v[j].w * inv * wn[j].w);
+  }
+  float amax = fmaxf(fmaxf(fabsf(v[0].x), fabsf(v[0].y)), fmaxf(fabsf(v[0].z), fabsf(v[0].w)));
+  if (two) amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[1].x), fabsf(v[1].y)), fmaxf(fabsf(v[1].z), fabsf(v[1].w))));
+  amax = wave_max(amax);
+  if ((t & 63) == 0) w_max[wv] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(w_max[0], w_max[1]), fmaxf(w_max[2], w_max[3]));
+  const float qinv = amax > 0.0f ? (float)kQuantMax / amax : 0.0f;
+  int sh = 0, sl = 0;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    if (j == 1 && !two) break;
+    const float e[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+    uint32_t hw = 0, lw = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float xf = fminf(fmaxf(rintf(e[q] * qinv), -(float)kQuantMax), (float)kQuantMax);
+      const int X = (int)xf;
+      const int H = (X + 128) >> 8;
+      const int L = X - (H << 8);
+      hw |= (uint32_t)(H & 0xFF) << (8 * q);
+      lw |= (uint32_t)(L & 0xFF) << (8 * q);
+      sh += H;
+      sl += L;
+    }
+    const int base = ((4 * f[j]) >> 7) * chunk_stride + ((4 * f[j]) & 127);
+    *reinterpret_cast<uint32_t*>(xq_row + base) = hw;
+    *reinterpret_cast<uint32_t*>(xq_row + base + 128) = lw;
+  }
+  sh = wave_sum_i(sh);
+  sl = wave_sum_i(sl);
+  if ((t & 63) == 0) {
+    w_sums[2 * wv] = sh;
+    w_sums[2 * wv + 1] = sl;
+  }
+  __syncthreads();
+  if (t == 0) {
+    *sx_out = amax > 0.0f ? amax / (float)kQuantMax : 1.0f;
+    sums_out[0] = (w_sums[0] + w_sums[2]) + (w_sums[4] + w_sums[6]);
+    sums_out[1] = (w_sums[1] + w_sums[3]) + (w_sums[5] + w_sums[7]);
   }
 }
 
