@@ -1984,18 +1984,29 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
       sc += __shfl_xor(sc, 16, 64);
       sc += __shfl_xor(sc, 32, 64);
       if (t0 + r >= t1) sc = -INFINITY;
+      // every row of 16 lanes now holds the wave's 16 scores: maximum and sum by DPP row steps, the
+      // weights to every lane by readlane (lane k2 holds key k2's)
+      auto dppf = [](float v, auto ctrl) { return __int_as_float(dpp_i<decltype(ctrl)::value>(__float_as_int(v))); };
+      using C1 = std::integral_constant<int, 0xB1>;   // quad_perm: lanes ^ 1
+      using C2 = std::integral_constant<int, 0x4E>;   // quad_perm: lanes ^ 2
+      using C4 = std::integral_constant<int, 0x124>;  // row_ror:4
+      using C8 = std::integral_constant<int, 0x128>;  // row_ror:8
       float m = sc;
-#pragma unroll
-      for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+      m = fmaxf(m, dppf(m, C1{}));
+      m = fmaxf(m, dppf(m, C2{}));
+      m = fmaxf(m, dppf(m, C4{}));
+      m = fmaxf(m, dppf(m, C8{}));
       const float pr = m == -INFINITY ? 0.0f : __expf(sc - m);  // a wave without keys: weight 0
       float l = pr;
-#pragma unroll
-      for (int o = 1; o < 16; o <<= 1) l += __shfl_xor(l, o, 64);
+      l += dppf(l, C1{});
+      l += dppf(l, C2{});
+      l += dppf(l, C4{});
+      l += dppf(l, C8{});
       float a0 = 0.0f, a1 = 0.0f;
       const float* vb = kv_lds + (kKvRows + 16 * wave) * QWEN_HEAD_DIM + 2 * lane;
 #pragma unroll
       for (int k2 = 0; k2 < 16; ++k2) {
-        const float pk = __shfl(pr, k2, 64);  // lane k2 holds key k2's weight
+        const float pk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pr), k2));
         const float2 v2 = *reinterpret_cast<const float2*>(vb + k2 * QWEN_HEAD_DIM);
         a0 += pk * v2.x;
         a1 += pk * v2.y;
