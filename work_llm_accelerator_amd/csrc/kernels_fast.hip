@@ -3462,9 +3462,11 @@ bool launch_gemm_i8_preq(const GemmArgs& a, const GemmArgs& pre, hipStream_t st)
       pre.in_dim != a.in_dim || !pre.y || !pre.sx_out || !pre.sums_out)
     return false;
   constexpr int kSplits = 5;  // 14 K chunks each, as the separate-quantization path
-  // one 16-row tile per block, its 14 K chunks split over the block's four waves (4, 4, 3, 3)
-  const int rg_count = a.out_dim / 16;
-  hipLaunchKernelGGL((gemm_skinny_preq_kernel<1, kEpiResidual, 14, true>), dim3(8 * ((rg_count * kSplits + 7) / 8)),
+  // two 16-row tiles per block, their 14 K chunks split over the block's four waves (4, 4, 3, 3): 240
+  // blocks (every block quantizes the whole 8960-wide row for its scale, so fewer blocks than the other
+  // one-token projections: 480 blocks of one tile, or 160 of three, were slower)
+  const int rg_count = a.out_dim / 32;
+  hipLaunchKernelGGL((gemm_skinny_preq_kernel<2, kEpiResidual, 14, true>), dim3(8 * ((rg_count * kSplits + 7) / 8)),
                      dim3(256), 0, st, a, rg_count, kSplits, pre);
   if (!(a.defer_reduce && a.fuse == kFuseNormQuant)) launch_reduce<kEpiResidual>(a, kSplits, st);
   return true;
