@@ -193,25 +193,18 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) l
 // next two rows' loads in flight.  Lane l holds x[8l + 512j .. + 7] (j < 3) in fp32 and forms its 24
 // products of a row in (j, e) order; the 64 lane sums are added by DPP row steps, then the four rows in
 // lane order.  Logits are rounded to bf16 and keyed as in lm_head_kernel (best[0][vb]).
-template <bool LOGITS>
+// NORM: the block reads the fp32 row `hidden` and the norm weights instead of the normalized row, and
+// every wave forms head_norm_kernel's values for its lanes' 24 columns itself (the sum of squares over
+// the whole row by each wave: exact in double, so the same var), with the first table rows in flight.
+template <bool LOGITS, bool NORM = false>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5)))
 lm_head_row_kernel(const uint16_t* __restrict__ table, int vocab, const uint16_t* __restrict__ xn,
-                   float* __restrict__ logits, unsigned long long* __restrict__ best) {
+                   float* __restrict__ logits, unsigned long long* __restrict__ best,
+                   const float* __restrict__ hidden = nullptr, const uint16_t* __restrict__ norm_w = nullptr) {
   __shared__ unsigned long long red[4];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int row0 = blockIdx.x * (2 * kHeadBlockRows) + wave * 32;
   constexpr int kRowU4 = QWEN_HIDDEN / 8;  // uint4 per table row
-  float x[3][8];
-#pragma unroll
-  for (int j = 0; j < 3; ++j) {
-    const uint4 q = *reinterpret_cast<const uint4*>(xn + 8 * lane + 512 * j);
-    const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      x[j][2 * e] = bits_f32(w4[e] << 16);
-      x[j][2 * e + 1] = bits_f32(w4[e] & 0xFFFF0000u);
-    }
-  }
   const uint4* tp = reinterpret_cast<const uint4*>(table) + (size_t)row0 * kRowU4 + lane;
   auto load2 = [&](int r, uint4 (&d)[2][3]) {
 #pragma unroll
@@ -223,7 +216,51 @@ lm_head_row_kernel(const uint16_t* __restrict__ table, int vocab, const uint16_t
       }
   };
   uint4 cur[2][3], nxt[2][3];
-  load2(0, cur);
+  load2(0, cur);  // the first two rows in flight while the activation row is formed
+  __builtin_amdgcn_sched_barrier(0);
+  float x[3][8];
+  if constexpr (NORM) {
+    float v[3][8];
+    uint4 wq[3];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const float4 a = *reinterpret_cast<const float4*>(hidden + 8 * lane + 512 * j);
+      const float4 b = *reinterpret_cast<const float4*>(hidden + 8 * lane + 512 * j + 4);
+      wq[j] = *reinterpret_cast<const uint4*>(norm_w + 8 * lane + 512 * j);
+      const float h[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[j][e] = to_bf16(h[e]);
+    }
+    double ss = 0.0;
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += (double)v[j][e] * (double)v[j][e];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    const float var = (float)ss / (float)QWEN_HIDDEN;
+    const float r = 1.0f / sqrtf(var + QWEN_RMS_EPS);
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const uint32_t w4[4] = {wq[j].x, wq[j].y, wq[j].z, wq[j].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float w = bits_f32(e & 1 ? (w4[e >> 1] & 0xFFFF0000u) : (w4[e >> 1] << 16));
+        x[j][e] = to_bf16(w * to_bf16(v[j][e] * r));
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const uint4 q = *reinterpret_cast<const uint4*>(xn + 8 * lane + 512 * j);
+      const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        x[j][2 * e] = bits_f32(w4[e] << 16);
+        x[j][2 * e + 1] = bits_f32(w4[e] & 0xFFFF0000u);
+      }
+    }
+  }
   unsigned long long bk = 0ull;
 #pragma unroll 1
   for (int r = 0; r < 32; r += 2) {
@@ -304,17 +341,22 @@ void launch_head(const float* hidden, int count, const uint16_t* norm_w, const u
       reinterpret_cast<unsigned long long*>(static_cast<char*>(workspace) + ((xn_bytes + 255u) & ~size_t(255u)));
   const int nblk = vocab / (2 * kHeadBlockRows);
   const size_t lds = (size_t)(count < 16 ? count : 16) * kHeadRow * 2u;  // live token rows of a tile
-  hipLaunchKernelGGL(head_norm_kernel, dim3(tiles * 16), dim3(256), 0, st, hidden, count, norm_w, xn);
+  // one token: the norm runs inside every lm_head block (no launch of its own)
   if (count == 1 && logits)
-    hipLaunchKernelGGL(lm_head_row_kernel<true>, dim3(nblk), dim3(256), 0, st, table, vocab, xn, logits, best);
+    hipLaunchKernelGGL((lm_head_row_kernel<true, true>), dim3(nblk), dim3(256), 0, st, table, vocab, xn, logits, best,
+                       hidden, norm_w);
   else if (count == 1)
-    hipLaunchKernelGGL(lm_head_row_kernel<false>, dim3(nblk), dim3(256), 0, st, table, vocab, xn, logits, best);
-  else if (logits)
-    hipLaunchKernelGGL(lm_head_kernel<true>, dim3(nblk, tiles), dim3(256), lds, st, table, vocab, xn, count, logits,
-                       best);
-  else
-    hipLaunchKernelGGL(lm_head_kernel<false>, dim3(nblk, tiles), dim3(256), lds, st, table, vocab, xn, count, logits,
-                       best);
+    hipLaunchKernelGGL((lm_head_row_kernel<false, true>), dim3(nblk), dim3(256), 0, st, table, vocab, xn, logits, best,
+                       hidden, norm_w);
+  else {
+    hipLaunchKernelGGL(head_norm_kernel, dim3(tiles * 16), dim3(256), 0, st, hidden, count, norm_w, xn);
+    if (logits)
+      hipLaunchKernelGGL(lm_head_kernel<true>, dim3(nblk, tiles), dim3(256), lds, st, table, vocab, xn, count, logits,
+                         best);
+    else
+      hipLaunchKernelGGL(lm_head_kernel<false>, dim3(nblk, tiles), dim3(256), lds, st, table, vocab, xn, count, logits,
+                         best);
+  }
   if (ids) hipLaunchKernelGGL(argmax_finalize_kernel, dim3(count), dim3(256), 0, st, best, nblk, ids);
 }
 
