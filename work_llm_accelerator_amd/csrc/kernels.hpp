@@ -146,7 +146,9 @@ bool launch_gemm_i8_prea(const GemmArgs& a, const AttnMergeArgs& am, hipStream_t
 // decode attention over the history keys fused in (AttnFuseArgs; af.chunk == kFusedAttnChunk, at most
 // kFusedAttnMaxSplits splits): its partials are merged, with the new key's term, by the O projection
 // (launch_gemm_i8_prea with am.qkv_new set).  _pre: the activation row is `pre`'s unfinished down-projection
-// reduce step (as launch_gemm_i8_pre with kEpiResidual); otherwise a.xq holds the quantized row.
+// reduce step (as launch_gemm_i8_pre with kEpiResidual; pre_splits == 0: the row pre.resid itself,
+// normalized and quantized, with pre.sums and pre.sx pointing at zeros and pre.y, pre.y_raw null);
+// otherwise a.xq holds the quantized row.
 // Returns false (nothing launched) for other shapes.
 bool launch_gemm_i8_attn(const GemmArgs& a, const AttnFuseArgs& af, hipStream_t st);
 bool launch_gemm_i8_pre_attn(const GemmArgs& a, const GemmArgs& pre, int pre_splits, const AttnFuseArgs& af,

@@ -1671,7 +1671,8 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
     // epilogue) or the down projection's five splits (residual).  (One wave alone, with the other
     // three issuing their loads, took 2.2 us of arithmetic on the launch's critical path.)
     reduce_norm_quant_row_w4<PRE_EPI, PRE_EPI == kEpiResidual ? 5 : 1>(
-        pre, pre_splits, reinterpret_cast<int8_t*>(xs), kXsChunk, &pre_sx, pre_sums, blockIdx.x == 0, issue_loads);
+        pre, pre_splits, reinterpret_cast<int8_t*>(xs), kXsChunk, &pre_sx, pre_sums, blockIdx.x == 0 && pre.y,
+        issue_loads);
   }
   if constexpr (kMade) {
     __builtin_amdgcn_sched_barrier(0);  // every load above is in flight before any use
@@ -3449,8 +3450,10 @@ bool launch_gemm_i8_attn(const GemmArgs& a, const AttnFuseArgs& af, hipStream_t 
 
 bool launch_gemm_i8_pre_attn(const GemmArgs& a, const GemmArgs& pre, int pre_splits, const AttnFuseArgs& af,
                              hipStream_t st) {
+  // pre_splits == 0: the row is pre.resid itself (the first layer of a range: RMSNorm and quantization
+  // of the input row, pre.sums / pre.sx pointing at zeros, nothing written back)
   if (!fused_attn_ok(a, af) || pre.out_dim != QWEN_HIDDEN || pre.fuse != kFuseNormQuant || pre.tokens != 1 ||
-      pre_splits < 1 || pre_splits > kMaxSplits)
+      pre_splits < 0 || pre_splits > kMaxSplits || (pre_splits == 0 && (!pre.resid || pre.y || pre.y_raw)))
     return false;
   hipLaunchKernelGGL(gemm_skinny_pre_attn_kernel, dim3(fused_attn_blocks(af.nsplit)), dim3(256), 0, st, a, pre,
                      pre_splits, af);

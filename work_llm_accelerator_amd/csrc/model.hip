@@ -301,7 +301,9 @@ struct qwen_hip_model {
       float* vc = vc0 + (size_t)i * ls;
       // With at most kSplitTokens sequences, RoPE + KV append and the two RMSNorm + quantize steps
       // run inside the split-K reduce kernels of the QKV, O and down projections.
-      if (i == 0 || !fused)
+      // (one sequence with the attention fused: the first layer's RMSNorm and quantization run in the
+      // Q/K/V blocks' prologue instead)
+      if ((i == 0 && !fuse_attn) || !fused)
         launch_norm_quant(hidden, QWEN_HIDDEN, B, QWEN_HIDDEN, f.ln, kNormDecode, w.xq, w.sx, w.sums, nullptr,
                           stream);
       if (fused) {
@@ -322,9 +324,24 @@ struct qwen_hip_model {
                         : !launch_gemm_i8_pre(qa, down_pending, kEpiResidual, 5, stream))
             throw std::runtime_error("Q/K/V with the down reduce: bad shape");
         } else if (fuse_attn) {
+          // the range's first layer: every block normalizes and quantizes the input row itself (a
+          // reduce step with no partials: the row is the "residual", the correction terms zero)
           const GemmArgs qa = args(w, B, QWEN_HIDDEN, (int)kQkvRows, f.qkv, f.sw_qkv, f.b_qkv, w.qkv, kQkvRows,
                                    nullptr, nullptr, nullptr, 0, 0, &fq);
-          if (!launch_gemm_i8_attn(qa, af, stream)) throw std::runtime_error("Q/K/V with the attention: bad shape");
+          GemmArgs in{};
+          in.fuse = kFuseNormQuant;
+          in.norm = kNormDecode;
+          in.norm_w = f.ln;
+          in.tokens = 1;
+          in.in_dim = QWEN_HIDDEN;
+          in.out_dim = QWEN_HIDDEN;
+          in.resid = hidden;
+          in.resid_stride = QWEN_HIDDEN;
+          in.sw = f.ln;  // read, times a zero correction
+          in.sums = w.zero_sums;
+          in.sx = reinterpret_cast<const float*>(w.zero_sums);
+          if (!launch_gemm_i8_pre_attn(qa, in, 0, af, stream))
+            throw std::runtime_error("Q/K/V with the attention: bad shape");
         } else {
           gemm(w, B, QWEN_HIDDEN, (int)kQkvRows, f.qkv, f.sw_qkv, f.b_qkv, w.qkv, kQkvRows, kEpiStore, nullptr,
                nullptr, nullptr, 0, 0, &fq);
