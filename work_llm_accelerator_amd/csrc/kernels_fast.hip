@@ -1195,6 +1195,59 @@ __device__ __forceinline__ void quant_row_slice(const float* __restrict__ x, int
   }
 }
 
+// Merge weights of one sequence's split-KV decode-attention partials, per head h: M = the maximum of
+// the splits' m (and of the new key's score s_new[h] when has_new), f = exp(m - M), L = sum of l * f
+// (+ exp(s_new[h] - M)), weight = f / L, written over m in ml ([h][kAttnMaxSplits][2]: m, l) for the
+// splits sp < nc (and to s_new[h] for the new key).  Threads 16h + j (h < 12) take splits j, j + 16,
+// j + 32, j + 48 of head h; the maximum and the sum meet by DPP row steps (one row of 16 lanes per
+// head), each lane's own splits first in ascending order.  Every thread of the block calls it.
+__device__ __forceinline__ void merge_split_weights(float* ml, int nc, float* s_new, bool has_new) {
+  static_assert(kAttnMaxSplits % 16 == 0, "splits in rows of 16 lanes");
+  constexpr int kPer = kAttnMaxSplits / 16;
+  const int t = threadIdx.x;
+  if (t < 16 * QWEN_Q_HEADS) {  // wave-uniform: waves 0..2
+    const int h = t >> 4, j = t & 15;
+    float* mh = ml + h * kAttnMaxSplits * 2;
+    auto rmax = [](float v) {
+      v = fmaxf(v, __int_as_float(dpp_i<0xB1>(__float_as_int(v))));
+      v = fmaxf(v, __int_as_float(dpp_i<0x4E>(__float_as_int(v))));
+      v = fmaxf(v, __int_as_float(dpp_i<0x124>(__float_as_int(v))));
+      return fmaxf(v, __int_as_float(dpp_i<0x128>(__float_as_int(v))));
+    };
+    auto rsum = [](float v) {
+      v += __int_as_float(dpp_i<0xB1>(__float_as_int(v)));
+      v += __int_as_float(dpp_i<0x4E>(__float_as_int(v)));
+      v += __int_as_float(dpp_i<0x124>(__float_as_int(v)));
+      return v + __int_as_float(dpp_i<0x128>(__float_as_int(v)));
+    };
+    float mv[kPer], lv[kPer];
+    float M = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int sp = j + 16 * k;
+      mv[k] = sp < nc ? mh[2 * sp] : -INFINITY;
+      lv[k] = sp < nc ? mh[2 * sp + 1] : 0.0f;
+      M = fmaxf(M, mv[k]);
+    }
+    M = rmax(M);
+    if (has_new) M = fmaxf(M, s_new[h]);
+    float L = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      mv[k] = j + 16 * k < nc ? __expf(mv[k] - M) : 0.0f;
+      L += lv[k] * mv[k];
+    }
+    L = rsum(L);
+    const float fn = has_new ? __expf(s_new[h] - M) : 0.0f;
+    L += fn;
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k)
+      if (j + 16 * k < nc) mh[2 * (j + 16 * k)] = mv[k] * inv;  // merge weight of split sp
+    if (has_new && j == 0) s_new[h] = fn * inv;                 // merge weight of the new key
+  }
+}
+
 // The merge of one sequence's split-KV decode-attention partials, in the arithmetic and order of
 // attn_decode_kernel's merge (per head: max of the split maxima, exp-weights normalised by the
 // weighted sum, then the weighted sum of the split partial rows), followed by quantize_row_lds's
@@ -1282,26 +1335,7 @@ __device__ __forceinline__ void attn_merge_quant_slice(const AttnMergeArgs& am, 
     }
   }
   __syncthreads();
-  if (threadIdx.x < QWEN_Q_HEADS) {
-    float* mh = ml + threadIdx.x * kAttnMaxSplits * 2;
-    float M = -INFINITY;
-    for (int sp = 0; sp < nc; ++sp) M = fmaxf(M, mh[2 * sp]);
-    if (has_new) M = fmaxf(M, s_new[threadIdx.x]);
-    float L = 0.0f;
-    for (int sp = 0; sp < nc; ++sp) {
-      const float f = __expf(mh[2 * sp] - M);
-      mh[2 * sp] = f;
-      L += mh[2 * sp + 1] * f;
-    }
-    float fn = 0.0f;
-    if (has_new) {
-      fn = __expf(s_new[threadIdx.x] - M);
-      L += fn;
-    }
-    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-    for (int sp = 0; sp < nc; ++sp) mh[2 * sp] *= inv;  // merge weight of split sp
-    if (NEWKEY) s_new[threadIdx.x] = fn * inv;         // merge weight of the new key (0 without one)
-  }
+  merge_split_weights(ml, nc, s_new, has_new);
   __syncthreads();
   float4 out[2] = {make_float4(0.0f, 0.0f, 0.0f, 0.0f), make_float4(0.0f, 0.0f, 0.0f, 0.0f)};
   for (int s0 = 0; s0 < nc; s0 += kFirst) {
@@ -2880,19 +2914,7 @@ attn_decode_kernel(const float* __restrict__ qkv, int qkv_stride, const float* _
     ml[(h * kAttnMaxSplits + sp) * 2 + 1] = v.y;
   }
   __syncthreads();
-  if (threadIdx.x < QWEN_Q_HEADS) {
-    float* mh = ml + threadIdx.x * kAttnMaxSplits * 2;
-    float M = -INFINITY;
-    for (int sp = 0; sp < nc; ++sp) M = fmaxf(M, mh[2 * sp]);
-    float L = 0.0f;
-    for (int sp = 0; sp < nc; ++sp) {
-      const float f = __expf(mh[2 * sp] - M);
-      mh[2 * sp] = f;
-      L += mh[2 * sp + 1] * f;
-    }
-    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-    for (int sp = 0; sp < nc; ++sp) mh[2 * sp] *= inv;  // merge weight of split sp
-  }
+  merge_split_weights(ml, nc, nullptr, false);
   __syncthreads();
   float out[6];
 #pragma unroll
