@@ -1256,7 +1256,7 @@ __device__ __forceinline__ void merge_split_weights(float* ml, int nc, float* s_
 // NEWKEY (the attention fused into the Q/K/V projection): the partials cover the history keys and the
 // new key is a term of its own, read from am.qkv_new: score s = (q / sqrt(128)) . k, weight exp(s - M)
 // with M the maximum over the splits and s, added to the sum with l = 1 and to the row with v.
-template <bool NEWKEY = false, class Issue>
+template <bool NEWKEY = false, int KF = 16, class Issue>
 __device__ __forceinline__ void attn_merge_quant_slice(const AttnMergeArgs& am, uint8_t* xs, int chunk_stride,
                                                        float* sx_lds, int* sums_lds, bool write_global,
                                                        Issue&& issue) {
@@ -1267,7 +1267,10 @@ __device__ __forceinline__ void attn_merge_quant_slice(const AttnMergeArgs& am, 
   // are loaded whatever the key count; the merge below reads only the splits that hold keys.  Thread
   // t owns float4 f = t and t + 256 (f < 384) of the context row: head f >> 5, dims 4 (f & 31) .. + 3;
   // 16-byte loads keep a wave's outstanding loads (with the caller's weights) under the counter's 63.
-  constexpr int kFirst = 16;  // one-sequence plans use at most 24 splits
+  // KF (8, 12 or 16) is the batch of splits loaded at once; with KF < 16 the caller guarantees
+  // nsplit <= KF, so one batch and one (m, l) pair per thread cover every split.
+  static_assert(KF == 8 || KF == 12 || KF == 16, "merge batch");
+  constexpr int kFirst = KF;
   const int nsplit = am.nsplit;
   float4 pv[2][kFirst];
   // Branch-free within a wave: past the last split the loads read the last split again (used by
@@ -1285,7 +1288,7 @@ __device__ __forceinline__ void attn_merge_quant_slice(const AttnMergeArgs& am, 
   };
   const int p0 = am.pos[0];
   load_part(0);
-  constexpr int kMlPer = (QWEN_Q_HEADS * kAttnMaxSplits + 255) / 256;  // (m, l) pairs per thread, at most
+  constexpr int kMlPer = (QWEN_Q_HEADS * (KF < 16 ? KF : kAttnMaxSplits) + 255) / 256;  // (m, l) pairs per thread
   float2 mlv[kMlPer];
 #pragma unroll
   for (int u = 0; u < kMlPer; ++u) {
@@ -1432,7 +1435,7 @@ __device__ __forceinline__ void attn_merge_quant_slice(const AttnMergeArgs& am, 
 // the q row, which the O projection's merge needs for the new key's term.
 template <int RTW, bool DUAL, int EPI, int NKC, bool ROPE, int KSW, bool PRE, int PRE_EPI = kEpiStore,
           bool PRE_QUANT = false, bool PRE_ATTN = false, bool GRP = false, bool ATTN = false, bool NEWKEY = false,
-          bool KW = false>
+          bool KW = false, int MKF = 16>
 __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count, int rg_count, int splits,
                                                  const GemmArgs& pre, int pre_splits,
                                                  const AttnMergeArgs& am = AttnMergeArgs{},
@@ -1693,7 +1696,7 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   __shared__ float pre_sx;
   __shared__ int pre_sums[2];
   if constexpr (PRE_ATTN)
-    attn_merge_quant_slice<NEWKEY>(am, xs, kXsChunk, &pre_sx, pre_sums, blockIdx.x == 0, issue_loads);
+    attn_merge_quant_slice<NEWKEY, MKF>(am, xs, kXsChunk, &pre_sx, pre_sums, blockIdx.x == 0, issue_loads);
   if constexpr (PRE_QUANT) {
     // token 0's row of the slice: K chunks kc0 .. kc0 + NKC - 1 (row 0 of each chunk, unswizzled)
     quant_row_slice<kQuantVecs>(pre.y, pre.in_dim, kc0, NKC, xs, 16 * 256, &pre_sx, pre_sums,
@@ -2099,9 +2102,9 @@ __global__ void __launch_bounds__(256) gemm_skinny_preq_kernel(GemmArgs a, int r
 
 // One token whose activation row is the decode attention's context: every block merges the split
 // partials and quantizes the row (see PRE_ATTN above; NEWKEY: with the new key's own term).
-template <int RTW, int EPI, int NKC, bool NEWKEY, bool KW = false>
+template <int RTW, int EPI, int NKC, bool NEWKEY, bool KW = false, int MKF = 16>
 __global__ void __launch_bounds__(256) gemm_skinny_prea_kernel(GemmArgs a, int rg_count, AttnMergeArgs am) {
-  gemm_skinny_body<RTW, false, EPI, NKC, false, 1, false, kEpiStore, false, true, false, false, NEWKEY, KW>(
+  gemm_skinny_body<RTW, false, EPI, NKC, false, 1, false, kEpiStore, false, true, false, false, NEWKEY, KW, MKF>(
       a, 1, rg_count, 1, a, 0, am);
 }
 
@@ -3439,14 +3442,25 @@ bool launch_gemm_i8_prea(const GemmArgs& a, const AttnMergeArgs& am, hipStream_t
       a.fuse != kFuseNormQuant || !am.part || !am.pml || !am.pos || !am.sx_out || !am.sums_out || am.nsplit < 1 ||
       am.nsplit > kAttnMaxSplits || am.chunk < 1)
     return false;
-  // one 16-row tile per block, K split over its four waves
+  // one 16-row tile per block, K split over its four waves; the merge loads 8, 12 or 16 splits at once
   const int rg_count = a.out_dim / 16;
-  if (am.qkv_new)
-    hipLaunchKernelGGL((gemm_skinny_prea_kernel<1, kEpiStore, 12, true, true>), dim3(8 * ((rg_count + 7) / 8)),
-                       dim3(256), 0, st, a, rg_count, am);
-  else
-    hipLaunchKernelGGL((gemm_skinny_prea_kernel<1, kEpiStore, 12, false, true>), dim3(8 * ((rg_count + 7) / 8)),
-                       dim3(256), 0, st, a, rg_count, am);
+  const dim3 grid(8 * ((rg_count + 7) / 8));
+  auto go = [&](auto newkey, auto kf) {
+    hipLaunchKernelGGL((gemm_skinny_prea_kernel<1, kEpiStore, 12, decltype(newkey)::value, true, decltype(kf)::value>),
+                       grid, dim3(256), 0, st, a, rg_count, am);
+  };
+  using K8 = std::integral_constant<int, 8>;
+  using K12 = std::integral_constant<int, 12>;
+  using K16 = std::integral_constant<int, 16>;
+  if (am.qkv_new) {
+    if (am.nsplit <= 8) go(std::true_type{}, K8{});
+    else if (am.nsplit <= 12) go(std::true_type{}, K12{});
+    else go(std::true_type{}, K16{});
+  } else {
+    if (am.nsplit <= 8) go(std::false_type{}, K8{});
+    else if (am.nsplit <= 12) go(std::false_type{}, K12{});
+    else go(std::false_type{}, K16{});
+  }
   if (!a.defer_reduce) launch_reduce<kEpiStore>(a, 1, st);
   return true;
 }
