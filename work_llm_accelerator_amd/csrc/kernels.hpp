@@ -112,6 +112,12 @@ struct GemmArgs {
   int* gcorr_out;
   const float* gsx;
   const int* gcorr;
+  // One token: the K-split gate/up projection writes max |SiLU.up| of each block's 16 rows to
+  // amax_out[block]; the down projection's quantization prologue (amax_in, amax_n maxima) then reads
+  // only its own K chunks of the row, and one extra block forms the row's scale and limb sums.
+  float* amax_out;
+  const float* amax_in;
+  int amax_n;
 };
 
 // K splits across blocks: at most kMaxSplits splits, only for GEMMs of at most kSplitTokens tokens;

@@ -1195,6 +1195,55 @@ __device__ __forceinline__ void quant_row_slice(const float* __restrict__ x, int
   }
 }
 
+// quant_row_slice for a row whose maximum comes as per-block maxima (amax_n of them, a multiple of 4,
+// at most 1024): the block reads the maxima and its own K chunks kc0 .. kc0 + nkc - 1 of x (nkc <= 16)
+// only, and quantizes those into the slice with the row's scale (the maximum of the maxima, the same
+// value as the whole row's: fmaxf is exact).  The row's limb sums are not formed here (sums_lds: 0).
+template <class Issue>
+__device__ __forceinline__ void quant_chunks_from_maxima(const float* __restrict__ x, const float* __restrict__ amax_in,
+                                                         int amax_n, int kc0, int nkc, uint8_t* xs, int chunk_stride,
+                                                         float* sx_lds, int* sums_lds, Issue&& issue) {
+  __shared__ float red_f[4];
+  const int t = threadIdx.x;
+  const int n4 = nkc * 32;  // float4s of the block's chunks
+  const float4* x4 = reinterpret_cast<const float4*>(x) + kc0 * 32;
+  float4 v[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) v[j] = x4[min(t + 256 * j, n4 - 1)];
+  const float4 m4 = reinterpret_cast<const float4*>(amax_in)[min(t, amax_n / 4 - 1)];
+  __builtin_amdgcn_sched_barrier(0);
+  issue();  // the caller's loads queue behind the row's
+  __builtin_amdgcn_sched_barrier(0);
+  float amax = t < amax_n / 4 ? fmaxf(fmaxf(m4.x, m4.y), fmaxf(m4.z, m4.w)) : 0.0f;
+  amax = block_max4(amax, red_f);
+  const float inv = amax > 0.0f ? (float)kQuantMax / amax : 0.0f;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int k = t + 256 * j;
+    if (k < n4) {
+      const float e[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+      uint32_t hw = 0, lw = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float xf = fminf(fmaxf(rintf(e[q] * inv), -(float)kQuantMax), (float)kQuantMax);
+        const int X = (int)xf;
+        const int H = (X + 128) >> 8;
+        const int L = X - (H << 8);
+        hw |= (uint32_t)(H & 0xFF) << (8 * q);
+        lw |= (uint32_t)(L & 0xFF) << (8 * q);
+      }
+      uint8_t* dst = xs + ((4 * k) >> 7) * chunk_stride + ((4 * k) & 127);
+      *reinterpret_cast<uint32_t*>(dst) = hw;
+      *reinterpret_cast<uint32_t*>(dst + 128) = lw;
+    }
+  }
+  if (t == 0) {
+    *sx_lds = amax > 0.0f ? amax / (float)kQuantMax : 1.0f;
+    sums_lds[0] = 0;
+    sums_lds[1] = 0;
+  }
+}
+
 // Merge weights of one sequence's split-KV decode-attention partials, per head h: M = the maximum of
 // the splits' m (and of the new key's score s_new[h] when has_new), f = exp(m - M), L = sum of l * f
 // (+ exp(s_new[h] - M)), weight = f / L, written over m in ml ([h][kAttnMaxSplits][2]: m, l) for the
@@ -1484,6 +1533,17 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   const int kg = KW ? (threadIdx.x >> 6) : (threadIdx.x >> 8);  // K group of the wave
   const int g = lane >> 4;
   const int col = lane & 15;
+  if constexpr (PRE_QUANT) {
+    // with per-block maxima, the launch's last block forms the row's scale and limb sums (the
+    // reduce step's correction) beside the projection blocks, which quantize only their own chunks
+    if (pre.amax_in && blockIdx.x == gridDim.x - 1) {
+      __shared__ float row_sx;
+      __shared__ int row_sums[2];
+      quant_row_slice<kQuantVecs>(pre.y, pre.in_dim, 0, 0, xs, 16 * 256, &row_sx, row_sums, pre.sx_out,
+                                  pre.sums_out, NoIssue{});
+      return;
+    }
+  }
   int rg_b, z_b, tt_b, ks = -1;  // ks: key split of an ATTN query-head block (-1: none)
   if constexpr (ATTN) {
     // ids 0..3: the k and v heads; 4..7: none; from 8 on, the six query heads of one (KV head, key split)
@@ -1699,8 +1759,12 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
     attn_merge_quant_slice<NEWKEY, MKF>(am, xs, kXsChunk, &pre_sx, pre_sums, blockIdx.x == 0, issue_loads);
   if constexpr (PRE_QUANT) {
     // token 0's row of the slice: K chunks kc0 .. kc0 + NKC - 1 (row 0 of each chunk, unswizzled)
-    quant_row_slice<kQuantVecs>(pre.y, pre.in_dim, kc0, NKC, xs, 16 * 256, &pre_sx, pre_sums,
-                                blockIdx.x == 0 ? pre.sx_out : nullptr, pre.sums_out, issue_loads);
+    if (pre.amax_in)
+      quant_chunks_from_maxima(pre.y, pre.amax_in, pre.amax_n, kc0, NKC, xs, 16 * 256, &pre_sx, pre_sums,
+                               issue_loads);
+    else
+      quant_row_slice<kQuantVecs>(pre.y, pre.in_dim, kc0, NKC, xs, 16 * 256, &pre_sx, pre_sums,
+                                  blockIdx.x == 0 ? pre.sx_out : nullptr, pre.sums_out, issue_loads);
   }
   if constexpr (PRE) {
     // token 0's row of the slice (K chunk c at xs + c * kXsChunk, row 0 of the chunk, unswizzled), made
@@ -2081,6 +2145,19 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
 #pragma unroll
         for (int q = 0; q < 4; ++q) o[q] = round_bf16(o[q]);
       *reinterpret_cast<float4*>(a.y + (size_t)tok * a.y_stride + row0) = make_float4(o[0], o[1], o[2], o[3]);
+    }
+    if constexpr (KW && EPI == kEpiSiluMul) {
+      if (a.amax_out) {  // max |SiLU.up| of the block's rows (lanes 0, 16, 32, 48 hold token 0's)
+        float m = 0.0f;
+#pragma unroll
+        for (int r = 0; r < RTW; ++r)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (ok[r]) m = fmaxf(m, fabsf(y[r][q]));
+        m = fmaxf(m, __shfl_xor(m, 16, 64));
+        m = fmaxf(m, __shfl_xor(m, 32, 64));
+        if (lane == 0) a.amax_out[rg] = m;
+      }
     }
   }
 }
@@ -3505,8 +3582,11 @@ bool launch_gemm_i8_preq(const GemmArgs& a, const GemmArgs& pre, hipStream_t st)
   // blocks (every block quantizes the whole 8960-wide row for its scale, so fewer blocks than the other
   // one-token projections: 480 blocks of one tile, or 160 of three, were slower)
   const int rg_count = a.out_dim / 32;
-  hipLaunchKernelGGL((gemm_skinny_preq_kernel<2, kEpiResidual, 14, true>), dim3(8 * ((rg_count * kSplits + 7) / 8)),
-                     dim3(256), 0, st, a, rg_count, kSplits, pre);
+  if (pre.amax_in && (pre.amax_n < 4 || pre.amax_n % 4 != 0 || pre.amax_n > 1024)) return false;
+  // (with per-block maxima: one more block, the row's scale and limb sums)
+  hipLaunchKernelGGL((gemm_skinny_preq_kernel<2, kEpiResidual, 14, true>),
+                     dim3(8 * ((rg_count * kSplits + 7) / 8) + (pre.amax_in ? 1 : 0)), dim3(256), 0, st, a, rg_count,
+                     kSplits, pre);
   if (!(a.defer_reduce && a.fuse == kFuseNormQuant)) launch_reduce<kEpiResidual>(a, kSplits, st);
   return true;
 }

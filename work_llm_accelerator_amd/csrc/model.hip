@@ -97,6 +97,7 @@ struct qwen_hip_model {
     float* gsx;     //   scales and offset terms
     int* gcorr;
     const int* zero_sums;  // kSkinnyTokens x (0, 0): the limb sums of code whose offsets are applied per group
+    float* gmax;           // one token: max |SiLU.up| of each 16-row block of the gate/up projection
   };
   // Fixed region at the start of the workspace: the decode attention's arrival counters, then the zero
   // limb sums; both are zeroed once per workspace buffer and never written otherwise (the counters
@@ -128,6 +129,7 @@ struct qwen_hip_model {
     const size_t o_gxq = take(xq_bytes(gtok, QWEN_INTERMEDIATE));
     const size_t o_gsx = take(gtok * (QWEN_INTERMEDIATE / 64) * 4u);
     const size_t o_gcorr = take(gtok * (QWEN_INTERMEDIATE / 64) * 4u);
+    const size_t o_gmax = take((QWEN_INTERMEDIATE / 16) * 4u);
     char* b = static_cast<char*>(ws.get(off));
     unsigned* arr = reinterpret_cast<unsigned*>(b + o_arr);
     if (ws.generation != arrivals_ready) {  // fresh buffer: arm the counters and zero the sums once
@@ -142,7 +144,7 @@ struct qwen_hip_model {
               reinterpret_cast<float*>(b + o_part), reinterpret_cast<float2*>(b + o_pml), arr,
               reinterpret_cast<float*>(b + o_splitk), reinterpret_cast<uint8_t*>(b + o_kvt),
               reinterpret_cast<int8_t*>(b + o_gxq), reinterpret_cast<float*>(b + o_gsx), reinterpret_cast<int*>(b + o_gcorr),
-              reinterpret_cast<const int*>(b + o_zs)};
+              reinterpret_cast<const int*>(b + o_zs), reinterpret_cast<float*>(b + o_gmax)};
   }
 
   // Plain scratch of `bytes` in the workspace, past the fixed region.
@@ -372,8 +374,9 @@ struct qwen_hip_model {
         const AttnMergeArgs am{w.part, w.pml, pos, plan.nsplit, plan.chunk, max_keys, w.sx, w.sums,
                                fuse_attn ? w.qkv : nullptr};
         if (!launch_gemm_i8_prea(oa, am, stream)) throw std::runtime_error("O with the attention merge: bad shape");
-        const GemmArgs ga = args(w, B, QWEN_HIDDEN, QWEN_INTERMEDIATE, f.gate, f.sw_gate, nullptr, w.s,
-                                 QWEN_INTERMEDIATE, f.up, f.sw_up);
+        GemmArgs ga = args(w, B, QWEN_HIDDEN, QWEN_INTERMEDIATE, f.gate, f.sw_gate, nullptr, w.s, QWEN_INTERMEDIATE,
+                           f.up, f.sw_up);
+        ga.amax_out = w.gmax;  // the down projection's blocks take the row's maximum from these
         if (!launch_gemm_i8_pre(ga, oa, kEpiStore, 1, stream))
           throw std::runtime_error("gate/up with the O reduce: bad shape");
       } else {
@@ -403,6 +406,8 @@ struct qwen_hip_model {
         sq.in_dim = QWEN_INTERMEDIATE;
         sq.sx_out = w.sx;
         sq.sums_out = w.sums;
+        sq.amax_in = w.gmax;
+        sq.amax_n = QWEN_INTERMEDIATE / 16;
         fn.defer_reduce = fuse_next ? 1 : 0;
         const GemmArgs da = args(w, B, QWEN_INTERMEDIATE, QWEN_HIDDEN, f.down, f.sw_down, nullptr, hidden,
                                  QWEN_HIDDEN, nullptr, nullptr, w.att, round, 0, fuse_next ? &fn : nullptr);
