@@ -1670,10 +1670,16 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   int sh_l = 0, sl_l = 0;
   float gsv[GRP ? 2 * KC : 1];  // GRP: scales and offset terms of the lane's token's 2*KC groups
   int gcv[GRP ? 2 * KC : 1];
-  // The decode SiLU's exp table, copied to LDS before the MFMAs: read from constant memory in the
-  // epilogue, each of a lane's SiLU evaluations waited on one more memory round trip (several tokens;
-  // with one token the copy cost as much as it saved).
-  constexpr bool kTab = EPI == kEpiSiluMul && !kMade;
+  // One token of the gate/up projection with K split over the waves (KW): only column 0 of the
+  // products is a token, its 16 rows per matrix four to a lane in lanes 0, 16, 32, 48.  The K groups
+  // leave those rows in LDS and lane r < 16 of wave 0 finishes row r: one SiLU per lane, not four in
+  // a row (its row scales loaded per lane, sw_row and sw2_row).
+  constexpr bool kRowLane = KW && EPI == kEpiSiluMul && DUAL && RTW == 1;
+  float sw_row = 0.0f, sw2_row = 0.0f;
+  // The decode SiLU's exp table, copied to LDS before the epilogue: read from constant memory there,
+  // each of a lane's SiLU evaluations waited on one more memory round trip (several tokens; with one
+  // token and four SiLUs per lane the copy cost as much as it saved).
+  constexpr bool kTab = EPI == kEpiSiluMul && (!kMade || kRowLane);
   __shared__ uint64_t exp_tab[kTab ? 32 : 1];
   uint64_t tab_v = 0;
 #pragma unroll
@@ -1717,14 +1723,20 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
     constexpr bool kBias = EPI == kEpiStore && !DUAL;
     const float* bsrc = kBias && a.bias ? a.bias : a.sw;
     const uint32_t bmask = kBias && a.bias ? 0xFFFFFFFFu : 0u;
+    if constexpr (kRowLane) {
+      const int row = (ok[0] ? row_tile(0) : 0) * 16 + (lane & 15);
+      sw_row = a.sw[row];
+      sw2_row = a.sw2[row];
+    } else {
 #pragma unroll
-    for (int r = 0; r < RTW; ++r) {
-      const int row0 = (ok[r] ? row_tile(r) : 0) * 16 + 4 * g;
+      for (int r = 0; r < RTW; ++r) {
+        const int row0 = (ok[r] ? row_tile(r) : 0) * 16 + 4 * g;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        swv[r][q] = a.sw[row0 + q];
-        sw2v[r][q] = DUAL ? a.sw2[row0 + q] : 0.0f;
-        biasv[r][q] = kBias ? __uint_as_float(__float_as_uint(bsrc[row0 + q]) & bmask) : 0.0f;
+        for (int q = 0; q < 4; ++q) {
+          swv[r][q] = a.sw[row0 + q];
+          sw2v[r][q] = DUAL ? a.sw2[row0 + q] : 0.0f;
+          biasv[r][q] = kBias ? __uint_as_float(__float_as_uint(bsrc[row0 + q]) & bmask) : 0.0f;
+        }
       }
     }
     if constexpr (!kMade) {
@@ -1869,7 +1881,49 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
       }
   }
 
-  if constexpr (KG > 1) {
+  if constexpr (kRowLane) {
+    __syncthreads();  // every wave's slice reads are done: the slice buffer takes the sums
+    int* red = reinterpret_cast<int*>(xs);  // [K group][matrix d][limb][row 0..15], exact int32
+    if (col == 0) {
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+        *reinterpret_cast<int4*>(red + kg * 64 + (2 * d) * 16 + 4 * g) =
+            make_int4(accH[0][d][0], accH[0][d][1], accH[0][d][2], accH[0][d][3]);
+        *reinterpret_cast<int4*>(red + kg * 64 + (2 * d + 1) * 16 + 4 * g) =
+            make_int4(accL[0][d][0], accL[0][d][1], accL[0][d][2], accL[0][d][3]);
+      }
+    }
+    if (threadIdx.x < 32) exp_tab[threadIdx.x] = tab_v;
+    __syncthreads();
+    if (kg > 0) return;
+    const int row = lane & 15;  // lanes 16.. repeat rows 0..15 (no stores)
+    int hs[2] = {0, 0}, ls[2] = {0, 0};
+#pragma unroll
+    for (int j = 0; j < KG; ++j)
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+        hs[d] += red[j * 64 + (2 * d) * 16 + row];
+        ls[d] += red[j * 64 + (2 * d + 1) * 16 + row];
+      }
+    const double sx = (double)pre_sx;
+    const int sh8 = 8 * pre_sums[0], sl8 = 8 * pre_sums[1];
+    const float v = (float)(((double)(hs[0] - sh8) * 256.0 + (double)(ls[0] - sl8)) * sx) * sw_row;
+    const float u = (float)(((double)(hs[1] - sh8) * 256.0 + (double)(ls[1] - sl8)) * sx) * sw2_row;
+    const float yv = silu_decode(v, exp_tab) * u;
+    if (!ok[0]) return;
+    if (lane < 16) a.y[(size_t)tok0 * a.y_stride + row_tile(0) * 16 + row] = yv;
+    if (a.amax_out) {  // max |SiLU.up| of the block's 16 rows: the DPP row max of lanes 0..15
+      float m = fmaxf(0.0f, fabsf(yv));
+      m = fmaxf(m, __int_as_float(dpp_i<0xB1>(__float_as_int(m))));
+      m = fmaxf(m, __int_as_float(dpp_i<0x4E>(__float_as_int(m))));
+      m = fmaxf(m, __int_as_float(dpp_i<0x124>(__float_as_int(m))));
+      m = fmaxf(m, __int_as_float(dpp_i<0x128>(__float_as_int(m))));
+      if (lane == 0) a.amax_out[rg] = m;
+    }
+    return;
+  }
+
+  if constexpr (KG > 1 && !kRowLane) {
     // K groups 1.. hand their exact int32 sums to K group 0 through LDS (the slice buffer, now read):
     // region (row wave, or with KW the K group's) of RTW * D * 8 * 64 ints each.
     __syncthreads();
@@ -2146,7 +2200,7 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
         for (int q = 0; q < 4; ++q) o[q] = round_bf16(o[q]);
       *reinterpret_cast<float4*>(a.y + (size_t)tok * a.y_stride + row0) = make_float4(o[0], o[1], o[2], o[3]);
     }
-    if constexpr (KW && EPI == kEpiSiluMul) {
+    if constexpr (KW && EPI == kEpiSiluMul && !kRowLane) {
       if (a.amax_out) {  // max |SiLU.up| of the block's rows (lanes 0, 16, 32, 48 hold token 0's)
         float m = 0.0f;
 #pragma unroll
@@ -3497,7 +3551,7 @@ bool launch_gemm_i8_pre(const GemmArgs& a, const GemmArgs& pre, int pre_epi, int
   if (a.tokens != 1 || a.in_dim != QWEN_HIDDEN || pre.out_dim != QWEN_HIDDEN || pre.fuse != kFuseNormQuant ||
       pre.tokens != 1 || pre_splits < 1 || pre_splits > kMaxSplits)
     return false;
-  if (a.wp2 && a.out_dim % 64 == 0 && pre_epi == kEpiStore) {  // gate/up after the O projection
+  if (a.wp2 && a.out_dim % 64 == 0 && pre_epi == kEpiStore && !a.prefill_silu) {  // decode gate/up after O
     // one 16-row tile of both matrices per block, K split over its four waves
     const int rg_count = a.out_dim / 16;
     hipLaunchKernelGGL((gemm_skinny_pre_kw_kernel<1, true, kEpiSiluMul, 12, kEpiStore>),
