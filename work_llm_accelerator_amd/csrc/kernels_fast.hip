@@ -2216,6 +2216,30 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   }
 }
 
+// Byte size of a kernel's explicit arguments T..., laid out in order at their natural alignments.
+template <class... T>
+constexpr int kernarg_bytes() {
+  int off = 0;
+  ((off = (off + (int)alignof(T) - 1) / (int)alignof(T) * (int)alignof(T) + (int)sizeof(T)), ...);
+  return off;
+}
+// Loads one dword of every 64-byte line of the first BYTES bytes of the kernel's argument segment,
+// all at once, and waits for them.  The compiler issues the argument loads where each value is first
+// needed, in batches with a wait between them, and the segment is written anew for every launch, so
+// each batch was a memory round trip of its own before the first global load; after this one round
+// trip the later argument loads hit the scalar cache.
+template <int BYTES>
+__device__ __forceinline__ void touch_kernargs() {
+  using KPtr = const __attribute__((address_space(4))) uint32_t*;
+  KPtr kp = (KPtr)__builtin_amdgcn_kernarg_segment_ptr();
+  constexpr int kLines = (BYTES + 63) / 64;
+  uint32_t v[kLines];
+#pragma unroll
+  for (int i = 0; i < kLines; ++i) v[i] = kp[16 * i];
+#pragma unroll
+  for (int i = 0; i < kLines; ++i) asm volatile("" ::"s"(v[i]));
+}
+
 template <int RTW, bool DUAL, int EPI, int NKC, bool ROPE, int KSW, bool GRP = false>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(3)))
 gemm_skinny_kernel(GemmArgs a, int tt_count, int rg_count, int splits) {
@@ -2227,6 +2251,7 @@ gemm_skinny_kernel(GemmArgs a, int tt_count, int rg_count, int splits) {
 // KW: the block's waves split K).
 template <int RTW, int EPI, int NKC, bool KW = false>
 __global__ void __launch_bounds__(256) gemm_skinny_preq_kernel(GemmArgs a, int rg_count, int splits, GemmArgs pre) {
+  touch_kernargs<kernarg_bytes<GemmArgs, int, int, GemmArgs>()>();
   gemm_skinny_body<RTW, false, EPI, NKC, false, 1, false, kEpiStore, true, false, false, false, false, KW>(
       a, 1, rg_count, splits, pre, 0);
 }
@@ -2235,6 +2260,7 @@ __global__ void __launch_bounds__(256) gemm_skinny_preq_kernel(GemmArgs a, int r
 // partials and quantizes the row (see PRE_ATTN above; NEWKEY: with the new key's own term).
 template <int RTW, int EPI, int NKC, bool NEWKEY, bool KW = false, int MKF = 16>
 __global__ void __launch_bounds__(256) gemm_skinny_prea_kernel(GemmArgs a, int rg_count, AttnMergeArgs am) {
+  touch_kernargs<kernarg_bytes<GemmArgs, int, AttnMergeArgs>()>();
   gemm_skinny_body<RTW, false, EPI, NKC, false, 1, false, kEpiStore, false, true, false, false, NEWKEY, KW, MKF>(
       a, 1, rg_count, 1, a, 0, am);
 }
@@ -2249,6 +2275,7 @@ __global__ void __launch_bounds__(256) gemm_skinny_attn_kernel(GemmArgs a, AttnF
 
 __global__ void __launch_bounds__(256) gemm_skinny_pre_attn_kernel(GemmArgs a, GemmArgs pre, int pre_splits,
                                                                    AttnFuseArgs af) {
+  touch_kernargs<kernarg_bytes<GemmArgs, GemmArgs, int, AttnFuseArgs>()>();
   gemm_skinny_body<2, false, kEpiStore, 12, true, 1, true, kEpiResidual, false, false, false, true>(
       a, 1, QWEN_QKV_ROWS / 128, 1, pre, pre_splits, AttnMergeArgs{}, af);
 }
@@ -2256,6 +2283,7 @@ __global__ void __launch_bounds__(256) gemm_skinny_pre_attn_kernel(GemmArgs a, G
 // One token, with the previous projection's reduce step redone by every block (see PRE above).
 template <int RTW, bool DUAL, int EPI, int NKC, bool ROPE, int PRE_EPI>
 __global__ void __launch_bounds__(256) gemm_skinny_pre_kernel(GemmArgs a, int rg_count, GemmArgs pre, int pre_splits) {
+  touch_kernargs<kernarg_bytes<GemmArgs, int, GemmArgs, int>()>();
   gemm_skinny_body<RTW, DUAL, EPI, NKC, ROPE, 1, true, PRE_EPI>(a, 1, rg_count, 1, pre, pre_splits);
 }
 
@@ -2263,6 +2291,7 @@ __global__ void __launch_bounds__(256) gemm_skinny_pre_kernel(GemmArgs a, int rg
 template <int RTW, bool DUAL, int EPI, int NKC, int PRE_EPI>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
 gemm_skinny_pre_kw_kernel(GemmArgs a, int rg_count, GemmArgs pre, int pre_splits) {
+  touch_kernargs<kernarg_bytes<GemmArgs, int, GemmArgs, int>()>();
   gemm_skinny_body<RTW, DUAL, EPI, NKC, false, 1, true, PRE_EPI, false, false, false, false, false, true>(
       a, 1, rg_count, 1, pre, pre_splits);
 }
@@ -2610,8 +2639,6 @@ __device__ __forceinline__ void reduce_norm_quant_row_w4(const GemmArgs& a, int 
   const float4* r4 = EPI == kEpiResidual ? reinterpret_cast<const float4*>(a.resid)
                                          : (a.bias ? reinterpret_cast<const float4*>(a.bias) : sw4);
   const float4* w4 = has_w ? reinterpret_cast<const float4*>(a.norm_w) : sw4;
-  const int sum_h = a.sums[0], sum_l = a.sums[1];
-  const float sx_tok = a.sx[0];
   float4 acc[2], sw[2], ad[2], wn[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
@@ -2620,16 +2647,31 @@ __device__ __forceinline__ void reduce_norm_quant_row_w4(const GemmArgs& a, int 
     wn[j] = w4[f[j]];
     acc[j] = make_float4(0, 0, 0, 0);
   }
+  // The first ZB splits' loads are issued unconditionally (without splits from a valid stand-in, their
+  // values unused), then the token's limb sums and scale as vector loads (a lane-varying zero index),
+  // then `issue`.  Behind a run-time branch, or with the sums as scalar loads, the partial loads waited
+  // for the sums' memory round trip: the wait for the kernel arguments that address the partials
+  // counted the scalar loads in flight too.
+  const float4* pt0 = splits > 0 ? pt : sw4;
+  const int zlast = max(splits, 1) - 1;
+  float4 pz[ZB][2];
+#pragma unroll
+  for (int u = 0; u < ZB; ++u)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) pz[u][j] = pt0[(size_t)min(u, zlast) * zstride4 + f[j]];
+  int lz;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(lz));
+  const int sum_h = a.sums[lz], sum_l = a.sums[lz + 1];
+  const float sx_tok = a.sx[lz];
+  __builtin_amdgcn_sched_barrier(0);
+  issue();
+  __builtin_amdgcn_sched_barrier(0);
   for (int z0 = 0; z0 < splits; z0 += ZB) {
-    float4 pz[ZB][2];
+    if (z0 > 0) {
 #pragma unroll
-    for (int u = 0; u < ZB; ++u)
+      for (int u = 0; u < ZB; ++u)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) pz[u][j] = pt[(size_t)min(z0 + u, splits - 1) * zstride4 + f[j]];
-    if (z0 == 0) {
-      __builtin_amdgcn_sched_barrier(0);
-      issue();
-      __builtin_amdgcn_sched_barrier(0);
+        for (int j = 0; j < 2; ++j) pz[u][j] = pt[(size_t)min(z0 + u, splits - 1) * zstride4 + f[j]];
     }
 #pragma unroll
     for (int u = 0; u < ZB; ++u)
@@ -2642,7 +2684,6 @@ __device__ __forceinline__ void reduce_norm_quant_row_w4(const GemmArgs& a, int 
           acc[j].w += pz[u][j].w;
         }
   }
-  if (splits < 1) issue();
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     if (!has_add) ad[j] = make_float4(0, 0, 0, 0);
