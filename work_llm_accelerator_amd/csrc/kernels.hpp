@@ -124,6 +124,9 @@ struct GemmArgs {
 // the workspace holds kMaxSplits x kSplitTokens x out floats.
 constexpr int kMaxSplits = 16;
 constexpr int kSplitTokens = 256;
+// K splits of the one-token down projection (8960 = 5 x 14 chunks of 128), whose partials the next
+// layer's Q/K/V blocks reduce in their prologue.
+constexpr int kPreResidualSplits = 5;
 // Decode GEMMs of at most kSkinnyTokens tokens (in_dim 1536 or 8960) run the skinny kernels.
 constexpr int kSkinnyTokens = 64;
 inline size_t splitk_bytes(size_t out) { return (size_t)kMaxSplits * kSplitTokens * out * 4u; }

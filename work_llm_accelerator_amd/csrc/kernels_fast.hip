@@ -1626,11 +1626,12 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   // block issues the same number of loads (the k and v heads and empty splits load row 0, which nobody
   // reads), so the wave's load counts stay exact; keys past the split's last one reload it (masked).
   constexpr int kKvLoads = ATTN ? 2 * (kFusedAttnChunk / 4) / 2 : 0;  // per wave: 8 of K, 8 of V
+  int pos_v = 0;  // ATTN after a PRE prologue: the position, loaded among the scalars
   auto issue_kv = [&]() {
     if constexpr (ATTN) {
       // after every other load of the wave: the addresses wait for the position
       __builtin_amdgcn_sched_barrier(0);
-      P = load_uniform_i32(a.pos);
+      P = PRE ? __builtin_amdgcn_readfirstlane(pos_v) : load_uniform_i32(a.pos);
       load_rope();
       const int t0 = ks * kFusedAttnChunk;
       const int t1 = min(hist_end(), t0 + kFusedAttnChunk);
@@ -1756,14 +1757,23 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
       }
     }
     if constexpr (kTab) tab_v = kExp2Tab[lane & 31];
+    if constexpr (ATTN && PRE) {
+      int lz;
+      asm volatile("v_mov_b32 %0, 0" : "=v"(lz));  // a vector load: the scalar one waited on lgkmcnt
+      pos_v = a.pos[lz];
+    }
   };
   // With a made slice (kMade) the weights and scalars are issued inside the prologue, after the
   // prologue's own loads: a wave's loads return in order, so the prologue's few loads must not queue
   // behind the weights.
+  // (ATTN after a PRE prologue: the RoPE and K/V rows are issued once the prologue is done and every
+  // other load has landed.  The K/V rows are direct loads into LDS, and while one is in flight the
+  // compiler waits for every load before any use of a loaded register: issued with the weights, the
+  // prologue's first add waited for the whole weight stream, and with it the norm and quantization.)
   auto issue_loads = [&]() {
     issue_weights();
     issue_scalars();
-    issue_kv();
+    if constexpr (!(ATTN && PRE)) issue_kv();
   };
   __shared__ float pre_sx;
   __shared__ int pre_sums[2];
@@ -1783,14 +1793,24 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
     // by the block's four waves together (three block barriers): the O projection's one K group (store
     // epilogue) or the down projection's five splits (residual).  (One wave alone, with the other
     // three issuing their loads, took 2.2 us of arithmetic on the launch's critical path.)
-    reduce_norm_quant_row_w4<PRE_EPI, PRE_EPI == kEpiResidual ? 5 : 1>(
+    reduce_norm_quant_row_w4<PRE_EPI, PRE_EPI == kEpiResidual ? kPreResidualSplits : 1>(
         pre, pre_splits, reinterpret_cast<int8_t*>(xs), kXsChunk, &pre_sx, pre_sums, blockIdx.x == 0 && pre.y,
         issue_loads);
   }
   if constexpr (kMade) {
     __builtin_amdgcn_sched_barrier(0);  // every load above is in flight before any use
-    wait_vmcnt<kKvLoads>();  // ATTN: the K/V rows (the wave's last loads) land during the MFMAs
-    __syncthreads();
+    if constexpr (ATTN && PRE) {
+      wait_vmcnt<0>();  // the weights and the position: the MFMAs then wait for nothing
+      issue_kv();       // the RoPE and K/V rows land during the MFMAs
+      // the slice's LDS writes are complete before the barrier (a __syncthreads here would also wait
+      // for the direct loads into LDS just issued)
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+    } else {
+      wait_vmcnt<kKvLoads>();  // ATTN: the K/V rows (the wave's last loads) land during the MFMAs
+      __syncthreads();
+    }
   } else {
     // Scalars, then the activation slice, then the weights in chunk order.  A wave's loads return in
     // order, so once at most the weight loads are outstanding its part of the slice has landed, and
@@ -2647,8 +2667,8 @@ __device__ __forceinline__ void reduce_norm_quant_row_w4(const GemmArgs& a, int 
     wn[j] = w4[f[j]];
     acc[j] = make_float4(0, 0, 0, 0);
   }
-  // The first ZB splits' loads are issued unconditionally (without splits from a valid stand-in, their
-  // values unused), then the token's limb sums and scale as vector loads (a lane-varying zero index),
+  // splits <= ZB (the launchers check).  The splits' loads are issued unconditionally (without splits
+  // from a valid stand-in, their values unused), then the token's limb sums and scale as vector loads (a lane-varying zero index),
   // then `issue`.  Behind a run-time branch, or with the sums as scalar loads, the partial loads waited
   // for the sums' memory round trip: the wait for the kernel arguments that address the partials
   // counted the scalar loads in flight too.
@@ -2666,23 +2686,19 @@ __device__ __forceinline__ void reduce_norm_quant_row_w4(const GemmArgs& a, int 
   __builtin_amdgcn_sched_barrier(0);
   issue();
   __builtin_amdgcn_sched_barrier(0);
-  for (int z0 = 0; z0 < splits; z0 += ZB) {
-    if (z0 > 0) {
+  // Added as selects, in split order (adding +0 leaves a sum that started at +0 unchanged).  (A loop
+  // over further batches, reloading pz, made the compiler wait for every load in flight, `issue`'s
+  // weights included, before the first add.)
 #pragma unroll
-      for (int u = 0; u < ZB; ++u)
+  for (int u = 0; u < ZB; ++u) {
+    const bool live = u < splits;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) pz[u][j] = pt[(size_t)min(z0 + u, splits - 1) * zstride4 + f[j]];
+    for (int j = 0; j < 2; ++j) {
+      acc[j].x += live ? pz[u][j].x : 0.0f;
+      acc[j].y += live ? pz[u][j].y : 0.0f;
+      acc[j].z += live ? pz[u][j].z : 0.0f;
+      acc[j].w += live ? pz[u][j].w : 0.0f;
     }
-#pragma unroll
-    for (int u = 0; u < ZB; ++u)
-      if (z0 + u < splits)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          acc[j].x += pz[u][j].x;
-          acc[j].y += pz[u][j].y;
-          acc[j].z += pz[u][j].z;
-          acc[j].w += pz[u][j].w;
-        }
   }
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
@@ -3590,7 +3606,7 @@ static void launch_gemm_epi(const GemmArgs& a, hipStream_t st) {
 
 bool launch_gemm_i8_pre(const GemmArgs& a, const GemmArgs& pre, int pre_epi, int pre_splits, hipStream_t st) {
   if (a.tokens != 1 || a.in_dim != QWEN_HIDDEN || pre.out_dim != QWEN_HIDDEN || pre.fuse != kFuseNormQuant ||
-      pre.tokens != 1 || pre_splits < 1 || pre_splits > kMaxSplits)
+      pre.tokens != 1 || pre_splits < 1 || pre_splits > (pre_epi == kEpiResidual ? kPreResidualSplits : 1))
     return false;
   if (a.wp2 && a.out_dim % 64 == 0 && pre_epi == kEpiStore && !a.prefill_silu) {  // decode gate/up after O
     // one 16-row tile of both matrices per block, K split over its four waves
@@ -3661,7 +3677,7 @@ bool launch_gemm_i8_pre_attn(const GemmArgs& a, const GemmArgs& pre, int pre_spl
   // pre_splits == 0: the row is pre.resid itself (the first layer of a range: RMSNorm and quantization
   // of the input row, pre.sums / pre.sx pointing at zeros, nothing written back)
   if (!fused_attn_ok(a, af) || pre.out_dim != QWEN_HIDDEN || pre.fuse != kFuseNormQuant || pre.tokens != 1 ||
-      pre_splits < 0 || pre_splits > kMaxSplits || (pre_splits == 0 && (!pre.resid || pre.y || pre.y_raw)))
+      pre_splits < 0 || pre_splits > kPreResidualSplits || (pre_splits == 0 && (!pre.resid || pre.y || pre.y_raw)))
     return false;
   hipLaunchKernelGGL(gemm_skinny_pre_attn_kernel, dim3(fused_attn_blocks(af.nsplit)), dim3(256), 0, st, a, pre,
                      pre_splits, af);
@@ -3672,7 +3688,7 @@ bool launch_gemm_i8_preq(const GemmArgs& a, const GemmArgs& pre, hipStream_t st)
   if (a.tokens != 1 || a.in_dim != QWEN_INTERMEDIATE || a.out_dim != QWEN_HIDDEN || a.wp2 || !a.part ||
       pre.in_dim != a.in_dim || !pre.y || !pre.sx_out || !pre.sums_out)
     return false;
-  constexpr int kSplits = 5;  // 14 K chunks each, as the separate-quantization path
+  constexpr int kSplits = kPreResidualSplits;  // 14 K chunks each, as the separate-quantization path
   // two 16-row tiles per block, their 14 K chunks split over the block's four waves (4, 4, 3, 3): 240
   // blocks (every block quantizes the whole 8960-wide row for its scale, so fewer blocks than the other
   // one-token projections: 480 blocks of one tile, or 160 of three, were slower)

@@ -322,8 +322,8 @@ struct qwen_hip_model {
           // projection finishes that row (residual, bf16 rounding, this layer's RMSNorm, quantization)
           const GemmArgs qa = args(w, B, QWEN_HIDDEN, (int)kQkvRows, f.qkv, f.sw_qkv, f.b_qkv, w.qkv, kQkvRows,
                                    nullptr, nullptr, nullptr, 0, 0, &fq);
-          if (fuse_attn ? !launch_gemm_i8_pre_attn(qa, down_pending, 5, af, stream)
-                        : !launch_gemm_i8_pre(qa, down_pending, kEpiResidual, 5, stream))
+          if (fuse_attn ? !launch_gemm_i8_pre_attn(qa, down_pending, kPreResidualSplits, af, stream)
+                        : !launch_gemm_i8_pre(qa, down_pending, kEpiResidual, kPreResidualSplits, stream))
             throw std::runtime_error("Q/K/V with the down reduce: bad shape");
         } else if (fuse_attn) {
           // the range's first layer: every block normalizes and quantizes the input row itself (a
