@@ -1835,6 +1835,7 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   const bool rope_in = ROPE && P >= 0 && P < a.limit;
   if constexpr (ROPE && !ATTN) load_rope();
   v4i accH[RTW][D], accL[RTW][D];
+  constexpr bool kPair = (kMade || ATTN) && !GRP;  // one token
 #pragma unroll
   for (int r = 0; r < RTW; ++r)
 #pragma unroll
@@ -1882,6 +1883,27 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
       continue;
     }
     if (KW && NKC % KG != 0 && kg * KC + c >= NKC) break;  // wave-uniform: the wave's chunks past NKC
+    if constexpr (kPair) {
+      // One token (a made slice, or ATTN): its two limbs go in as two columns of one product, the H
+      // limbs in the even columns and the L limbs in the odd ones, so a chunk takes two products per
+      // tile and matrix instead of four (the 16 columns would otherwise all hold the one token, or
+      // nothing).  accH takes the chunk's first 64 K and accL its second 64 (two accumulator chains);
+      // their sum's columns 0 and 1 are the token's H and L sums.
+      const uint8_t* xr = xs + (kg * KC + c) * kXsChunk;  // row 0 of the chunk, unswizzled
+      const int sb = (col & 1) << 3;
+      const v4i b1 = *reinterpret_cast<const v4i*>(xr + ((sb + 2 * g) << 4));
+      const v4i b2 = *reinterpret_cast<const v4i*>(xr + ((sb + 2 * g + 1) << 4));
+#pragma unroll
+      for (int r = 0; r < RTW; ++r)
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+          v4i a1, a2;
+          unpack16(wv[r][d][c], a1, a2);
+          accH[r][d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, accH[r][d], 0, 0, 0);
+          accL[r][d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2, b2, accL[r][d], 0, 0, 0);
+        }
+      continue;
+    }
     const int colr = ATTN ? 0 : col;  // ATTN: every column reads token 0's row
     const uint8_t* xr = xs + ((kg * KC + c) * kXsRows + colr) * 256;
     const v4i bh1 = *reinterpret_cast<const v4i*>(xr + (((2 * g) ^ colr) << 4));
@@ -1899,6 +1921,19 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
         accL[r][d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bl1, accL[r][d], 0, 0, 0);
         accL[r][d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2, bl2, accL[r][d], 0, 0, 0);
       }
+  }
+  if constexpr (kPair) {
+    // column 0 of the sum: the H sums; column 1 (the lane to the right): the L sums
+#pragma unroll
+    for (int r = 0; r < RTW; ++r)
+#pragma unroll
+      for (int d = 0; d < D; ++d)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int t = accH[r][d][q] + accL[r][d][q];
+          accH[r][d][q] = t;
+          accL[r][d][q] = dpp_i<0xB1>(t);
+        }
   }
 
   if constexpr (kRowLane) {
