@@ -141,6 +141,9 @@ void launch_gemm_i8(const GemmArgs& a, int epi, hipStream_t st);
 // SiLU·up after the O projection (pre_epi kEpiStore), the fused Q/K/V + RoPE after the down
 // projection (pre_epi kEpiResidual).  Returns false (nothing launched) for other shapes.
 bool launch_gemm_i8_pre(const GemmArgs& a, const GemmArgs& pre, int pre_epi, int pre_splits, hipStream_t st);
+// Row-maxima count that the one-token gate/up projection (launch_gemm_i8_pre with wp2 and amax_out)
+// writes for an out_dim-row output: one per block.
+int gate_up_maxima_count(int out_dim);
 // The down projection (+ residual) of one token whose activation row is the fp32 row pre.y
 // (pre.in_dim = 8960 wide): every block quantizes that row for its own K chunks (as norm_quant_kernel
 // without a norm), block 0 writes its scale and limb sums to pre.sx_out / pre.sums_out (= a.sx,

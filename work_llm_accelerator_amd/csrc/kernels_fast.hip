@@ -1335,7 +1335,14 @@ __device__ __forceinline__ void attn_merge_quant_slice(const AttnMergeArgs& am, 
             am.part + ((size_t)(f >> 5) * nsplit + min(s0 + j, nsplit - 1)) * QWEN_HEAD_DIM + 4 * (f & 31));
     }
   };
-  const int p0 = am.pos[0];
+  // the position as a vector load whose register is held until it is needed (read back early, its
+  // register was reused and the wait for it held the rest of the loads back by a memory round trip)
+  int p0v;
+  {
+    int lz;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(lz));
+    p0v = am.pos[lz];
+  }
   load_part(0);
   constexpr int kMlPer = (QWEN_Q_HEADS * (KF < 16 ? KF : kAttnMaxSplits) + 255) / 256;  // (m, l) pairs per thread
   float2 mlv[kMlPer];
@@ -1368,6 +1375,8 @@ __device__ __forceinline__ void attn_merge_quant_slice(const AttnMergeArgs& am, 
       ml[(h * kAttnMaxSplits + sp) * 2 + 1] = mlv[u].y;
     }
   }
+  asm volatile("" : "+v"(p0v));
+  const int p0 = __builtin_amdgcn_readfirstlane(p0v);
   const int n = min(max(p0, 0) + 1, am.max_keys);
   // NEWKEY: the history keys end at p0 when the new key is one of the n keys
   const bool has_new = NEWKEY && p0 >= 0 && p0 < am.max_keys;
@@ -1672,10 +1681,11 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   float gsv[GRP ? 2 * KC : 1];  // GRP: scales and offset terms of the lane's token's 2*KC groups
   int gcv[GRP ? 2 * KC : 1];
   // One token of the gate/up projection with K split over the waves (KW): only column 0 of the
-  // products is a token, its 16 rows per matrix four to a lane in lanes 0, 16, 32, 48.  The K groups
-  // leave those rows in LDS and lane r < 16 of wave 0 finishes row r: one SiLU per lane, not four in
-  // a row (its row scales loaded per lane, sw_row and sw2_row).
-  constexpr bool kRowLane = KW && EPI == kEpiSiluMul && DUAL && RTW == 1;
+  // products is a token, each tile's 16 rows per matrix four to a lane in lanes 0, 16, 32, 48.  The K
+  // groups leave those rows in LDS and lane 16 r + i of wave 0 finishes row i of tile r: one SiLU per
+  // lane, not 4 RTW in a row (its row scales loaded per lane, sw_row and sw2_row).
+  constexpr bool kRowLane = KW && EPI == kEpiSiluMul && DUAL && (RTW == 1 || RTW == 2);
+  const int rl_r = (lane >> 4) & (RTW - 1);  // kRowLane: the lane's tile (lanes past 16 RTW repeat)
   float sw_row = 0.0f, sw2_row = 0.0f;
   // The decode SiLU's exp table, copied to LDS before the epilogue: read from constant memory there,
   // each of a lane's SiLU evaluations waited on one more memory round trip (several tokens; with one
@@ -1725,7 +1735,8 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
     const float* bsrc = kBias && a.bias ? a.bias : a.sw;
     const uint32_t bmask = kBias && a.bias ? 0xFFFFFFFFu : 0u;
     if constexpr (kRowLane) {
-      const int row = (ok[0] ? row_tile(0) : 0) * 16 + (lane & 15);
+      const int rt = row_tile(rl_r);
+      const int row = (rt < row_tiles ? rt : 0) * 16 + (lane & 15);
       sw_row = a.sw[row];
       sw2_row = a.sw2[row];
     } else {
@@ -1938,41 +1949,46 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
 
   if constexpr (kRowLane) {
     __syncthreads();  // every wave's slice reads are done: the slice buffer takes the sums
-    int* red = reinterpret_cast<int*>(xs);  // [K group][matrix d][limb][row 0..15], exact int32
+    // [K group][tile r][matrix d][limb][row 0..15], exact int32
+    int* red = reinterpret_cast<int*>(xs);
+    constexpr int kPerKg = RTW * D * 2 * 16;
     if (col == 0) {
 #pragma unroll
-      for (int d = 0; d < D; ++d) {
-        *reinterpret_cast<int4*>(red + kg * 64 + (2 * d) * 16 + 4 * g) =
-            make_int4(accH[0][d][0], accH[0][d][1], accH[0][d][2], accH[0][d][3]);
-        *reinterpret_cast<int4*>(red + kg * 64 + (2 * d + 1) * 16 + 4 * g) =
-            make_int4(accL[0][d][0], accL[0][d][1], accL[0][d][2], accL[0][d][3]);
-      }
+      for (int r = 0; r < RTW; ++r)
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+          int* dst = red + kg * kPerKg + ((r * D + d) * 2) * 16 + 4 * g;
+          *reinterpret_cast<int4*>(dst) = make_int4(accH[r][d][0], accH[r][d][1], accH[r][d][2], accH[r][d][3]);
+          *reinterpret_cast<int4*>(dst + 16) = make_int4(accL[r][d][0], accL[r][d][1], accL[r][d][2], accL[r][d][3]);
+        }
     }
     if (threadIdx.x < 32) exp_tab[threadIdx.x] = tab_v;
     __syncthreads();
     if (kg > 0) return;
-    const int row = lane & 15;  // lanes 16.. repeat rows 0..15 (no stores)
+    const int row = lane & 15;  // of tile rl_r; lanes past 16 RTW repeat rows (no stores)
     int hs[2] = {0, 0}, ls[2] = {0, 0};
 #pragma unroll
     for (int j = 0; j < KG; ++j)
 #pragma unroll
       for (int d = 0; d < D; ++d) {
-        hs[d] += red[j * 64 + (2 * d) * 16 + row];
-        ls[d] += red[j * 64 + (2 * d + 1) * 16 + row];
+        const int* src = red + j * kPerKg + ((rl_r * D + d) * 2) * 16 + row;
+        hs[d] += src[0];
+        ls[d] += src[16];
       }
     const double sx = (double)pre_sx;
     const int sh8 = 8 * pre_sums[0], sl8 = 8 * pre_sums[1];
     const float v = (float)(((double)(hs[0] - sh8) * 256.0 + (double)(ls[0] - sl8)) * sx) * sw_row;
     const float u = (float)(((double)(hs[1] - sh8) * 256.0 + (double)(ls[1] - sl8)) * sx) * sw2_row;
     const float yv = silu_decode(v, exp_tab) * u;
-    if (!ok[0]) return;
-    if (lane < 16) a.y[(size_t)tok0 * a.y_stride + row_tile(0) * 16 + row] = yv;
-    if (a.amax_out) {  // max |SiLU.up| of the block's 16 rows: the DPP row max of lanes 0..15
-      float m = fmaxf(0.0f, fabsf(yv));
+    const bool live = row_tile(rl_r) < row_tiles;
+    if (lane < 16 * RTW && live) a.y[(size_t)tok0 * a.y_stride + row_tile(rl_r) * 16 + row] = yv;
+    if (a.amax_out) {  // max |SiLU.up| of the block's rows: DPP row maxima of lanes 0..15 (and 16..31)
+      float m = live ? fmaxf(0.0f, fabsf(yv)) : 0.0f;
       m = fmaxf(m, __int_as_float(dpp_i<0xB1>(__float_as_int(m))));
       m = fmaxf(m, __int_as_float(dpp_i<0x4E>(__float_as_int(m))));
       m = fmaxf(m, __int_as_float(dpp_i<0x124>(__float_as_int(m))));
       m = fmaxf(m, __int_as_float(dpp_i<0x128>(__float_as_int(m))));
+      if (RTW == 2) m = fmaxf(m, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 16)));
       if (lane == 0) a.amax_out[rg] = m;
     }
     return;
@@ -3639,14 +3655,17 @@ static void launch_gemm_epi(const GemmArgs& a, hipStream_t st) {
   }
 }
 
+// gate/up after O: kGateUpTiles 16-row tiles of both matrices per block, K split over its four waves
+constexpr int kGateUpTiles = 1;
+int gate_up_maxima_count(int out_dim) { return out_dim / (16 * kGateUpTiles); }
+
 bool launch_gemm_i8_pre(const GemmArgs& a, const GemmArgs& pre, int pre_epi, int pre_splits, hipStream_t st) {
   if (a.tokens != 1 || a.in_dim != QWEN_HIDDEN || pre.out_dim != QWEN_HIDDEN || pre.fuse != kFuseNormQuant ||
       pre.tokens != 1 || pre_splits < 1 || pre_splits > (pre_epi == kEpiResidual ? kPreResidualSplits : 1))
     return false;
   if (a.wp2 && a.out_dim % 64 == 0 && pre_epi == kEpiStore && !a.prefill_silu) {  // decode gate/up after O
-    // one 16-row tile of both matrices per block, K split over its four waves
-    const int rg_count = a.out_dim / 16;
-    hipLaunchKernelGGL((gemm_skinny_pre_kw_kernel<1, true, kEpiSiluMul, 12, kEpiStore>),
+    const int rg_count = gate_up_maxima_count(a.out_dim);
+    hipLaunchKernelGGL((gemm_skinny_pre_kw_kernel<kGateUpTiles, true, kEpiSiluMul, 12, kEpiStore>),
                        dim3(8 * ((rg_count + 7) / 8)), dim3(256), 0, st, a, rg_count, pre, pre_splits);
     return true;
   }

@@ -407,7 +407,7 @@ struct qwen_hip_model {
         sq.sx_out = w.sx;
         sq.sums_out = w.sums;
         sq.amax_in = w.gmax;
-        sq.amax_n = QWEN_INTERMEDIATE / 16;
+        sq.amax_n = gate_up_maxima_count(QWEN_INTERMEDIATE);
         fn.defer_reduce = fuse_next ? 1 : 0;
         const GemmArgs da = args(w, B, QWEN_INTERMEDIATE, QWEN_HIDDEN, f.down, f.sw_down, nullptr, hidden,
                                  QWEN_HIDDEN, nullptr, nullptr, w.att, round, 0, fuse_next ? &fn : nullptr);
