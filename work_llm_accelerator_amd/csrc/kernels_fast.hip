@@ -1405,15 +1405,19 @@ __device__ __forceinline__ void attn_merge_quant_slice(const AttnMergeArgs& am, 
     for (int u = 0; u < 2; ++u) {
       const int f = threadIdx.x + 256 * u;
       if (f < QWEN_HIDDEN / 4) {
+        // the batch's merge weights read at once (slots past nc hold stale values, not used), then
+        // the splits in order as selects: a branch per split waited for its own LDS read
+        float w[kFirst];
 #pragma unroll
-        for (int j = 0; j < kFirst; ++j)
-          if (s0 + j < nc) {
-            const float w = ml[((f >> 5) * kAttnMaxSplits + s0 + j) * 2];
-            out[u].x += pv[u][j].x * w;
-            out[u].y += pv[u][j].y * w;
-            out[u].z += pv[u][j].z * w;
-            out[u].w += pv[u][j].w * w;
-          }
+        for (int j = 0; j < kFirst; ++j) w[j] = ml[((f >> 5) * kAttnMaxSplits + s0 + j) * 2];
+#pragma unroll
+        for (int j = 0; j < kFirst; ++j) {
+          const bool live = s0 + j < nc;
+          out[u].x = live ? __builtin_fmaf(pv[u][j].x, w[j], out[u].x) : out[u].x;
+          out[u].y = live ? __builtin_fmaf(pv[u][j].y, w[j], out[u].y) : out[u].y;
+          out[u].z = live ? __builtin_fmaf(pv[u][j].z, w[j], out[u].z) : out[u].z;
+          out[u].w = live ? __builtin_fmaf(pv[u][j].w, w[j], out[u].w) : out[u].w;
+        }
       }
     }
   }
