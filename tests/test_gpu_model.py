@@ -380,17 +380,28 @@ def test_model_prefill_fast_many_seqs(torch, layers2):
         m1.close()
 
 
+# The one-sequence forms against the separate launches, without the bf16 rounding between layers (which
+# turns any difference into a whole bf16 step): the O projection's blocks quantize the context row per
+# head range (kOneTokenOSplits ranges of 768 columns, each with its own scale) where the separate form
+# quantizes the whole row with one scale, so the forms differ by about that code's rounding, not bit for
+# bit (measured on MI355X: up to 3.8e-4 of max after two calls of two layers).
+ONE_VS_SEPARATE_TOL = 1e-3
+
+
 @pytest.mark.parametrize("past", [0, 37, 1500])
 def test_model_decode_o_reduce_in_gate_up(torch, layers2, model2, past):
     """One sequence: the decode attention's split merge and the context row's quantization run in
-    every block of the O projection, the O projection's reduce step (RMSNorm, quantization) in every
-    block of the gate/up projection, the SiLU·up row's quantization in every block of the down projection,
+    every block of the O projection (each block merging and quantizing one head range), the O
+    projection's reduce step (adding the head ranges' partials, RMSNorm, quantization) in every block
+    of the gate/up projection, the SiLU·up row's quantization in every block of the down projection,
     and layer 0's down-projection reduce step (residual, bf16 rounding, layer 1's RMSNorm,
-    quantization) in every block of layer 1's Q/K/V projection, instead of their own launches; both
-    forms must give exactly the same hidden row and K/V cache, over both layers with the driver's
-    bf16 rounding, for two calls in a row.  1500 keys: 24 attention splits, so the O blocks' merge
-    loads its partials in two batches (16 + 8); its first call is also checked against the oracle."""
-    from work_llm_accelerator_amd.model import FLAG_SEPARATE_ATTN, FLAG_SEPARATE_REDUCE, MODE_FAST
+    quantization) in every block of layer 1's Q/K/V projection, instead of their own launches.  Over
+    both layers without the bf16 rounding: layer 0's new K/V row is bit-identical to the separate
+    form's (it precedes the O projection), the hidden row and layer 1's K/V row agree within
+    ONE_VS_SEPARATE_TOL of max, for two calls in a row (the second from the first's output).  1500
+    keys: 24 attention splits, so the O blocks' merge loads its partials in two batches (16 + 8); its
+    first call is also checked against the oracle."""
+    from work_llm_accelerator_amd.model import FLAG_NO_BF16_ROUND, FLAG_SEPARATE_ATTN, FLAG_SEPARATE_REDUCE, MODE_FAST
 
     print(f"model decode fast O reduce in gate/up past={past}", flush=True)
     if past > 1000:
@@ -403,19 +414,27 @@ def test_model_decode_o_reduce_in_gate_up(torch, layers2, model2, past):
         vl = [hist[(l, 0)][1].copy() for l in range(2)]
         ref = oracle_decode(layers2, x[0], past, kl, vl)
         assert rel_err(hidden.cpu().numpy()[0], ref) <= FAST_TOL_ROUNDED
-    outs = []
+    outs = {}
     # the attention runs as its own launch in both forms (its fusion into Q/K/V rounds differently,
     # checked by test_model_decode_fused_attention)
     for flag in (FLAG_SEPARATE_ATTN, FLAG_SEPARATE_REDUCE):
         cache, _, x = decode_setup(torch, 2, [past], max(48, past + 1), seed=61)
         hidden = torch.from_numpy(x).cuda()
         pos = torch.tensor([past], dtype=torch.int32, device="cuda")
+        calls = []
         for _ in range(2):
-            model2.decode(MODE_FAST | flag, hidden, pos, past + 1, cache)
-        model2.synchronize()
-        outs.append((hidden.cpu().numpy(), cache.k.cpu().numpy(), cache.v.cpu().numpy()))
-    for a, b in zip(outs[0], outs[1]):
-        assert bits_equal(a.reshape(-1), b.reshape(-1)), first_mismatch(a.reshape(-1), b.reshape(-1))
+            model2.decode(MODE_FAST | FLAG_NO_BF16_ROUND | flag, hidden, pos, past + 1, cache)
+            model2.synchronize()
+            calls.append((hidden.cpu().numpy()[0], cache.k[:, 0, past].cpu().numpy(), cache.v[:, 0, past].cpu().numpy()))
+        outs[flag] = calls
+    one, sep = outs[FLAG_SEPARATE_ATTN], outs[FLAG_SEPARATE_REDUCE]
+    for i in (1, 2):  # the first call's layer-0 K/V row
+        assert bits_equal(one[0][i][0], sep[0][i][0]), first_mismatch(one[0][i][0], sep[0][i][0])
+    for c in range(2):
+        d_h = rel_err(one[c][0], sep[c][0])
+        d_kv = max(rel_err(one[c][i][l], sep[c][i][l]) for i in (1, 2) for l in range(2))
+        print(f"  call {c}: hidden {d_h:.3g}, K/V rows {d_kv:.3g} of max", flush=True)
+        assert d_h <= ONE_VS_SEPARATE_TOL and d_kv <= ONE_VS_SEPARATE_TOL
 
 
 # The two attention forms: |y_fused - y_sep| <= 5e-4 * max|y_sep|.  The context rows differ in the last

@@ -127,6 +127,10 @@ constexpr int kSplitTokens = 256;
 // K splits of the one-token down projection (8960 = 5 x 14 chunks of 128), whose partials the next
 // layer's Q/K/V blocks reduce in their prologue.
 constexpr int kPreResidualSplits = 5;
+// Head ranges (K ranges of 1536 / kOneTokenOSplits columns) of the one-token O projection: each block
+// merges the attention of its range's heads and quantizes them with their own scale, and the gate/up
+// projection's prologue adds the kOneTokenOSplits partials.
+constexpr int kOneTokenOSplits = 2;
 // Decode GEMMs of at most kSkinnyTokens tokens (in_dim 1536 or 8960) run the skinny kernels.
 constexpr int kSkinnyTokens = 64;
 inline size_t splitk_bytes(size_t out) { return (size_t)kMaxSplits * kSplitTokens * out * 4u; }

@@ -1247,14 +1247,15 @@ __device__ __forceinline__ void quant_chunks_from_maxima(const float* __restrict
 // Merge weights of one sequence's split-KV decode-attention partials, per head h: M = the maximum of
 // the splits' m (and of the new key's score s_new[h] when has_new), f = exp(m - M), L = sum of l * f
 // (+ exp(s_new[h] - M)), weight = f / L, written over m in ml ([h][kAttnMaxSplits][2]: m, l) for the
-// splits sp < nc (and to s_new[h] for the new key).  Threads 16h + j (h < 12) take splits j, j + 16,
+// splits sp < nc (and to s_new[h] for the new key).  Threads 16h + j (h < NH) take splits j, j + 16,
 // j + 32, j + 48 of head h; the maximum and the sum meet by DPP row steps (one row of 16 lanes per
 // head), each lane's own splits first in ascending order.  Every thread of the block calls it.
+template <int NH = QWEN_Q_HEADS>
 __device__ __forceinline__ void merge_split_weights(float* ml, int nc, float* s_new, bool has_new) {
   static_assert(kAttnMaxSplits % 16 == 0, "splits in rows of 16 lanes");
   constexpr int kPer = kAttnMaxSplits / 16;
   const int t = threadIdx.x;
-  if (t < 16 * QWEN_Q_HEADS) {  // wave-uniform: waves 0..2
+  if (t < 16 * NH) {  // wave-uniform for NH a multiple of 4: waves 0..2 for 12 heads
     const int h = t >> 4, j = t & 15;
     float* mh = ml + h * kAttnMaxSplits * 2;
     auto rmax = [](float v) {
@@ -1300,39 +1301,44 @@ __device__ __forceinline__ void merge_split_weights(float* ml, int nc, float* s_
 // The merge of one sequence's split-KV decode-attention partials, in the arithmetic and order of
 // attn_decode_kernel's merge (per head: max of the split maxima, exp-weights normalised by the
 // weighted sum, then the weighted sum of the split partial rows), followed by quantize_row_lds's
-// quantization of the context row (from registers) into token 0's row of a skinny-GEMM slice (K chunk c at xs + c * chunk_stride).  The
-// partials come from the previous launch, so plain loads see them.  256 threads.
+// quantization of the merged rows (from registers) into token 0's row of a skinny-GEMM slice (K
+// chunk c at xs + c * chunk_stride).  The block merges query heads h0 .. h0 + HS - 1, i.e. context
+// columns 128 h0 .. 128 (h0 + HS) - 1, and quantizes them with their own scale and limb sums (HS = 12:
+// the whole row).  The partials come from the previous launch, so plain loads see them.  256 threads.
 // NEWKEY (the attention fused into the Q/K/V projection): the partials cover the history keys and the
 // new key is a term of its own, read from am.qkv_new: score s = (q / sqrt(128)) . k, weight exp(s - M)
 // with M the maximum over the splits and s, added to the sum with l = 1 and to the row with v.
-template <bool NEWKEY = false, int KF = 16, class Issue>
-__device__ __forceinline__ void attn_merge_quant_slice(const AttnMergeArgs& am, uint8_t* xs, int chunk_stride,
+template <bool NEWKEY = false, int KF = 16, int HS = QWEN_Q_HEADS, class Issue>
+__device__ __forceinline__ void attn_merge_quant_slice(const AttnMergeArgs& am, int h0, uint8_t* xs, int chunk_stride,
                                                        float* sx_lds, int* sums_lds, bool write_global,
                                                        Issue&& issue) {
-  __shared__ float ml[QWEN_Q_HEADS * kAttnMaxSplits * 2];  // (m, l) per head and split, then merge weights
+  static_assert(QWEN_Q_HEADS % HS == 0 && HS * 32 <= 512, "a head range of the context row");
+  __shared__ float ml[HS * kAttnMaxSplits * 2];  // (m, l) per head and split, then merge weights
   __shared__ float red_f[4];
   __shared__ int red_i[8];
   // The loads do not wait for the position: the first kFirst splits' partials and every (m, l) pair
   // are loaded whatever the key count; the merge below reads only the splits that hold keys.  Thread
-  // t owns float4 f = t and t + 256 (f < 384) of the context row: head f >> 5, dims 4 (f & 31) .. + 3;
-  // 16-byte loads keep a wave's outstanding loads (with the caller's weights) under the counter's 63.
+  // t owns float4 f = t and t + 256 (f < kF4) of the block's columns: local head f >> 5, dims 4 (f & 31)
+  // .. + 3 (threads past the last float4 load its values again, used by nobody); 16-byte loads keep a
+  // wave's outstanding loads (with the caller's weights) under the counter's 63.
   // KF (8, 12 or 16) is the batch of splits loaded at once; with KF < 16 the caller guarantees
   // nsplit <= KF, so one batch and one (m, l) pair per thread cover every split.
   static_assert(KF == 8 || KF == 12 || KF == 16, "merge batch");
   constexpr int kFirst = KF;
+  constexpr int kF4 = HS * 32;                // float4s of the block's columns
+  constexpr int kU = (kF4 + 255) / 256;       // float4s per thread
   const int nsplit = am.nsplit;
-  float4 pv[2][kFirst];
-  // Branch-free within a wave: past the last split the loads read the last split again (used by
-  // nobody), so every load of a batch is issued at once; waves 2 and 3 own one float4 of the row.
+  float4 pv[kU][kFirst];
+  auto fidx = [&](int u) { return min((int)threadIdx.x + 256 * u, kF4 - 1); };
+  auto owns = [&](int u) { return (int)threadIdx.x + 256 * u < kF4; };
   auto load_part = [&](int s0) {
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      if (u == 1 && threadIdx.x >= QWEN_HIDDEN / 4 - 256) break;  // wave-uniform: waves 2, 3 own one float4
-      const int f = (int)threadIdx.x + 256 * u;
+    for (int u = 0; u < kU; ++u) {
+      const int f = fidx(u);
 #pragma unroll
       for (int j = 0; j < kFirst; ++j)
         pv[u][j] = *reinterpret_cast<const float4*>(
-            am.part + ((size_t)(f >> 5) * nsplit + min(s0 + j, nsplit - 1)) * QWEN_HEAD_DIM + 4 * (f & 31));
+            am.part + ((size_t)(h0 + (f >> 5)) * nsplit + min(s0 + j, nsplit - 1)) * QWEN_HEAD_DIM + 4 * (f & 31));
     }
   };
   // the position as a vector load whose register is held until it is needed (read back early, its
@@ -1344,21 +1350,21 @@ __device__ __forceinline__ void attn_merge_quant_slice(const AttnMergeArgs& am, 
     p0v = am.pos[lz];
   }
   load_part(0);
-  constexpr int kMlPer = (QWEN_Q_HEADS * (KF < 16 ? KF : kAttnMaxSplits) + 255) / 256;  // (m, l) pairs per thread
+  constexpr int kMlPer = (HS * (KF < 16 ? KF : kAttnMaxSplits) + 255) / 256;  // (m, l) pairs per thread
   float2 mlv[kMlPer];
 #pragma unroll
   for (int u = 0; u < kMlPer; ++u) {
-    const int i = min((int)threadIdx.x + 256 * u, QWEN_Q_HEADS * nsplit - 1);
-    mlv[u] = am.pml[i];  // pml[h][sp] at h * nsplit + sp
+    const int i = min((int)threadIdx.x + 256 * u, HS * nsplit - 1);
+    mlv[u] = am.pml[h0 * nsplit + i];  // pml[h][sp] at h * nsplit + sp
   }
-  // NEWKEY: the thread's q, k and v float4s of the new key (head f >> 5, KV head (f >> 5) / 6)
-  float4 nq[2], nk[2], nv[2];
+  // NEWKEY: the thread's q, k and v float4s of the new key (head h0 + (f >> 5), its KV head)
+  float4 nq[kU], nk[kU], nv[kU];
   if constexpr (NEWKEY) {
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int f = min((int)threadIdx.x + 256 * u, QWEN_HIDDEN / 4 - 1);
-      const int d4 = 4 * (f & 31), kvo = ((f >> 5) / QWEN_GROUPS) * QWEN_HEAD_DIM + d4;
-      nq[u] = *reinterpret_cast<const float4*>(am.qkv_new + (f >> 5) * QWEN_HEAD_DIM + d4);
+    for (int u = 0; u < kU; ++u) {
+      const int f = fidx(u), h = h0 + (f >> 5);
+      const int d4 = 4 * (f & 31), kvo = (h / QWEN_GROUPS) * QWEN_HEAD_DIM + d4;
+      nq[u] = *reinterpret_cast<const float4*>(am.qkv_new + h * QWEN_HEAD_DIM + d4);
       nk[u] = *reinterpret_cast<const float4*>(am.qkv_new + QWEN_HIDDEN + kvo);
       nv[u] = *reinterpret_cast<const float4*>(am.qkv_new + QWEN_HIDDEN + QWEN_KV_WIDTH + kvo);
     }
@@ -1369,7 +1375,7 @@ __device__ __forceinline__ void attn_merge_quant_slice(const AttnMergeArgs& am, 
 #pragma unroll
   for (int u = 0; u < kMlPer; ++u) {
     const int i = threadIdx.x + 256 * u;
-    if (i < QWEN_Q_HEADS * nsplit) {
+    if (i < HS * nsplit) {
       const int h = i / nsplit, sp = i % nsplit;
       ml[(h * kAttnMaxSplits + sp) * 2] = mlv[u].x;
       ml[(h * kAttnMaxSplits + sp) * 2 + 1] = mlv[u].y;
@@ -1382,29 +1388,31 @@ __device__ __forceinline__ void attn_merge_quant_slice(const AttnMergeArgs& am, 
   const bool has_new = NEWKEY && p0 >= 0 && p0 < am.max_keys;
   const int hist = has_new ? p0 : n;
   const int nc = (hist + am.chunk - 1) / am.chunk;  // splits that hold keys (the rest hold stale values)
-  __shared__ float s_new[QWEN_Q_HEADS];  // NEWKEY: the new key's score per head, then its merge weight
+  __shared__ float s_new[HS];  // NEWKEY: the new key's score per head, then its merge weight
   if constexpr (NEWKEY) {
     constexpr float kScale = 0.08838834764831845f;  // 1/sqrt(128), the scale of the split partials' q
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      if (u == 1 && threadIdx.x >= QWEN_HIDDEN / 4 - 256) break;  // wave-uniform: waves 2, 3 own one float4
+    for (int u = 0; u < kU; ++u) {
+      if (u > 0 && !owns(u)) break;  // wave-uniform: the waves without a second float4
       float sc = (nq[u].x * kScale) * nk[u].x + (nq[u].y * kScale) * nk[u].y + (nq[u].z * kScale) * nk[u].z +
                  (nq[u].w * kScale) * nk[u].w;
 #pragma unroll
       for (int o = 1; o < 32; o <<= 1) sc += __shfl_xor(sc, o, 64);  // over the head's 32 lanes
-      if ((threadIdx.x & 31) == 0) s_new[(threadIdx.x + 256 * u) >> 5] = sc;
+      if ((threadIdx.x & 31) == 0 && owns(u)) s_new[(threadIdx.x + 256 * u) >> 5] = sc;
     }
   }
   __syncthreads();
-  merge_split_weights(ml, nc, s_new, has_new);
+  merge_split_weights<HS>(ml, nc, s_new, has_new);
   __syncthreads();
-  float4 out[2] = {make_float4(0.0f, 0.0f, 0.0f, 0.0f), make_float4(0.0f, 0.0f, 0.0f, 0.0f)};
+  float4 out[kU];
+#pragma unroll
+  for (int u = 0; u < kU; ++u) out[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   for (int s0 = 0; s0 < nc; s0 += kFirst) {
     if (s0 > 0) load_part(s0);
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
+    for (int u = 0; u < kU; ++u) {
       const int f = threadIdx.x + 256 * u;
-      if (f < QWEN_HIDDEN / 4) {
+      if (f < kF4) {
         // the batch's merge weights read at once (slots past nc hold stale values, not used), then
         // the splits in order as selects: a branch per split waited for its own LDS read
         float w[kFirst];
@@ -1423,9 +1431,9 @@ __device__ __forceinline__ void attn_merge_quant_slice(const AttnMergeArgs& am, 
   }
   if constexpr (NEWKEY) {
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
+    for (int u = 0; u < kU; ++u) {
       const int f = threadIdx.x + 256 * u;
-      if (f < QWEN_HIDDEN / 4) {
+      if (f < kF4) {
         const float w = s_new[f >> 5];
         out[u].x += nv[u].x * w;
         out[u].y += nv[u].y * w;
@@ -1437,16 +1445,16 @@ __device__ __forceinline__ void attn_merge_quant_slice(const AttnMergeArgs& am, 
   // quantize_row_lds's arithmetic on the thread's own float4s, straight from registers
   float amax = 0.0f;
 #pragma unroll
-  for (int u = 0; u < 2; ++u)
-    if (threadIdx.x + 256 * u < QWEN_HIDDEN / 4)
+  for (int u = 0; u < kU; ++u)
+    if (owns(u))
       amax = fmaxf(amax, fmaxf(fmaxf(fabsf(out[u].x), fabsf(out[u].y)), fmaxf(fabsf(out[u].z), fabsf(out[u].w))));
   amax = block_max4(amax, red_f);
   const float inv = amax > 0.0f ? (float)kQuantMax / amax : 0.0f;
   int sh = 0, sl = 0;
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
+  for (int u = 0; u < kU; ++u) {
     const int f = threadIdx.x + 256 * u;
-    if (f < QWEN_HIDDEN / 4) {
+    if (f < kF4) {
       const float e[4] = {out[u].x, out[u].y, out[u].z, out[u].w};
       uint32_t hw = 0, lw = 0;
 #pragma unroll
@@ -1508,8 +1516,8 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
                 "ATTN: the one-token [q | k | v] projection with RoPE");
   static_assert(!PRE || (KSW == 1 && NKC * kKChunk == QWEN_HIDDEN), "PRE: one K group over a 1536-wide row");
   static_assert(!PRE_QUANT || (KSW == 1 && !PRE), "PRE_QUANT: one K group");
-  static_assert(!PRE_ATTN || (KSW == 1 && !PRE && !PRE_QUANT && NKC * kKChunk == QWEN_HIDDEN),
-                "PRE_ATTN: one K group over the 1536-wide context row");
+  static_assert(!PRE_ATTN || (KSW == 1 && !PRE && !PRE_QUANT && QWEN_HIDDEN % (NKC * kKChunk) == 0),
+                "PRE_ATTN: one K group over the 1536-wide context row, or over a range of its heads");
   constexpr bool kMade = PRE || PRE_QUANT || PRE_ATTN;  // the slice is made by the block
   // GRP: the activations are the grouped two-limb code (GemmArgs::gsx, gcorr): each 64-wide K group,
   // one MFMA of a K chunk, is dequantized with its own scale, so the block's partials are fp32 sums
@@ -1793,7 +1801,8 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   __shared__ float pre_sx;
   __shared__ int pre_sums[2];
   if constexpr (PRE_ATTN)
-    attn_merge_quant_slice<NEWKEY, MKF>(am, xs, kXsChunk, &pre_sx, pre_sums, blockIdx.x == 0, issue_loads);
+    attn_merge_quant_slice<NEWKEY, MKF, NKC>(am, z * NKC, xs, kXsChunk, &pre_sx, pre_sums,
+                                             NKC == QWEN_Q_HEADS && blockIdx.x == 0, issue_loads);
   if constexpr (PRE_QUANT) {
     // token 0's row of the slice: K chunks kc0 .. kc0 + NKC - 1 (row 0 of each chunk, unswizzled)
     if (pre.amax_in)
@@ -1808,7 +1817,7 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
     // by the block's four waves together (three block barriers): the O projection's one K group (store
     // epilogue) or the down projection's five splits (residual).  (One wave alone, with the other
     // three issuing their loads, took 2.2 us of arithmetic on the launch's critical path.)
-    reduce_norm_quant_row_w4<PRE_EPI, PRE_EPI == kEpiResidual ? kPreResidualSplits : 1>(
+    reduce_norm_quant_row_w4<PRE_EPI, PRE_EPI == kEpiResidual ? kPreResidualSplits : kOneTokenOSplits>(
         pre, pre_splits, reinterpret_cast<int8_t*>(xs), kXsChunk, &pre_sx, pre_sums, blockIdx.x == 0 && pre.y,
         issue_loads);
   }
@@ -2106,6 +2115,10 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   const double sx = (double)(kMade ? pre_sx : sx_l);
   const bool partial = splits > 1 || (!DUAL && !ROPE && a.fuse != kFuseNone);
   if (partial) {
+    // PRE_ATTN over a range of heads: the range has its own scale and limb sums, so its partial takes
+    // its own offset correction (the reduce step then adds the partials with a zero correction)
+    constexpr bool kOwnCorr = PRE_ATTN && NKC * kKChunk < QWEN_HIDDEN;
+    const int ch8 = kOwnCorr ? 8 * pre_sums[0] : 0, cl8 = kOwnCorr ? 8 * pre_sums[1] : 0;
 #pragma unroll
     for (int r = 0; r < RTW; ++r) {
       if (!ok[r]) continue;
@@ -2114,7 +2127,8 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
 #pragma unroll
       for (int q = 0; q < 4; ++q)
         out[q] = GRP ? gacc[r][q] * swv[r][q]
-                     : (float)(((double)accH[r][0][q] * 256.0 + (double)accL[r][0][q]) * sx) * swv[r][q];
+                     : (float)(((double)(accH[r][0][q] - ch8) * 256.0 + (double)(accL[r][0][q] - cl8)) * sx) *
+                           swv[r][q];
       *reinterpret_cast<float4*>(a.part + ((size_t)z * a.tokens + tok) * a.out_dim + row0) =
           make_float4(out[0], out[1], out[2], out[3]);
     }
@@ -2337,7 +2351,7 @@ template <int RTW, int EPI, int NKC, bool NEWKEY, bool KW = false, int MKF = 16>
 __global__ void __launch_bounds__(256) gemm_skinny_prea_kernel(GemmArgs a, int rg_count, AttnMergeArgs am) {
   touch_kernargs<kernarg_bytes<GemmArgs, int, AttnMergeArgs>()>();
   gemm_skinny_body<RTW, false, EPI, NKC, false, 1, false, kEpiStore, false, true, false, false, NEWKEY, KW, MKF>(
-      a, 1, rg_count, 1, a, 0, am);
+      a, 1, rg_count, QWEN_HIDDEN / (NKC * kKChunk), a, 0, am);
 }
 
 // One token's fused [q | k | v] projection + RoPE + K/V append with the decode attention over the
@@ -3665,7 +3679,8 @@ int gate_up_maxima_count(int out_dim) { return out_dim / (16 * kGateUpTiles); }
 
 bool launch_gemm_i8_pre(const GemmArgs& a, const GemmArgs& pre, int pre_epi, int pre_splits, hipStream_t st) {
   if (a.tokens != 1 || a.in_dim != QWEN_HIDDEN || pre.out_dim != QWEN_HIDDEN || pre.fuse != kFuseNormQuant ||
-      pre.tokens != 1 || pre_splits < 1 || pre_splits > (pre_epi == kEpiResidual ? kPreResidualSplits : 1))
+      pre.tokens != 1 || pre_splits < 1 ||
+      pre_splits > (pre_epi == kEpiResidual ? kPreResidualSplits : kOneTokenOSplits))
     return false;
   if (a.wp2 && a.out_dim % 64 == 0 && pre_epi == kEpiStore && !a.prefill_silu) {  // decode gate/up after O
     const int rg_count = gate_up_maxima_count(a.out_dim);
@@ -3688,12 +3703,18 @@ bool launch_gemm_i8_prea(const GemmArgs& a, const AttnMergeArgs& am, hipStream_t
       a.fuse != kFuseNormQuant || !am.part || !am.pml || !am.pos || !am.sx_out || !am.sums_out || am.nsplit < 1 ||
       am.nsplit > kAttnMaxSplits || am.chunk < 1)
     return false;
-  // one 16-row tile per block, K split over its four waves; the merge loads 8, 12 or 16 splits at once
+  // one 16-row tile and one of kOneTokenOSplits head ranges (K ranges) per block, K split over its four
+  // waves; the merge loads 8, 12 or 16 splits at once.  (With more than one range each range's partial
+  // carries its own offset correction, so the reduce step must run with zero limb sums: only the
+  // deferred form, whose caller passes them, is offered.)
+  constexpr int kSplits = kOneTokenOSplits, kNkc = QWEN_Q_HEADS / kSplits;
+  if (kSplits > 1 && !a.defer_reduce) return false;
   const int rg_count = a.out_dim / 16;
-  const dim3 grid(8 * ((rg_count + 7) / 8));
+  const dim3 grid(8 * ((rg_count * kSplits + 7) / 8));
   auto go = [&](auto newkey, auto kf) {
-    hipLaunchKernelGGL((gemm_skinny_prea_kernel<1, kEpiStore, 12, decltype(newkey)::value, true, decltype(kf)::value>),
-                       grid, dim3(256), 0, st, a, rg_count, am);
+    hipLaunchKernelGGL(
+        (gemm_skinny_prea_kernel<1, kEpiStore, kNkc, decltype(newkey)::value, true, decltype(kf)::value>), grid,
+        dim3(256), 0, st, a, rg_count, am);
   };
   using K8 = std::integral_constant<int, 8>;
   using K12 = std::integral_constant<int, 12>;
@@ -3707,7 +3728,7 @@ bool launch_gemm_i8_prea(const GemmArgs& a, const AttnMergeArgs& am, hipStream_t
     else if (am.nsplit <= 12) go(std::false_type{}, K12{});
     else go(std::false_type{}, K16{});
   }
-  if (!a.defer_reduce) launch_reduce<kEpiStore>(a, 1, st);
+  if (!a.defer_reduce) launch_reduce<kEpiStore>(a, kSplits, st);
   return true;
 }
 

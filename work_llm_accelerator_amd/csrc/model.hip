@@ -377,7 +377,11 @@ struct qwen_hip_model {
         GemmArgs ga = args(w, B, QWEN_HIDDEN, QWEN_INTERMEDIATE, f.gate, f.sw_gate, nullptr, w.s, QWEN_INTERMEDIATE,
                            f.up, f.sw_up);
         ga.amax_out = w.gmax;  // the down projection's blocks take the row's maximum from these
-        if (!launch_gemm_i8_pre(ga, oa, kEpiStore, 1, stream))
+        // the O partials of the head ranges carry their own offset corrections: a zero correction here
+        GemmArgs op = oa;
+        op.sums = w.zero_sums;
+        op.sx = reinterpret_cast<const float*>(w.zero_sums);
+        if (!launch_gemm_i8_pre(ga, op, kEpiStore, kOneTokenOSplits, stream))
           throw std::runtime_error("gate/up with the O reduce: bad shape");
       } else {
         if (fused) {
