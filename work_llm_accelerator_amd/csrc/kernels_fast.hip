@@ -1696,8 +1696,8 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   // products is a token, each tile's 16 rows per matrix four to a lane in lanes 0, 16, 32, 48.  The K
   // groups leave those rows in LDS and lane 16 r + i of wave 0 finishes row i of tile r: one SiLU per
   // lane, not 4 RTW in a row (its row scales loaded per lane, sw_row and sw2_row).
-  constexpr bool kRowLane = KW && EPI == kEpiSiluMul && DUAL && (RTW == 1 || RTW == 2);
-  const int rl_r = (lane >> 4) & (RTW - 1);  // kRowLane: the lane's tile (lanes past 16 RTW repeat)
+  constexpr bool kRowLane = KW && EPI == kEpiSiluMul && DUAL && RTW <= 4;
+  const int rl_r = min(lane >> 4, RTW - 1);  // kRowLane: the lane's tile (lanes past 16 RTW repeat)
   float sw_row = 0.0f, sw2_row = 0.0f;
   // The decode SiLU's exp table, copied to LDS before the epilogue: read from constant memory there,
   // each of a lane's SiLU evaluations waited on one more memory round trip (several tokens; with one
@@ -1995,13 +1995,14 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
     const float yv = silu_decode(v, exp_tab) * u;
     const bool live = row_tile(rl_r) < row_tiles;
     if (lane < 16 * RTW && live) a.y[(size_t)tok0 * a.y_stride + row_tile(rl_r) * 16 + row] = yv;
-    if (a.amax_out) {  // max |SiLU.up| of the block's rows: DPP row maxima of lanes 0..15 (and 16..31)
+    if (a.amax_out) {  // max |SiLU.up| of the block's rows: DPP row maxima of lanes 16 r .. 16 r + 15
       float m = live ? fmaxf(0.0f, fabsf(yv)) : 0.0f;
       m = fmaxf(m, __int_as_float(dpp_i<0xB1>(__float_as_int(m))));
       m = fmaxf(m, __int_as_float(dpp_i<0x4E>(__float_as_int(m))));
       m = fmaxf(m, __int_as_float(dpp_i<0x124>(__float_as_int(m))));
       m = fmaxf(m, __int_as_float(dpp_i<0x128>(__float_as_int(m))));
-      if (RTW == 2) m = fmaxf(m, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 16)));
+#pragma unroll
+      for (int r = 1; r < RTW; ++r) m = fmaxf(m, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 16 * r)));
       if (lane == 0) a.amax_out[rg] = m;
     }
     return;
@@ -3673,9 +3674,14 @@ static void launch_gemm_epi(const GemmArgs& a, hipStream_t st) {
   }
 }
 
-// gate/up after O: kGateUpTiles 16-row tiles of both matrices per block, K split over its four waves
-constexpr int kGateUpTiles = 1;
-int gate_up_maxima_count(int out_dim) { return out_dim / (16 * kGateUpTiles); }
+// gate/up after O: kGateUpTiles 16-row tiles of both matrices per block, K split over its four waves;
+// one block (and one row maximum) per group of tiles, the group count rounded up to a multiple of 4
+// for the maxima's float4 reads (the groups past the last tile write a maximum of 0)
+constexpr int kGateUpTiles = 3;
+int gate_up_maxima_count(int out_dim) {
+  const int groups = (out_dim / 16 + kGateUpTiles - 1) / kGateUpTiles;
+  return (groups + 3) / 4 * 4;
+}
 
 bool launch_gemm_i8_pre(const GemmArgs& a, const GemmArgs& pre, int pre_epi, int pre_splits, hipStream_t st) {
   if (a.tokens != 1 || a.in_dim != QWEN_HIDDEN || pre.out_dim != QWEN_HIDDEN || pre.fuse != kFuseNormQuant ||
