@@ -2333,6 +2333,7 @@ __device__ __forceinline__ void touch_kernargs() {
 template <int RTW, bool DUAL, int EPI, int NKC, bool ROPE, int KSW, bool GRP = false>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(3)))
 gemm_skinny_kernel(GemmArgs a, int tt_count, int rg_count, int splits) {
+  touch_kernargs<kernarg_bytes<GemmArgs, int, int, int>()>();
   gemm_skinny_body<RTW, DUAL, EPI, NKC, ROPE, KSW, false, kEpiStore, false, false, GRP>(a, tt_count, rg_count, splits,
                                                                                       a, 0);
 }
@@ -2861,6 +2862,7 @@ __device__ __forceinline__ void reduce_norm_quant_row(const GemmArgs& a, int spl
 // another order.
 template <int EPI>
 __global__ void __launch_bounds__(128) reduce_norm_quant_pair_kernel(GemmArgs a, int splits) {
+  touch_kernargs<kernarg_bytes<GemmArgs, int>()>();
   const int tok = blockIdx.x;
   int8_t* xq_row = a.xq_out + (size_t)tok * (2 * QWEN_HIDDEN);
   if (splits == 1)
@@ -3022,6 +3024,8 @@ attn_decode_kernel(const float* __restrict__ qkv, int qkv_stride, const float* _
                    const float* __restrict__ v_cache, size_t seq_stride, const int* __restrict__ pos, int chunk,
                    int max_keys, float* __restrict__ part, float2* __restrict__ pml, unsigned* __restrict__ arrivals,
                    float* __restrict__ ctx, int8_t* __restrict__ xq, float* __restrict__ sx, int* __restrict__ sums) {
+  touch_kernargs<kernarg_bytes<const float*, int, const float*, const float*, size_t, const int*, int, int, float*,
+                               float2*, unsigned*, float*, int8_t*, float*, int*>()>();
   __shared__ __align__(16) float qs[16][kQRow];
   __shared__ __align__(16) float s_acc[4][QWEN_GROUPS][QWEN_HEAD_DIM];  // reused by the merge step
   __shared__ float s_m[4][QWEN_GROUPS], s_l[4][QWEN_GROUPS];
