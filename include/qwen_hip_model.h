@@ -47,10 +47,12 @@ typedef struct qwen_hip_model qwen_hip_model;
  * rather than in the prologue of every block of the projection that follows them: the decode
  * attention's split merge + context quantization (fused into O), the O projection's
  * reduce (fused into gate/up), the SiLU·up quantization (fused into down) and the down projection's
- * reduce + next RMSNorm + quantization (fused into the next layer's Q/K/V).  Same arithmetic, same
- * results; it exists to check the fused forms. */
+ * reduce + next RMSNorm + quantization (fused into the next layer's Q/K/V).  The same arithmetic except
+ * the context row's code: the fused O projection quantizes it per head range (two scales), the
+ * separate form with one scale for the row, so the two agree within the FAST tolerance, not bit for
+ * bit.  It exists to check the fused forms. */
 #define QWEN_FLAG_SEPARATE_REDUCE 0x200
-/* OR-ed into `mode` (FAST decode of one sequence with at most 1536 keys): run the decode attention as
+/* OR-ed into `mode` (FAST decode of one sequence with at most 1280 keys): run the decode attention as
  * a launch of its own rather than in the blocks of the Q/K/V projection (the fused form attends over
  * the history keys there and adds the new key's term in the O projection's merge).  The two forms
  * round differently; both are within the FAST tolerance.  QWEN_FLAG_SEPARATE_REDUCE implies it. */
