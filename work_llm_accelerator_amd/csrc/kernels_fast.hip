@@ -219,6 +219,13 @@ __device__ __forceinline__ void block_sum4_i2(int& a, int& b, int* s8) {
   b = (s8[4] + s8[5]) + (s8[6] + s8[7]);
   __syncthreads();
 }
+// The two sums of a 256-thread block from per-wave partials in LDS (w[2v], w[2v + 1]: wave v's), read
+// after a barrier that follows their writes: the one-token prologues leave them so, and the barrier
+// that publishes their activation slice also publishes the sums, one barrier fewer on the launch's
+// critical path (the sums are first needed in the epilogue).
+__device__ __forceinline__ int2 wave_sums_total(const int* w) {
+  return make_int2((w[0] + w[2]) + (w[4] + w[6]), (w[1] + w[3]) + (w[5] + w[7]));
+}
 
 // ---------------------------------------------------------------------------------------------
 // Two-limb activation quantization of one row held in LDS (n values, n % 128 == 0), done by a
@@ -1473,18 +1480,25 @@ __device__ __forceinline__ void attn_merge_quant_slice(const AttnMergeArgs& am, 
       *reinterpret_cast<uint32_t*>(dst + 128) = lw;
     }
   }
-  block_sum4_i2(sh, sl, red_i);
-  if (threadIdx.x == 0) {
-    const float sx = amax > 0.0f ? amax / (float)kQuantMax : 1.0f;
-    *sx_lds = sx;
-    sums_lds[0] = sh;
-    sums_lds[1] = sl;
-    if (write_global) {
+  // the limb sums as per-wave partials in sums_lds (8 ints, totals by wave_sums_total after the
+  // caller's slice barrier), the scale in *sx_lds; block 0 of a whole-row merge also writes the totals
+  const float sx = amax > 0.0f ? amax / (float)kQuantMax : 1.0f;
+  if (write_global) {  // block-uniform
+    int th = sh, tl = sl;
+    block_sum4_i2(th, tl, red_i);
+    if (threadIdx.x == 0) {
       *am.sx_out = sx;
-      am.sums_out[0] = sh;
-      am.sums_out[1] = sl;
+      am.sums_out[0] = th;
+      am.sums_out[1] = tl;
     }
   }
+  sh = wave_sum_i(sh);
+  sl = wave_sum_i(sl);
+  if ((threadIdx.x & 63) == 0) {
+    sums_lds[2 * (threadIdx.x >> 6)] = sh;
+    sums_lds[2 * (threadIdx.x >> 6) + 1] = sl;
+  }
+  if (threadIdx.x == 0) *sx_lds = sx;
 }
 
 // PRE (one token, KSW = 1): the activation slice is not loaded but made by the block: its four waves
@@ -1799,7 +1813,8 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
     if constexpr (!(ATTN && PRE)) issue_kv();
   };
   __shared__ float pre_sx;
-  __shared__ int pre_sums[2];
+  __shared__ int pre_sums[8];  // the made slice's limb sums: per-wave partials (wave_sums_total)
+  int2 pre_tot = make_int2(0, 0);  // their totals, read after the slice barrier
   if constexpr (PRE_ATTN)
     attn_merge_quant_slice<NEWKEY, MKF, NKC>(am, z * NKC, xs, kXsChunk, &pre_sx, pre_sums,
                                              NKC == QWEN_Q_HEADS && blockIdx.x == 0, issue_loads);
@@ -1811,10 +1826,11 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
     else
       quant_row_slice<kQuantVecs>(pre.y, pre.in_dim, kc0, NKC, xs, 16 * 256, &pre_sx, pre_sums,
                                   blockIdx.x == 0 ? pre.sx_out : nullptr, pre.sums_out, issue_loads);
+    if (threadIdx.x < 6) pre_sums[2 + threadIdx.x] = 0;  // the totals in [0], [1] (wave_sums_total)
   }
   if constexpr (PRE) {
     // token 0's row of the slice (K chunk c at xs + c * kXsChunk, row 0 of the chunk, unswizzled), made
-    // by the block's four waves together (three block barriers): the O projection's one K group (store
+    // by the block's four waves together (two block barriers): the O projection's K groups (store
     // epilogue) or the down projection's five splits (residual).  (One wave alone, with the other
     // three issuing their loads, took 2.2 us of arithmetic on the launch's critical path.)
     reduce_norm_quant_row_w4<PRE_EPI, PRE_EPI == kEpiResidual ? kPreResidualSplits : kOneTokenOSplits>(
@@ -1835,6 +1851,7 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
       wait_vmcnt<kKvLoads>();  // ATTN: the K/V rows (the wave's last loads) land during the MFMAs
       __syncthreads();
     }
+    pre_tot = wave_sums_total(pre_sums);
   } else {
     // Scalars, then the activation slice, then the weights in chunk order.  A wave's loads return in
     // order, so once at most the weight loads are outstanding its part of the slice has landed, and
@@ -1989,7 +2006,7 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
         ls[d] += src[16];
       }
     const double sx = (double)pre_sx;
-    const int sh8 = 8 * pre_sums[0], sl8 = 8 * pre_sums[1];
+    const int sh8 = 8 * pre_tot.x, sl8 = 8 * pre_tot.y;
     const float v = (float)(((double)(hs[0] - sh8) * 256.0 + (double)(ls[0] - sl8)) * sx) * sw_row;
     const float u = (float)(((double)(hs[1] - sh8) * 256.0 + (double)(ls[1] - sl8)) * sx) * sw2_row;
     const float yv = silu_decode(v, exp_tab) * u;
@@ -2119,7 +2136,7 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
     // PRE_ATTN over a range of heads: the range has its own scale and limb sums, so its partial takes
     // its own offset correction (the reduce step then adds the partials with a zero correction)
     constexpr bool kOwnCorr = PRE_ATTN && NKC * kKChunk < QWEN_HIDDEN;
-    const int ch8 = kOwnCorr ? 8 * pre_sums[0] : 0, cl8 = kOwnCorr ? 8 * pre_sums[1] : 0;
+    const int ch8 = kOwnCorr ? 8 * pre_tot.x : 0, cl8 = kOwnCorr ? 8 * pre_tot.y : 0;
 #pragma unroll
     for (int r = 0; r < RTW; ++r) {
       if (!ok[r]) continue;
@@ -2135,8 +2152,8 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
     }
     return;
   }
-  const int sh8 = 8 * (kMade ? pre_sums[0] : sh_l);
-  const int sl8 = 8 * (kMade ? pre_sums[1] : sl_l);
+  const int sh8 = 8 * (kMade ? pre_tot.x : sh_l);
+  const int sl8 = 8 * (kMade ? pre_tot.y : sl_l);
   float y[RTW][4];
 #pragma unroll
   for (int r = 0; r < RTW; ++r) {
@@ -2708,16 +2725,16 @@ __device__ __forceinline__ void reduce_norm_quant_row_zb(const GemmArgs& a, int 
 
 // reduce_norm_quant_row_zb's arithmetic for token 0's 1536-wide row (decode norm or none) by the four
 // waves of a 256-thread block: thread t owns float4 t and, for t < 128 (waves 0 and 1), float4 t + 256.
-// The sum of squares, the maximum and the limb sums are each a wave reduction (wave_sum's order) and
-// one exchange of the four waves' values through LDS: three barriers in all.  Every wave calls `issue`
-// once, right after its loads of the row.
+// The sum of squares and the maximum are each a wave reduction (wave_sum's order) and one exchange of
+// the four waves' values through LDS (two barriers); the limb sums are left as per-wave partials in
+// sums_out (8 ints; see wave_sums_total), and the scale in *sx_out, both published by the caller's
+// barrier.  Every wave calls `issue` once, right after its loads of the row.
 template <int EPI, int ZB, class Issue>
 __device__ __forceinline__ void reduce_norm_quant_row_w4(const GemmArgs& a, int splits, int8_t* xq_row,
                                                          int chunk_stride, float* sx_out, int* sums_out, bool write_y,
                                                          Issue&& issue) {
   __shared__ double w_ss[4];
   __shared__ float w_max[4];
-  __shared__ int w_sums[8];
   constexpr int kF = QWEN_HIDDEN / 4;  // float4s of the row
   const int t = threadIdx.x, wv = t >> 6;
   const bool two = t < kF - 256;  // wave-uniform
@@ -2831,18 +2848,15 @@ __device__ __forceinline__ void reduce_norm_quant_row_w4(const GemmArgs& a, int 
     *reinterpret_cast<uint32_t*>(xq_row + base) = hw;
     *reinterpret_cast<uint32_t*>(xq_row + base + 128) = lw;
   }
+  // the limb sums as per-wave partials (sums_out: 8 ints, totals by wave_sums_total after the
+  // caller's slice barrier)
   sh = wave_sum_i(sh);
   sl = wave_sum_i(sl);
   if ((t & 63) == 0) {
-    w_sums[2 * wv] = sh;
-    w_sums[2 * wv + 1] = sl;
+    sums_out[2 * wv] = sh;
+    sums_out[2 * wv + 1] = sl;
   }
-  __syncthreads();
-  if (t == 0) {
-    *sx_out = amax > 0.0f ? amax / (float)kQuantMax : 1.0f;
-    sums_out[0] = (w_sums[0] + w_sums[2]) + (w_sums[4] + w_sums[6]);
-    sums_out[1] = (w_sums[1] + w_sums[3]) + (w_sums[5] + w_sums[7]);
-  }
+  if (t == 0) *sx_out = amax > 0.0f ? amax / (float)kQuantMax : 1.0f;
 }
 
 
