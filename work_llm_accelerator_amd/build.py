@@ -8,7 +8,10 @@ Outputs, under work_llm_accelerator_amd/_lib/:
 Every .hip source is compiled with hipcc for gfx950 only.  Sources whose name starts with
 "kernels_fast" are compiled with -ffp-contract=fast (reordered, tolerance-checked kernels); all
 others with -ffp-contract=off so that each written fp32/f64 operation is one IEEE operation.
-Packed fp32 instructions are disabled for every source (-packed-fp32-ops).
+Packed fp32 instructions are disabled for every source (-packed-fp32-ops).  The "kernels_fast"
+sources also have the leading 14 dwords of scalar kernel arguments preloaded into SGPRs at wave
+launch (-amdgpu-kernarg-preload-count): the one-token kernels take the operands of their first
+loads there, instead of waiting for the argument segment's memory round trip.
 """
 
 from __future__ import annotations
@@ -54,8 +57,9 @@ def common_flags() -> list[str]:
 
 def compile_one(src: Path) -> Path:
     obj = OBJ_DIR / (src.stem + ".o")
-    contract = "-ffp-contract=fast" if src.name.startswith("kernels_fast") else "-ffp-contract=off"
-    cmd = [hipcc(), *common_flags(), contract, "-c", str(src), "-o", str(obj)]
+    fast = src.name.startswith("kernels_fast")
+    extra = ["-ffp-contract=fast", "-mllvm", "-amdgpu-kernarg-preload-count=14"] if fast else ["-ffp-contract=off"]
+    cmd = [hipcc(), *common_flags(), *extra, "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stdout}\n{res.stderr}")
