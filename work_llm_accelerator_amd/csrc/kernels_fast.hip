@@ -1145,10 +1145,10 @@ template <int EPI, class Issue = NoIssue>
 __device__ __forceinline__ void reduce_norm_quant_row(const GemmArgs& a, int splits, int tok, int8_t* xq_row,
                                                       int chunk_stride, float* sx_out, int* sums_out, bool write_y,
                                                       Issue&& issue = Issue{});
-template <int EPI, int ZB, class Issue, int W = 1>
+template <int EPI, int ZB, class Issue, int W = 1, bool HOT = false>
 __device__ __forceinline__ void reduce_norm_quant_row_zb(const GemmArgs& a, int splits, int tok, int8_t* xq_row,
                                                          int chunk_stride, float* sx_out, int* sums_out, bool write_y,
-                                                         Issue&& issue);
+                                                         Issue&& issue, const HotArgs& hot = HotArgs{});
 template <int EPI, int ZB, bool HOT, class Issue>
 __device__ __forceinline__ void reduce_norm_quant_row_w4(const GemmArgs& a, int splits, int8_t* xq_row,
                                                          int chunk_stride, float* sx_out, int* sums_out, bool write_y,
@@ -1693,6 +1693,18 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   const int tok0 = tt * 16;
   const int row_tiles = kHot ? HOT_OUT / 16 : a.out_dim / 16;
   const size_t row_stride_x = (size_t)(kHot ? HOT_IN : a.in_dim) * 2u;
+  // (hot without a made slice, 1..64 tokens: HotArgs p0 the activation code, p1 the weights, p2 the up
+  // matrix (DUAL) or the group scales (GRP), p3 the positions (ROPE), the groups' offset terms (GRP)
+  // or the grouped code's scales out (DUAL, null without it), n0 the token count)
+  constexpr bool kHotB = kHot && !kMade;
+  const int n_tok = kHotB ? hot.n0 : a.tokens;
+  const void* xq_p = kHotB ? hot.p0 : a.xq;
+  const void* wp_p = kHotB ? hot.p1 : a.wp;
+  const void* wp2_p = kHotB && DUAL ? hot.p2 : a.wp2;
+  const int* pos_p = kHotB && ROPE ? static_cast<const int*>(hot.p3) : a.pos;
+  const float* gsx_p = kHotB && GRP ? static_cast<const float*>(hot.p2) : a.gsx;
+  const int* gcorr_p = kHotB && GRP ? static_cast<const int*>(hot.p3) : a.gcorr;
+  const bool gsx_out_set = kHotB && DUAL ? hot.p3 != nullptr : a.gsx_out != nullptr;
 
   // activation slice -> LDS: chunk c, rows 4q..4q+3 per load (1 KiB), wave w takes chunks w, w+4KSW, ..
   // (ATTN: token 0's row of chunks 4j..4j+3 per load, wave w takes j = w, w+4, ..)
@@ -1710,9 +1722,9 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int row = 4 * q + (lane >> 4);
-        const int tok = min(tok0 + row, a.tokens - 1);  // rows past the last token reload a valid row
+        const int tok = min(tok0 + row, n_tok - 1);  // rows past the last token reload a valid row
         const int seg = (lane & 15) ^ row;
-        const uint8_t* src = reinterpret_cast<const uint8_t*>(a.xq) + (size_t)tok * row_stride_x +
+        const uint8_t* src = reinterpret_cast<const uint8_t*>(xq_p) + (size_t)tok * row_stride_x +
                              (size_t)(kc0 + c) * 256u + seg * 16;
         __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src),
                                          (__attribute__((address_space(3))) void*)(xs + (c * 16 + 4 * q) * 256), 16,
@@ -1723,7 +1735,7 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   // decode position of this lane's token (RoPE epilogue), loaded with the weights
   // (ATTN, one token: read through the scalar cache once the weights are in flight, in issue_kv: a
   // vector load here made the compiler wait for every load in flight before its first use)
-  int P = ROPE && !ATTN ? a.pos[min(tok0 + col, a.tokens - 1)] : 0;
+  int P = ROPE && !ATTN ? pos_p[min(tok0 + col, n_tok - 1)] : 0;
   // RoPE cos/sin of pairs p = 16*wave + 4g + q, q < 4, at position P (ATTN: loaded in issue_kv, ahead
   // of the K/V rows; otherwise after the slice barrier, in flight during the MFMAs)
   float4 rc = make_float4(1.0f, 1.0f, 1.0f, 1.0f), rs = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -1777,12 +1789,12 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
   // projection's 16x16x64 products cover, per 128-wide K chunk c, the K of row tiles 8c + {0,2,4,6}
   // (one product) and 8c + {1,3,5,7} (the other), so block rg takes tiles 8(rg/2) + 2 wave + rg%2 and
   // its 64 rows are exactly group rg.
-  const bool gmap = EPI == kEpiSiluMul && DUAL && !kMade && KSW == 1 && RTW == 1 && a.gsx_out != nullptr;
+  const bool gmap = EPI == kEpiSiluMul && DUAL && !kMade && KSW == 1 && RTW == 1 && gsx_out_set;
   auto row_tile = [&](int r) {
     return KW ? rg * RTW + r : gmap ? 8 * (rg >> 1) + 2 * wave + (rg & 1) : rg * 4 * RTW + wave + 4 * r;
   };
   float swv[RTW][4], sw2v[RTW][4], biasv[RTW][4];
-  const int tok_l = kHot ? 0 : min(tok0 + col, a.tokens - 1);
+  const int tok_l = kHot && kMade ? 0 : min(tok0 + col, n_tok - 1);
   float sx_l = 0.0f;
   int sh_l = 0, sl_l = 0;
   float gsv[GRP ? 2 * KC : 1];  // GRP: scales and offset terms of the lane's token's 2*KC groups
@@ -1815,7 +1827,7 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
         const size_t base = ((size_t)(ok[r] ? rt : 0) * nkc_all + kc0) * 64u + lane;
 #pragma unroll
         for (int d = 0; d < D; ++d) {
-          const uint4* wp = reinterpret_cast<const uint4*>(d ? a.wp2 : a.wp) + base;
+          const uint4* wp = reinterpret_cast<const uint4*>(d ? wp2_p : wp_p) + base;
 #pragma unroll
           for (int c = 0; c < KC; ++c) wv[r][d][c] = wp[(size_t)min(kg * KC + c, NKC - 1) * 64u];
         }
@@ -1829,8 +1841,22 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
           const size_t base = ((size_t)(ok[r] ? rt : 0) * nkc_all + kc0 + kg * KC + c) * 64u + lane;
 #pragma unroll
           for (int d = 0; d < D; ++d)  // cached: reused by the XCD's other token tiles
-            wv[r][d][c] = reinterpret_cast<const uint4*>(d ? a.wp2 : a.wp)[base];
+            wv[r][d][c] = reinterpret_cast<const uint4*>(d ? wp2_p : wp_p)[base];
         }
+    }
+  };
+  auto issue_groups = [&]() {
+    if constexpr (GRP) {
+      static_assert((2 * KC) % 4 == 0, "groups in float4 loads");
+      // 16-byte aligned: KC even, in_dim % 256 == 0
+      const size_t gb = (size_t)tok_l * ((kHot ? HOT_IN : a.in_dim) / 64) + 2 * (kc0 + kg * KC);
+#pragma unroll
+      for (int i = 0; i < 2 * KC; i += 4) {
+        const float4 s4 = *reinterpret_cast<const float4*>(gsx_p + gb + i);
+        const int4 c4 = *reinterpret_cast<const int4*>(gcorr_p + gb + i);
+        gsv[i] = s4.x, gsv[i + 1] = s4.y, gsv[i + 2] = s4.z, gsv[i + 3] = s4.w;
+        gcv[i] = c4.x, gcv[i + 1] = c4.y, gcv[i + 2] = c4.z, gcv[i + 3] = c4.w;
+      }
     }
   };
   auto issue_scalars = [&]() {
@@ -1863,17 +1889,7 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
       sh_l = a.sums[2 * tok_l];
       sl_l = a.sums[2 * tok_l + 1];
     }
-    if constexpr (GRP) {
-      static_assert((2 * KC) % 4 == 0, "groups in float4 loads");
-      const size_t gb = (size_t)tok_l * (a.in_dim / 64) + 2 * (kc0 + kg * KC);  // 16-byte aligned: KC even, in_dim % 256 == 0
-#pragma unroll
-      for (int i = 0; i < 2 * KC; i += 4) {
-        const float4 s4 = *reinterpret_cast<const float4*>(a.gsx + gb + i);
-        const int4 c4 = *reinterpret_cast<const int4*>(a.gcorr + gb + i);
-        gsv[i] = s4.x, gsv[i + 1] = s4.y, gsv[i + 2] = s4.z, gsv[i + 3] = s4.w;
-        gcv[i] = c4.x, gcv[i + 1] = c4.y, gcv[i + 2] = c4.z, gcv[i + 3] = c4.w;
-      }
-    }
+    if constexpr (GRP && !kHotB) issue_groups();
     if constexpr (kTab) tab_v = kExp2Tab[lane & 31];
     if constexpr (ATTN && PRE) {
       int lz;
@@ -1942,12 +1958,27 @@ __device__ __forceinline__ void gemm_skinny_body(const GemmArgs& a, int tt_count
     // order, so once at most the weight loads are outstanding its part of the slice has landed, and
     // after the barrier the whole slice has; chunk c's MFMAs then wait only for chunk c's weights
     // (the compiler's own waits on the weight registers), so the MFMAs run under the weight stream.
-    issue_scalars();
-    issue_slice();
-    issue_weights();
-    issue_kv();
-    __builtin_amdgcn_sched_barrier(0);  // every load above is in flight before any use
-    wait_vmcnt<RTW * D * KC + (ATTN ? 2 : 0) + kKvLoads>();
+    if constexpr (kHotB) {
+      // hot: the slice, the groups and the weights from the preloaded operands, then (once the
+      // argument segment has landed) the epilogue's scalars; at least the weight and K/V loads were
+      // issued after the slice
+      issue_slice();
+      issue_groups();
+      issue_weights();
+      __builtin_amdgcn_sched_barrier(0);  // (else the wait and the epilogue's addressing move above them)
+      kernarg_lines_wait(klines);
+      issue_scalars();
+      issue_kv();
+      __builtin_amdgcn_sched_barrier(0);
+      wait_vmcnt<RTW * D * KC + kKvLoads>();
+    } else {
+      issue_scalars();
+      issue_slice();
+      issue_weights();
+      issue_kv();
+      __builtin_amdgcn_sched_barrier(0);  // every load above is in flight before any use
+      wait_vmcnt<RTW * D * KC + (ATTN ? 2 : 0) + kKvLoads>();
+    }
     if (kTab && threadIdx.x < 32) exp_tab[threadIdx.x] = tab_v;
     if (kTab) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the table store lands before the barrier
     __builtin_amdgcn_s_barrier();
@@ -2416,6 +2447,19 @@ gemm_skinny_kernel(GemmArgs a, int tt_count, int rg_count, int splits) {
                                                                                       a, 0);
 }
 
+// The same for the model's shapes (IN -> OUT) with the operands of the first loads preloaded (HotArgs:
+// the activation code, the weights, the up matrix or group scales, the positions, offset terms or
+// grouped code's scales out, then the counts).
+template <int RTW, bool DUAL, int EPI, int NKC, bool ROPE, int KSW, bool GRP, int IN, int OUT>
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(3)))
+gemm_skinny_hot_kernel(const void* p0, const void* p1, const void* p2, const void* p3, int tokens, int tt_count,
+                       int rg_count, int splits, GemmArgs a) {
+  constexpr int kKb = kernarg_bytes<const void*, const void*, const void*, const void*, int, int, int, int, GemmArgs>();
+  gemm_skinny_body<RTW, DUAL, EPI, NKC, ROPE, KSW, false, kEpiStore, false, false, GRP, false, false, false, 16, kKb,
+                   IN, OUT>(a, tt_count, rg_count, splits, a, 0, AttnMergeArgs{}, AttnFuseArgs{},
+                            HotArgs{p0, p1, p2, p3, nullptr, nullptr, tokens});
+}
+
 // One token, the activation row quantized by every block for its own K chunks (see PRE_QUANT above;
 // KW: the block's waves split K).
 template <int RTW, int EPI, int NKC, bool KW = false>
@@ -2670,10 +2714,14 @@ __global__ void __launch_bounds__(256) reduce_norm_quant_kernel(GemmArgs a, int 
 // or a token row of a GEMM's LDS activation slice), the scale and limb sums to sx_out / sums_out;
 // the finished row goes to a.y (and a.y_raw) when write_y.
 // `issue` runs right after the row's loads are issued (a caller's own loads then queue behind them).
-template <int EPI, int ZB, class Issue, int W>
+// HOT: the first loads' operands from HotArgs (p0 partials, p1 residual rows of 1536 floats or the
+// bias or a stand-in, p2 row scales, p3 norm weights or a stand-in, p4 limb sums, p5 scales, n0 the
+// token count), the flags read from `a` after the loads are issued; the outputs are the token's row
+// of a.xq_out (chunk_stride 256), a.sx_out and a.sums_out, whatever xq_row, sx_out and sums_out say.
+template <int EPI, int ZB, class Issue, int W, bool HOT>
 __device__ __forceinline__ void reduce_norm_quant_row_zb(const GemmArgs& a, int splits, int tok, int8_t* xq_row,
                                                          int chunk_stride, float* sx_out, int* sums_out, bool write_y,
-                                                         Issue&& issue) {
+                                                         Issue&& issue, const HotArgs& hot) {
   static_assert(W == 1 || W == 2, "one or two waves per row");
   constexpr int NV = QWEN_HIDDEN / (256 * W);
   constexpr int LS = 64 * W;                  // float4 stride between a lane's columns
@@ -2683,19 +2731,25 @@ __device__ __forceinline__ void reduce_norm_quant_row_zb(const GemmArgs& a, int 
   __shared__ float x_ssf[W > 1 ? 2 : 1], x_amax[W > 1 ? 2 : 1];
   __shared__ int x_sums[W > 1 ? 4 : 1];
   const int wv = (threadIdx.x >> 6) & (W - 1);
-  const size_t zstride4 = (size_t)a.tokens * (QWEN_HIDDEN / 4);
-  const float4* pt = reinterpret_cast<const float4*>(a.part + (size_t)tok * QWEN_HIDDEN) + lane;
-  const float4* sw4 = reinterpret_cast<const float4*>(a.sw) + lane;
-  const bool has_add = EPI == kEpiResidual || a.bias != nullptr;
-  const bool has_w = a.norm != kNormNone;
+  const size_t zstride4 = (size_t)(HOT ? hot.n0 : a.tokens) * (QWEN_HIDDEN / 4);
+  const float* part = HOT ? static_cast<const float*>(hot.p0) : a.part;
+  const float4* pt = reinterpret_cast<const float4*>(part + (size_t)tok * QWEN_HIDDEN) + lane;
+  const float4* sw4 = reinterpret_cast<const float4*>(HOT ? hot.p2 : a.sw) + lane;
   // Every load in one batch and without branches (a single memory round trip for up to ZB splits): an
   // absent operand (bias, norm weights) is read from the row scales and zeroed after, and the splits of
   // a batch past the last one read the last split again and are not added.
-  const float4* r4 = EPI == kEpiResidual ? reinterpret_cast<const float4*>(a.resid + (size_t)tok * a.resid_stride) + lane
-                                         : (a.bias ? reinterpret_cast<const float4*>(a.bias) + lane : sw4);
-  const float4* w4 = has_w ? reinterpret_cast<const float4*>(a.norm_w) + lane : sw4;
-  const int sum_h = a.sums[2 * tok], sum_l = a.sums[2 * tok + 1];
-  const float sx_tok = a.sx[tok];
+  const float4* r4 =
+      HOT ? reinterpret_cast<const float4*>(static_cast<const float*>(hot.p1) +
+                                            (EPI == kEpiResidual ? (size_t)tok * QWEN_HIDDEN : 0)) + lane
+      : EPI == kEpiResidual ? reinterpret_cast<const float4*>(a.resid + (size_t)tok * a.resid_stride) + lane
+                            : (a.bias ? reinterpret_cast<const float4*>(a.bias) + lane : sw4);
+  const float4* w4 = HOT                 ? reinterpret_cast<const float4*>(hot.p3) + lane
+                     : a.norm != kNormNone ? reinterpret_cast<const float4*>(a.norm_w) + lane
+                                           : sw4;
+  const int* sums = HOT ? static_cast<const int*>(hot.p4) : a.sums;
+  const float* sxs = HOT ? static_cast<const float*>(hot.p5) : a.sx;
+  const int sum_h = sums[2 * tok], sum_l = sums[2 * tok + 1];
+  const float sx_tok = sxs[tok];
   float4 acc[NV], sw[NV], ad[NV], wn[NV];
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
@@ -2706,7 +2760,37 @@ __device__ __forceinline__ void reduce_norm_quant_row_zb(const GemmArgs& a, int 
   // split sums in z order
 #pragma unroll
   for (int j = 0; j < NV; ++j) acc[j] = make_float4(0, 0, 0, 0);
-  for (int z0 = 0; z0 < splits; z0 += ZB) {
+  if constexpr (HOT) {
+    // splits <= ZB (the launcher checks), straight-line: every split's loads issued unconditionally
+    // (past the last split the last again, unused; without splits the row scales), `issue`, then the
+    // adds as selects (adding +0 leaves a sum that started at +0 unchanged)
+    const float4* pt0 = splits > 0 ? pt : sw4;
+    const int zlast = max(splits, 1) - 1;
+    float4 pz[ZB][NV];
+#pragma unroll
+    for (int u = 0; u < ZB; ++u)
+#pragma unroll
+      for (int j = 0; j < NV; ++j) pz[u][j] = pt0[(size_t)min(u, zlast) * zstride4 + LS * j];
+    __builtin_amdgcn_sched_barrier(0);
+    issue();
+    __builtin_amdgcn_sched_barrier(0);
+    // the outputs: the token's row of a.xq_out, its scale and limb sums (addressed only now)
+    xq_row = a.xq_out + (size_t)tok * (2 * QWEN_HIDDEN);
+    sx_out = a.sx_out + tok;
+    sums_out = a.sums_out + 2 * tok;
+#pragma unroll
+    for (int u = 0; u < ZB; ++u) {
+      const bool live = u < splits;
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        acc[j].x += live ? pz[u][j].x : 0.0f;
+        acc[j].y += live ? pz[u][j].y : 0.0f;
+        acc[j].z += live ? pz[u][j].z : 0.0f;
+        acc[j].w += live ? pz[u][j].w : 0.0f;
+      }
+    }
+  }
+  for (int z0 = 0; !HOT && z0 < splits; z0 += ZB) {
     float4 pz[ZB][NV];
 #pragma unroll
     for (int u = 0; u < ZB; ++u)
@@ -2728,7 +2812,9 @@ __device__ __forceinline__ void reduce_norm_quant_row_zb(const GemmArgs& a, int 
           acc[j].w += pz[u][j].w;
         }
   }
-  if (splits < 1) issue();  // the caller's loads are issued exactly once, also without splits
+  if (!HOT && splits < 1) issue();  // the caller's loads are issued exactly once, also without splits
+  const bool has_add = EPI == kEpiResidual || a.bias != nullptr;
+  const bool has_w = a.norm != kNormNone;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     if (!has_add) ad[j] = make_float4(0, 0, 0, 0);
@@ -2991,6 +3077,26 @@ __global__ void __launch_bounds__(128) reduce_norm_quant_pair_kernel(GemmArgs a,
                                                   NoIssue{});
 }
 
+// The same with the first loads' operands preloaded (HotArgs of reduce_norm_quant_row_zb), residual
+// rows 1536 floats apart.
+template <int EPI>
+__global__ void __launch_bounds__(128) reduce_norm_quant_pair_hot_kernel(const void* p0, const void* p1, const void* p2,
+                                                                         const void* p3, const void* p4, const void* p5,
+                                                                         int tokens, int splits, GemmArgs a) {
+  const auto klines = kernarg_lines_issue<kernarg_bytes<const void*, const void*, const void*, const void*,
+                                                        const void*, const void*, int, int, GemmArgs>()>();
+  const HotArgs hot{p0, p1, p2, p3, p4, p5, tokens};
+  auto issue = [&]() { kernarg_lines_wait(klines); };
+  const int tok = blockIdx.x;
+  // (the outputs are addressed inside, once the loads are issued)
+  if (splits == 1)
+    reduce_norm_quant_row_zb<EPI, 1, decltype(issue)&, 2, true>(a, splits, tok, nullptr, 256, nullptr, nullptr, true,
+                                                                issue, hot);
+  else
+    reduce_norm_quant_row_zb<EPI, 5, decltype(issue)&, 2, true>(a, splits, tok, nullptr, 256, nullptr, nullptr, true,
+                                                                issue, hot);
+}
+
 // ---------------------------------------------------------------------------------------------
 // RoPE of q (in place) and k, plus the K/V cache append, for rows of a fused [q | k | v] buffer
 // (qkv_stride floats per token).  Decode: token b is sequence b at position pos[b].  Prefill:
@@ -3142,8 +3248,11 @@ attn_decode_kernel(const float* __restrict__ qkv, int qkv_stride, const float* _
                    const float* __restrict__ v_cache, size_t seq_stride, const int* __restrict__ pos, int chunk,
                    int max_keys, float* __restrict__ part, float2* __restrict__ pml, unsigned* __restrict__ arrivals,
                    float* __restrict__ ctx, int8_t* __restrict__ xq, float* __restrict__ sx, int* __restrict__ sums) {
-  touch_kernargs<kernarg_bytes<const float*, int, const float*, const float*, size_t, const int*, int, int, float*,
-                               float2*, unsigned*, float*, int8_t*, float*, int*>()>();
+  // (the leading 14 argument dwords, through max_keys, are preloaded: the first loads wait for nothing;
+  // the segment's other lines are requested at entry and waited for once the first tile is in flight)
+  const auto klines = kernarg_lines_issue<kernarg_bytes<const float*, int, const float*, const float*, size_t,
+                                                        const int*, int, int, float*, float2*, unsigned*, float*,
+                                                        int8_t*, float*, int*>()>();
   __shared__ __align__(16) float qs[16][kQRow];
   __shared__ __align__(16) float s_acc[4][QWEN_GROUPS][QWEN_HEAD_DIM];  // reused by the merge step
   __shared__ float s_m[4][QWEN_GROUPS], s_l[4][QWEN_GROUPS];
@@ -3192,6 +3301,7 @@ attn_decode_kernel(const float* __restrict__ qkv, int qkv_stride, const float* _
         for (int h = 0; h < 2; ++h) vr0[r][h] = ld_stream(reinterpret_cast<const float4*>(vrow + 64 * h));
       }
     }
+    kernarg_lines_wait(klines);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int i = threadIdx.x + 256 * j;
@@ -3635,7 +3745,14 @@ static void launch_reduce(const GemmArgs& a, int splits, hipStream_t st) {
   if (a.fuse == kFuseQkvRope) {
     hipLaunchKernelGGL(reduce_qkv_rope_kernel, dim3(a.tokens), dim3(256), 0, st, a, splits);
   } else if (a.fuse == kFuseNormQuant) {
-    if (a.out_dim == QWEN_HIDDEN)
+    if (a.out_dim == QWEN_HIDDEN && splits <= 5 && (EPI != kEpiResidual || a.resid_stride == QWEN_HIDDEN)) {
+      // the first loads' operands preloaded (an absent bias or norm weight read from the row scales)
+      const void* add = EPI == kEpiResidual ? (const void*)a.resid : a.bias ? (const void*)a.bias : a.sw;
+      const void* nw = a.norm != kNormNone ? (const void*)a.norm_w : a.sw;
+      hipLaunchKernelGGL((reduce_norm_quant_pair_hot_kernel<EPI>), dim3(a.tokens), dim3(128), 0, st,
+                         (const void*)a.part, add, (const void*)a.sw, nw, (const void*)a.sums, (const void*)a.sx,
+                         a.tokens, splits, a);
+    } else if (a.out_dim == QWEN_HIDDEN)
       hipLaunchKernelGGL((reduce_norm_quant_pair_kernel<EPI>), dim3(a.tokens), dim3(128), 0, st, a, splits);
     else
       hipLaunchKernelGGL((reduce_norm_quant_kernel<EPI>), dim3(a.tokens), dim3(256), 0, st, a, splits);
@@ -3683,6 +3800,17 @@ static void launch_skinny_t(const GemmArgs& a, int rg_count, int splits, hipStre
   const int tt = (a.tokens + 15) / 16;
   const int groups = rg_count * splits;
   const int blocks = 8 * tt * ((groups + 7) / 8);
+  // the model's shapes: the kernel with the first loads' operands preloaded
+  constexpr int kIn = NKC == 12 ? QWEN_HIDDEN : NKC == 14 ? QWEN_INTERMEDIATE : 0;
+  constexpr int kOut = NKC == 14 ? QWEN_HIDDEN : ROPE ? QWEN_QKV_ROWS : DUAL ? QWEN_INTERMEDIATE : QWEN_HIDDEN;
+  if (kIn > 0 && a.in_dim == kIn && a.out_dim == kOut && splits * NKC * kKChunk == kIn) {
+    const void* p2 = GRP ? (const void*)a.gsx : DUAL ? (const void*)a.wp2 : nullptr;
+    const void* p3 = GRP ? (const void*)a.gcorr : ROPE ? (const void*)a.pos : DUAL ? (const void*)a.gsx_out : nullptr;
+    hipLaunchKernelGGL((gemm_skinny_hot_kernel<RTW, DUAL, EPI, NKC, ROPE, KSW, GRP, kIn, kOut>), dim3(blocks),
+                       dim3(256 * KSW), 0, st, (const void*)a.xq, (const void*)a.wp, p2, p3, a.tokens, tt, rg_count,
+                       splits, a);
+    return;
+  }
   hipLaunchKernelGGL((gemm_skinny_kernel<RTW, DUAL, EPI, NKC, ROPE, KSW, GRP>), dim3(blocks), dim3(256 * KSW), 0, st, a,
                      tt, rg_count, splits);
 }
