@@ -98,10 +98,12 @@ def integer_rows(seed, tokens, n, small, large):
 # (tokens, in_dim, out_dim, flags): the kernel each shape takes inside launch_gemm_i8
 SHAPES = [
     (1, 1536, 2048, 0),     # skinny, one K group (decode Q/K/V shape)
-    (16, 1536, 1536, 0),    # skinny, one token tile
+    (1, 1536, 1536, 0),     # skinny, one token, the O shape (operands of the first loads preloaded)
+    (16, 1536, 1536, 0),    # skinny, one token tile (preloaded operands)
+    (64, 1536, 1536, 0),    # skinny, four token tiles (preloaded operands)
     (64, 1536, 8960, 0),    # skinny, four token tiles (decode gate/up shape)
-    (1, 8960, 1536, 0),     # skinny, 5 K splits of 14 chunks + reduce (decode down)
-    (64, 8960, 1536, 0),    # skinny, 5 K splits, four token tiles
+    (1, 8960, 1536, 0),     # skinny, 5 K splits of 14 chunks + reduce (decode down; preloaded operands)
+    (64, 8960, 1536, 0),    # skinny, 5 K splits, four token tiles (preloaded operands)
     (5, 8960, 1536, 1),     # direct-load kernel, in-block 4-way K split (no split workspace)
     (7, 1536, 1040, 0),     # direct-load kernel (out_dim not a multiple of 64)
     (40, 1536, 1040, 0),    # pipelined 4-stage, cross-block K split over 12 blocks + reduce
