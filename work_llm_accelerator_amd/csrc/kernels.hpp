@@ -175,8 +175,9 @@ void launch_rope_qkv(float* qkv, int qkv_stride, const int* pos, int seq_len, in
                      const float* rope, float* k_cache, float* v_cache, size_t seq_stride, hipStream_t st);
 // Decode attention split: nsplit blocks of `chunk` keys (a multiple of 16) per sequence and KV
 // head, sized so that one launch fills the device once.  Workspace: part [batch][12][nsplit][128]
-// floats, pml [batch][12][nsplit] (m, l) pairs, arrivals [batch] counters that must be zero before
-// the first launch (every launch leaves them at zero).
+// floats, pml [batch][12][nsplit] (m, l) pairs.  launch_attn_decode leaves the split partials there,
+// then (xq given) merges them into the context row, written to ctx when given, and its two-limb
+// code (xq, sx, sums); batch <= 65535 (one grid z index per sequence).
 struct AttnDecodePlan {
   int nsplit, chunk;
 };
@@ -185,8 +186,7 @@ AttnDecodePlan plan_attn_decode(int batch, int max_keys, int cus = 0);
 void launch_zero_u32(unsigned* p, int n, hipStream_t st);
 void launch_attn_decode(const float* qkv, int qkv_stride, const float* k_cache, const float* v_cache,
                         size_t seq_stride, const int* pos, int batch, int max_keys, const AttnDecodePlan& plan,
-                        float* part, float2* pml, unsigned* arrivals, float* ctx, int8_t* xq, float* sx, int* sums,
-                        hipStream_t st);
+                        float* part, float2* pml, float* ctx, int8_t* xq, float* sx, int* sums, hipStream_t st);
 // Prefill attention of S new tokens per sequence at positions past..past+S-1 over the cache rows
 // 0..past+S-1: K/V converted once into bf16 hi/lo tiles (workspace of
 // attn_prefill_workspace_bytes(past + S, nseq)), then the causal attention over them.

@@ -44,24 +44,6 @@ __device__ __forceinline__ float2 ld_stream(const float2* p) {
   return make_float2(v[0], v[1]);
 }
 
-// Device-coherent (agent-scope) store and load: visible across XCDs without an L2 write-back.
-__device__ __forceinline__ void store_agent(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float load_agent(const float* p) {
-  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// The same for a pair of floats, as one 8-byte access.
-__device__ __forceinline__ void store_agent2(float2* p, float x, float y) {
-  const uint64_t v = (uint64_t)__float_as_uint(x) | ((uint64_t)__float_as_uint(y) << 32);
-  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float2 load_agent2(const float2* p) {
-  const uint64_t v =
-      __hip_atomic_load(reinterpret_cast<uint64_t*>(const_cast<float2*>(p)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return make_float2(__uint_as_float((uint32_t)v), __uint_as_float((uint32_t)(v >> 32)));
-}
-
 // Prefill SiLU for the FAST GEMM epilogue: v / (1 + e(-v)) with the division as v * rcp(1 + e)
 // (v_rcp_f32, 1 ulp).  For s = -v >= -1 the reference's approx_exp is its degree-6 Taylor series
 // (qwen_prefill_mlp_kernel.cpp:158-181, no halving), kept here in Horner form (a few ulp from the
@@ -3139,8 +3121,8 @@ __global__ void __launch_bounds__(64) rope_qkv_kernel(float* __restrict__ qkv, i
 }
 
 // ---------------------------------------------------------------------------------------------
-// Decode attention on the fp32 matrix cores, split over the KV length, with the split merge and
-// the O-projection input quantization fused in (qwen_decode_attention_kernel.cpp:113-162 semantics:
+// Decode attention on the fp32 matrix cores, split over the KV length; the split merge and the
+// O-projection input quantization follow in attn_decode_merge_kernel (qwen_decode_attention_kernel.cpp:113-162 semantics:
 // s_t = (q . k_t) * 0.08838834764831845f over keys 0..pos, softmax, ctx = sum_t p_t v_t; here with
 // an online softmax, reordered sums and __expf).
 // grid = (nsplit, 2 KV heads, batch), block = 256 (4 waves).  Block (split c, KV head kvh, sequence
@@ -3154,11 +3136,12 @@ __global__ void __launch_bounds__(64) rope_qkv_kernel(float* __restrict__ qkv, i
 //   O += P . V:   MFMA (r, h, e): A = P[head col][key 4g+r] (the lane's own p[r]),
 //                 B = V[key 4g+r][dim 4col+e+64h]; lane holds O[head 4g+r'][dim 4col+e+64h].
 // The block merges its 4 waves in LDS and writes (m, l, acc[128]) per query head to
-// part[b][head][c][128] and pml[b][head][c] with device-coherent stores and counts itself in
-// arrivals[b]; the last of the sequence's 2*nsplit blocks to arrive merges the sequence's splits
-// into ctx[b] (optional), quantizes that row for the O projection (xq, sx, sums) and re-arms
-// arrivals[b] to 0 for the next launch.  With xq == nullptr the launch ends after the partials (the
-// O projection of a one-sequence decode merges them in every block: attn_merge_quant_slice).
+// part[b][head][c][128] and pml[b][head][c] with plain stores (the launch boundary publishes them).
+// The splits are merged by the next launch: the merge kernel below, or for one sequence every block
+// of the O projection (attn_merge_quant_slice).  (Merged inside this launch by the last-arriving
+// block of each sequence, the partials needed device-coherent stores, an arrival count and
+// device-coherent reloads, all behind the other blocks' key stream: 95 us per 64 x 4096 launch
+// against 85 us for the partials alone plus ~1.2 us of launch hand-off and the merge launch.)
 // ---------------------------------------------------------------------------------------------
 typedef float v4f __attribute__((ext_vector_type(4)));
 constexpr int kQRow = QWEN_HEAD_DIM + 4;  // LDS floats per query row (16-byte pad: no bank aliasing)
@@ -3246,21 +3229,14 @@ __device__ __forceinline__ void attn_decode_tile(const float* __restrict__ kb, c
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
 attn_decode_kernel(const float* __restrict__ qkv, int qkv_stride, const float* __restrict__ k_cache,
                    const float* __restrict__ v_cache, size_t seq_stride, const int* __restrict__ pos, int chunk,
-                   int max_keys, float* __restrict__ part, float2* __restrict__ pml, unsigned* __restrict__ arrivals,
-                   float* __restrict__ ctx, int8_t* __restrict__ xq, float* __restrict__ sx, int* __restrict__ sums) {
+                   int max_keys, float* __restrict__ part, float2* __restrict__ pml) {
   // (the leading 14 argument dwords, through max_keys, are preloaded: the first loads wait for nothing;
   // the segment's other lines are requested at entry and waited for once the first tile is in flight)
-  const auto klines = kernarg_lines_issue<kernarg_bytes<const float*, int, const float*, const float*, size_t,
-                                                        const int*, int, int, float*, float2*, unsigned*, float*,
-                                                        int8_t*, float*, int*>()>();
+  const auto klines = kernarg_lines_issue<
+      kernarg_bytes<const float*, int, const float*, const float*, size_t, const int*, int, int, float*, float2*>()>();
   __shared__ __align__(16) float qs[16][kQRow];
-  __shared__ __align__(16) float s_acc[4][QWEN_GROUPS][QWEN_HEAD_DIM];  // reused by the merge step
+  __shared__ __align__(16) float s_acc[4][QWEN_GROUPS][QWEN_HEAD_DIM];
   __shared__ float s_m[4][QWEN_GROUPS], s_l[4][QWEN_GROUPS];
-  __shared__ float red_f[4];
-  __shared__ int red_i[8];
-  __shared__ int s_last;
-  static_assert(2 * QWEN_Q_HEADS * kAttnMaxSplits <= 4 * QWEN_GROUPS * QWEN_HEAD_DIM && QWEN_HIDDEN <= 16 * kQRow,
-                "merge scratch");
   const int nsplit = gridDim.x;
   const int c = blockIdx.x;
   const int kvh = blockIdx.y;
@@ -3362,73 +3338,84 @@ attn_decode_kernel(const float* __restrict__ qkv, int qkv_stride, const float* _
         A += s_acc[w][head][d] * f;
       }
       const int qh = kvh * QWEN_GROUPS + head;
-      store_agent(&part[(((size_t)b * QWEN_Q_HEADS + qh) * nsplit + c) * QWEN_HEAD_DIM + d], A);
+      part[(((size_t)b * QWEN_Q_HEADS + qh) * nsplit + c) * QWEN_HEAD_DIM + d] = A;
       if (d == 0) {
-        store_agent2(&pml[((size_t)b * QWEN_Q_HEADS + qh) * nsplit + c], M, L);
+        pml[((size_t)b * QWEN_Q_HEADS + qh) * nsplit + c] = make_float2(M, L);
       }
     }
   }
+}
 
-  if (xq == nullptr) return;  // partials only: the next launch merges them
-
-  // Arrival.  The partials were written with device-coherent (agent-scope) stores; once every wave
-  // has waited for its stores to complete, they are visible to every XCD, and one thread counts the
-  // block.  The last block reads them back with device-coherent loads, so no cache write-back or
-  // invalidation is needed on either side.
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (threadIdx.x == 0) s_last = atomicAdd(&arrivals[b], 1u) == gridDim.x * gridDim.y - 1u;  // splits x KV heads
-  __syncthreads();
-  if (!s_last) return;
-
-  // Merge of the sequence's splits (the last block only).  The (m, l) pairs and this thread's first
-  // 8 splits of partial values are loaded together, so sequences with at most 8 splits need one
-  // memory round trip.  Thread t owns dims d = t & 127 of heads (t >> 7) + 2k, k < 6.
+// The split merge of attn_decode_kernel's partials, one block per sequence: per head the merge
+// weights of the splits that hold keys (merge_split_weights), the weighted sum of their partial rows
+// in split order into the context row (written to ctx when given), then the row's two-limb code,
+// scale and limb sums for the O projection (quantize_row_lds).  Thread t owns float4 columns t and
+// t + 256 (< 384) of the row.  Every load of a batch of 8 splits is issued unconditionally (splits
+// past the last one load the last again, unused) together with the (m, l) pairs, so sequences with
+// at most 8 splits need one memory round trip.
+__global__ void __launch_bounds__(256) attn_decode_merge_kernel(const float* __restrict__ part,
+                                                                const float2* __restrict__ pml,
+                                                                const int* __restrict__ pos, int nsplit, int chunk,
+                                                                int max_keys, float* __restrict__ ctx,
+                                                                int8_t* __restrict__ xq, float* __restrict__ sx,
+                                                                int* __restrict__ sums) {
+  constexpr int kF4 = QWEN_HIDDEN / 4;  // float4 columns of the row
+  __shared__ __align__(16) float row[QWEN_HIDDEN];         // the context row
+  __shared__ float ml[QWEN_Q_HEADS * kAttnMaxSplits * 2];  // (m, l), then merge weights in place
+  __shared__ float red_f[4];
+  __shared__ int red_i[8];
+  const int b = blockIdx.x;
+  const int n = min(max(pos[b], 0) + 1, max_keys);
   const int nc = (n + chunk - 1) / chunk;  // splits that hold keys
-  float* ml = &s_acc[0][0][0];             // [12][kAttnMaxSplits][2] (m, l), then merge weights in place
-  float* row = &qs[0][0];                  // [1536] context row
   const float2* pb = pml + (size_t)b * QWEN_Q_HEADS * nsplit;
-  const int d = threadIdx.x & 127;
-  const int h0 = threadIdx.x >> 7;
-  const float* pa = part + (size_t)b * QWEN_Q_HEADS * nsplit * QWEN_HEAD_DIM + d;
-  float pv[6][8];
+  const float* pa = part + (size_t)b * QWEN_Q_HEADS * nsplit * QWEN_HEAD_DIM;
+  const int f[2] = {(int)threadIdx.x, min((int)threadIdx.x + 256, kF4 - 1)};
+  const bool two = threadIdx.x + 256 < kF4;  // wave-uniform
+  float4 pv[2][8];
   auto load_part = [&](int s0) {
 #pragma unroll
-    for (int k = 0; k < 6; ++k)
+    for (int u = 0; u < 2; ++u) {
+      const int h = f[u] >> 5, d4 = 4 * (f[u] & 31);
 #pragma unroll
       for (int j = 0; j < 8; ++j)
-        pv[k][j] = s0 + j < nc ? load_agent(pa + ((size_t)(h0 + 2 * k) * nsplit + s0 + j) * QWEN_HEAD_DIM) : 0.0f;
+        pv[u][j] = *reinterpret_cast<const float4*>(pa + ((size_t)h * nsplit + min(s0 + j, nc - 1)) * QWEN_HEAD_DIM + d4);
+    }
   };
   load_part(0);
   for (int i = threadIdx.x; i < QWEN_Q_HEADS * nc; i += 256) {
     const int h = i / nc, sp = i % nc;
-    const float2 v = load_agent2(pb + h * nsplit + sp);  // (m, l) in one memory round trip
+    const float2 v = pb[h * nsplit + sp];  // (m, l) in one memory round trip
     ml[(h * kAttnMaxSplits + sp) * 2] = v.x;
     ml[(h * kAttnMaxSplits + sp) * 2 + 1] = v.y;
   }
   __syncthreads();
   merge_split_weights(ml, nc, nullptr, false);
   __syncthreads();
-  float out[6];
-#pragma unroll
-  for (int k = 0; k < 6; ++k) out[k] = 0.0f;
+  float4 out[2] = {make_float4(0.0f, 0.0f, 0.0f, 0.0f), make_float4(0.0f, 0.0f, 0.0f, 0.0f)};
   for (int s0 = 0; s0 < nc; s0 += 8) {
     if (s0 > 0) load_part(s0);
 #pragma unroll
-    for (int k = 0; k < 6; ++k)
+    for (int u = 0; u < 2; ++u) {
+      const int h = f[u] >> 5;
 #pragma unroll
       for (int j = 0; j < 8; ++j)
-        if (s0 + j < nc) out[k] += pv[k][j] * ml[((h0 + 2 * k) * kAttnMaxSplits + s0 + j) * 2];
+        if (s0 + j < nc) {  // block-uniform
+          const float w = ml[(h * kAttnMaxSplits + s0 + j) * 2];
+          out[u].x += pv[u][j].x * w;
+          out[u].y += pv[u][j].y * w;
+          out[u].z += pv[u][j].z * w;
+          out[u].w += pv[u][j].w * w;
+        }
+    }
   }
 #pragma unroll
-  for (int k = 0; k < 6; ++k) {
-    const int i = (h0 + 2 * k) * QWEN_HEAD_DIM + d;
-    row[i] = out[k];
-    if (ctx) ctx[(size_t)b * QWEN_HIDDEN + i] = out[k];
+  for (int u = 0; u < 2; ++u) {
+    if (u == 1 && !two) break;
+    reinterpret_cast<float4*>(row)[f[u]] = out[u];
+    if (ctx) reinterpret_cast<float4*>(ctx + (size_t)b * QWEN_HIDDEN)[f[u]] = out[u];
   }
   __syncthreads();
   quantize_row_lds(row, QWEN_HIDDEN, xq + (size_t)b * (2 * QWEN_HIDDEN), sx + b, sums + 2 * b, red_f, red_i);
-  if (threadIdx.x == 0) arrivals[b] = 0u;
 }
 
 __global__ void zero_u32_kernel(unsigned* __restrict__ p, int n) {
@@ -4108,10 +4095,12 @@ void launch_zero_u32(unsigned* p, int n, hipStream_t st) {
 
 void launch_attn_decode(const float* qkv, int qkv_stride, const float* k_cache, const float* v_cache,
                         size_t seq_stride, const int* pos, int batch, int max_keys, const AttnDecodePlan& plan,
-                        float* part, float2* pml, unsigned* arrivals, float* ctx, int8_t* xq, float* sx, int* sums,
-                        hipStream_t st) {
+                        float* part, float2* pml, float* ctx, int8_t* xq, float* sx, int* sums, hipStream_t st) {
   hipLaunchKernelGGL(attn_decode_kernel, dim3(plan.nsplit, QWEN_KV_HEADS, batch), dim3(256), 0, st, qkv, qkv_stride,
-                     k_cache, v_cache, seq_stride, pos, plan.chunk, max_keys, part, pml, arrivals, ctx, xq, sx, sums);
+                     k_cache, v_cache, seq_stride, pos, plan.chunk, max_keys, part, pml);
+  if (xq)
+    hipLaunchKernelGGL(attn_decode_merge_kernel, dim3(batch), dim3(256), 0, st, part, pml, pos, plan.nsplit, plan.chunk,
+                       max_keys, ctx, xq, sx, sums);
 }
 
 size_t attn_prefill_workspace_bytes(int keys, int nseq) {

@@ -26,7 +26,7 @@ struct FastLayer {
 };
 
 constexpr size_t kQkvRows = QWEN_QKV_ROWS;  // 2048
-constexpr size_t kMaxArrivals = 4096;       // most sequences of one FAST decode call
+constexpr size_t kMaxDecodeBatch = 65535;    // most sequences of one FAST decode call (attention grid z)
 constexpr size_t kRepackedLayerBytes = QWEN_PACKED_WEIGHT_BYTES;
 
 // Device buffer that only grows (freed after a device synchronize); `generation` counts the
@@ -78,19 +78,16 @@ struct qwen_hip_model {
   DevBuf head_ws;                 // head: normalized rows and per-block argmax candidates
   Arena arena;                    // ORDERED per-layer intermediates
   DevBuf ws;                      // FAST workspace and ORDERED attention output
-  unsigned arrivals_ready = 0;    // ws generation whose arrival counters were zeroed
+  unsigned zero_sums_ready = 0;   // ws generation whose zero limb sums were written
   LastCall last;
 
   // FAST workspace carve-up for `tokens` rows and `batch` x `nsplit` decode-attention partials.
-  // The decode-attention arrival counters (one per sequence, batch <= kMaxArrivals) sit at offset 0
-  // of every carve-up and return to zero after each launch, so they are zeroed once per buffer.
   struct Ws {
     int8_t* xq;
     float* sx;
     int* sums;
     float *qkv, *ctx, *att, *s, *tmp, *part;
     float2* pml;
-    unsigned* arrivals;
     float* splitk;  // K-split partials of the non-dual projections (out <= 2048)
     uint8_t* kvt;   // prefill attention: bf16 hi/lo K/V tiles of one layer
     int8_t* gxq;    // grouped code of the SiLU·up rows (2..64 tokens): limbs, per-(token, 64-row group)
@@ -99,11 +96,9 @@ struct qwen_hip_model {
     const int* zero_sums;  // kSkinnyTokens x (0, 0): the limb sums of code whose offsets are applied per group
     float* gmax;           // one token: max |SiLU.up| of each 16-row block of the gate/up projection
   };
-  // Fixed region at the start of the workspace: the decode attention's arrival counters, then the zero
-  // limb sums; both are zeroed once per workspace buffer and never written otherwise (the counters
-  // are re-armed by the attention itself).
-  static constexpr size_t kZeroSumsOffset = (kMaxArrivals * 4u + 255u) & ~size_t(255u);
-  static constexpr size_t kFixedBytes = kZeroSumsOffset + ((kSkinnyTokens * 8u + 255u) & ~size_t(255u));
+  // Fixed region at the start of the workspace: the zero limb sums, zeroed once per workspace buffer
+  // and never written otherwise.
+  static constexpr size_t kFixedBytes = (kSkinnyTokens * 8u + 255u) & ~size_t(255u);
   Ws carve(size_t tokens, size_t batch, size_t nsplit, size_t kvt_bytes = 0) {
     size_t off = 0;
     auto take = [&](size_t bytes) {
@@ -111,8 +106,7 @@ struct qwen_hip_model {
       off = (off + bytes + 255u) & ~size_t(255u);
       return o;
     };
-    const size_t o_arr = take(kMaxArrivals * 4u);  // fixed offsets: never overlap the parts below
-    const size_t o_zs = take(kSkinnyTokens * 8u);
+    const size_t o_zs = take(kSkinnyTokens * 8u);  // fixed offset: never overlaps the parts below
     const size_t o_xq = take(xq_bytes(tokens, QWEN_INTERMEDIATE));
     const size_t o_sx = take(tokens * 4u);
     const size_t o_sums = take(tokens * 8u);
@@ -131,17 +125,15 @@ struct qwen_hip_model {
     const size_t o_gcorr = take(gtok * (QWEN_INTERMEDIATE / 64) * 4u);
     const size_t o_gmax = take((QWEN_INTERMEDIATE / 16) * 4u);
     char* b = static_cast<char*>(ws.get(off));
-    unsigned* arr = reinterpret_cast<unsigned*>(b + o_arr);
-    if (ws.generation != arrivals_ready) {  // fresh buffer: arm the counters and zero the sums once
-      static_assert(kZeroSumsOffset == kMaxArrivals * 4u, "counters and zero sums are one run of words");
-      launch_zero_u32(arr, (int)(kMaxArrivals + 2 * kSkinnyTokens), stream);
-      arrivals_ready = ws.generation;
+    if (ws.generation != zero_sums_ready) {  // fresh buffer: zero the sums once
+      launch_zero_u32(reinterpret_cast<unsigned*>(b + o_zs), (int)(2 * kSkinnyTokens), stream);
+      zero_sums_ready = ws.generation;
     }
     return Ws{reinterpret_cast<int8_t*>(b + o_xq), reinterpret_cast<float*>(b + o_sx),
               reinterpret_cast<int*>(b + o_sums), reinterpret_cast<float*>(b + o_qkv),
               reinterpret_cast<float*>(b + o_ctx), reinterpret_cast<float*>(b + o_att),
               reinterpret_cast<float*>(b + o_s), reinterpret_cast<float*>(b + o_tmp),
-              reinterpret_cast<float*>(b + o_part), reinterpret_cast<float2*>(b + o_pml), arr,
+              reinterpret_cast<float*>(b + o_part), reinterpret_cast<float2*>(b + o_pml),
               reinterpret_cast<float*>(b + o_splitk), reinterpret_cast<uint8_t*>(b + o_kvt),
               reinterpret_cast<int8_t*>(b + o_gxq), reinterpret_cast<float*>(b + o_gsx), reinterpret_cast<int*>(b + o_gcorr),
               reinterpret_cast<const int*>(b + o_zs), reinterpret_cast<float*>(b + o_gmax)};
@@ -354,8 +346,8 @@ struct qwen_hip_model {
       }
       // one sequence: the attention leaves its split partials, merged by every block of the O projection
       if (!fuse_attn)
-        launch_attn_decode(w.qkv, (int)kQkvRows, kc, vc, ss, pos, B, max_keys, plan, w.part, w.pml, w.arrivals,
-                           nullptr, one ? nullptr : w.xq, w.sx, w.sums, stream);
+        launch_attn_decode(w.qkv, (int)kQkvRows, kc, vc, ss, pos, B, max_keys, plan, w.part, w.pml, nullptr,
+                           one ? nullptr : w.xq, w.sx, w.sums, stream);
       GemmArgs fn{};
       fn.fuse = kFuseNormQuant;
       fn.norm = kNormDecode;
@@ -672,7 +664,7 @@ int qwen_hip_model_decode_layers(qwen_hip_model* m, int mode, int first_layer, i
   mode &= ~(QWEN_FLAG_NO_BF16_ROUND | QWEN_FLAG_SEPARATE_REDUCE | QWEN_FLAG_SEPARATE_ATTN);
   if (batch <= 0 || max_keys <= 0 || max_keys > QWEN_MAX_SEQ || (mode != QWEN_MODE_ORDERED && mode != QWEN_MODE_FAST))
     return invalid("invalid decode shape or mode");
-  if (mode == QWEN_MODE_FAST && (size_t)batch > kMaxArrivals) return invalid("FAST decode batch above 4096 sequences");
+  if (mode == QWEN_MODE_FAST && (size_t)batch > kMaxDecodeBatch) return invalid("FAST decode batch above 65535 sequences");
   if (seq_stride < (uint64_t)max_keys * QWEN_KV_WIDTH || (batch > 1 && layer_stride < (uint64_t)batch * seq_stride) ||
       (layer_count > 1 && layer_stride == 0))
     return invalid("KV strides too small for max_keys / batch");
@@ -824,9 +816,9 @@ int qwen_hip_model_time_kernel(qwen_hip_model* m, int kernel, int layer, int rep
       const size_t la = (size_t)((layer - c.first + rep++) % c.count) * c.layer_stride;
       switch (kernel) {
         case QWEN_KERNEL_ATTN_DECODE:
+          // the partials launch alone (without xq no merge follows): the kernel the roofline covers
           launch_attn_decode(w.qkv, (int)kQkvRows, c.k_cache + la, c.v_cache + la, c.seq_stride, c.positions,
-                             c.batch, c.max_keys, plan, w.part, w.pml, w.arrivals, nullptr, w.xq, w.sx, w.sums,
-                             m->stream);
+                             c.batch, c.max_keys, plan, w.part, w.pml, nullptr, nullptr, w.sx, w.sums, m->stream);
           break;
         case QWEN_KERNEL_GEMM_GATE_UP:
           m->gemm(w, T, QWEN_HIDDEN, QWEN_INTERMEDIATE, f.gate, f.sw_gate, nullptr, w.tmp, QWEN_INTERMEDIATE,
