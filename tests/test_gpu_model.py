@@ -165,6 +165,32 @@ def test_model_decode(torch, layers2, model2, mode_name):
             assert rel_err(got[b], ref) <= FAST_TOL_ROUNDED, (b, rel_err(got[b], ref))
 
 
+def test_model_decode_fast_many_splits(torch, layers2):
+    """Two sequences with long histories (700 and 1100 keys): the decode attention plan gives them
+    18 key splits of 64, so the merge launch combines 11 and 18 splits in batches of 8 (two and three
+    batches).  One layer without rounding, within the per-layer tolerance of the oracle."""
+    from work_llm_accelerator_amd.model import FLAG_NO_BF16_ROUND, MODE_FAST, DeviceModel
+
+    pasts = [700, 1100]
+    print(f"model decode fast many splits pasts={pasts}", flush=True)
+    m1 = DeviceModel(1, layers2[0].weight_ddr, layers2[0].scale_ddr)
+    try:
+        cache1, hist1, x = decode_setup(torch, 1, pasts, 1120, seed=11)
+        h1 = torch.from_numpy(x).cuda()
+        pos = torch.tensor(pasts, dtype=torch.int32, device="cuda")
+        m1.decode(MODE_FAST | FLAG_NO_BF16_ROUND, h1, pos, max(pasts) + 1, cache1)
+        m1.synchronize()
+        got = h1.cpu().numpy()
+        for b, past in enumerate(pasts):
+            ref = oracle_decode(layers2[:1], x[b], past, [hist1[(0, b)][0].copy()], [hist1[(0, b)][1].copy()],
+                                rounding=False)
+            err = rel_err(got[b], ref)
+            print(f"  seq {b} past {past}: rel err {err:.2e}", flush=True)
+            assert err <= FAST_TOL, (b, err)
+    finally:
+        m1.close()
+
+
 @pytest.mark.parametrize("mode_name", ["ordered", "fast"])
 def test_model_prefill(torch, layers2, model2, mode_name):
     from work_llm_accelerator_amd.model import FLAG_NO_BF16_ROUND, MODE_FAST, MODE_ORDERED, DeviceModel, KvCache
