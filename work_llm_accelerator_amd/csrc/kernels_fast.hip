@@ -3818,7 +3818,12 @@ static bool launch_skinny(const GemmArgs& a, hipStream_t st) {
       return true;
     }
     if (!DUAL && a.fuse != kFuseNone && !a.part) return false;
-    launch_skinny_t<1, DUAL, EPI, 12, false>(a, row_tiles / 4, 1, st);
+    // the O shape over more than one token tile: two wave groups split K, as Q/K/V (64 x 4096 decode
+    // +0.25%, interleaved; the sums are exact int32, so the bits are the same)
+    if (!DUAL && a.tokens > 16 && a.out_dim == QWEN_HIDDEN)
+      launch_skinny_t<1, false, EPI, 12, false, 2>(a, row_tiles / 4, 1, st);
+    else
+      launch_skinny_t<1, DUAL, EPI, 12, false>(a, row_tiles / 4, 1, st);
     if (!DUAL && a.fuse != kFuseNone && !(a.defer_reduce && a.tokens == 1 && a.fuse == kFuseNormQuant))
       launch_reduce<EPI>(a, 1, st);
     return true;
